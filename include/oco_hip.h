@@ -1,0 +1,244 @@
+/*
+ * oco_hip.h -- C ABI of the MI355X (gfx950) quantized-weight matrix path.
+ *
+ * Drop-in for the Metal kernels and operator seams of xhjkl/oco:
+ *   - GGUF block dequantization fused into decode matvec (shaders/matrix),
+ *   - the top-k routed expert path (shaders/experts),
+ *   - prefill matmul on MFMA,
+ * behind plain-C entry points: pointers and sizes only, no C++ or torch types.
+ *
+ * Conventions (mirroring the reference's seam, src/gpu/dispatch.rs:211-285 and
+ * src/error.rs:9-27):
+ *   - every entry point returns an int status, OCO_OK (0) on success; the
+ *     message of the last failure on the calling thread is oco_last_error();
+ *   - no C++ exception crosses the ABI;
+ *   - device pointers are plain `void *` in device memory (oco_buffer_alloc or
+ *     any hipMalloc'd memory); weights are read-only and may sit at any byte
+ *     offset (GGUF guarantees only 1-byte alignment for MXFP4 blocks);
+ *   - calls are ordered on the given stream (NULL = the default stream) and
+ *     never synchronise the host except oco_stream_sync and the transfer
+ *     helpers marked "blocking";
+ *   - kernels never report data errors: NaN is the in-band failure signal
+ *     (E8M0 exponent 255, non-finite router inputs), as in the reference.
+ *
+ * Each declaration cites the reference interface it replaces (file:line,
+ * relative to the oco checkout).
+ */
+#ifndef OCO_HIP_H
+#define OCO_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status ------------------------------------------------------------ */
+enum {
+    OCO_OK = 0,
+    OCO_ERR_INVALID = 1,     /* bad argument or geometry (Error::Request)      */
+    OCO_ERR_UNSUPPORTED = 2, /* format/variant without a kernel               */
+    OCO_ERR_HIP = 3,         /* HIP runtime failure (Error::Gpu)              */
+    OCO_ERR_MEMORY = 4       /* allocation failure                            */
+};
+
+/* GGUF format codes: src/tensor.rs:9-20 (WeightFormat). */
+typedef enum oco_format {
+    OCO_F32 = 0,
+    OCO_F16 = 1,
+    OCO_Q4_0 = 2,
+    OCO_Q4_1 = 3,
+    OCO_Q8_0 = 8,
+    OCO_Q4_K = 12,
+    OCO_Q5_K = 13,
+    OCO_Q6_K = 14,
+    OCO_BF16 = 30,
+    OCO_MXFP4 = 39
+} oco_format;
+
+/* Activation / output element types.  The reference's kernels read bf16 and
+ * store bf16 unless `output_f32` is specialised (weights.metal:24-33). */
+typedef enum oco_dtype { OCO_DT_F32 = 0, OCO_DT_BF16 = 1, OCO_DT_F16 = 2 } oco_dtype;
+
+/* Kernel parameter block: shaders/matrix/weights.metal:87-89 and
+ * src/weights/compute/matrix.rs:10-20 (Matrix).
+ *   k, n       : input width, output rows (GGUF shape [k, n(, experts)])
+ *   m          : routes (vector rows); for oco_matmul the activation rows
+ *   route_major: routed input is indexed by route, not route/routes
+ *   routes     : routes per token (top-k)
+ *   experts    : experts in the bank; > 1 selects rows through ids[route]
+ *   has_bias   : 0 none, 1 add bf16(bias), 2 add bf16(bias + 1) (gpt-oss up)
+ * Routed rows: expert = experts > 1 ? ids[route] : 0, input =
+ * experts > 1 && !route_major ? route / routes : route, output at
+ * route * n + row, and f32 output whenever experts > 1 && !route_major
+ * (vector.metal:76-78, 142-146). */
+typedef struct oco_matrix {
+    uint32_t k, n, m, route_major, routes, experts, has_bias;
+} oco_matrix;
+
+typedef void *oco_stream; /* hipStream_t; NULL = default stream */
+typedef void *oco_event;  /* hipEvent_t */
+
+/* Thread-local message of the last failed call on this thread ("" if none). */
+const char *oco_last_error(void);
+
+/* (elements, bytes) per GGUF block: src/tensor.rs:24-38 (block_layout). */
+int oco_block_layout(uint32_t format, uint32_t *elements, uint32_t *bytes);
+
+/* Bytes of one row of `k` coefficients; 0 when k is not block aligned. */
+uint64_t oco_row_bytes(uint32_t format, uint32_t k);
+
+/* ---- device, memory, streams: src/gpu.rs:34-117, src/gpu/buffer.rs,
+ *      src/gpu/dispatch.rs, src/weights/compute/submission.rs ------------- */
+
+/* Select device `ordinal` for this thread and report its compute units.
+ * Replaces Gpu::new (src/gpu.rs:41-50). */
+int oco_device_open(int ordinal, int *compute_units);
+
+/* Device allocations (MappedRegions / Arena storage, src/gpu/buffer.rs:145-297,
+ * src/gpu/arena.rs:19-125). */
+int oco_buffer_alloc(size_t bytes, void **out);
+int oco_buffer_free(void *ptr);
+/* Blocking host<->device copies (the reference's BufferView reads/writes). */
+int oco_buffer_upload(void *dst, const void *src, size_t bytes);
+int oco_buffer_download(void *dst, const void *src, size_t bytes);
+/* Device-to-device copy on a stream. */
+int oco_buffer_copy(void *dst, const void *src, size_t bytes, oco_stream stream);
+/* Fill `words` 32-bit words with `pattern` by a kernel (guard sentinels,
+ * dispatch_tests.rs:12-13); safe inside captured graphs. */
+int oco_buffer_fill32(void *dst, uint32_t pattern, size_t words, oco_stream stream);
+
+/* One queue per session (src/weights/compute.rs:36-55). */
+int oco_stream_create(oco_stream *out);
+int oco_stream_sync(oco_stream stream);
+int oco_stream_destroy(oco_stream stream);
+
+/* Timestamps (OCO_PROFILE stamps, src/gpu/profile.rs:33-46). */
+int oco_event_create(oco_event *out);
+int oco_event_record(oco_event event, oco_stream stream);
+int oco_event_elapsed_ms(oco_event start, oco_event stop, float *ms);
+int oco_event_destroy(oco_event event);
+
+/* ---- dequantization ----------------------------------------------------- */
+
+/* Decode `count` coefficients (a multiple of the block's elements) of a GGUF
+ * tensor starting at `w` into f32: the `weight()` decoder of
+ * shaders/matrix/weights.metal:48-85 (mxfp4 at :40-46).  Bit-exact:
+ * Q8_0, Q6_K, Q4_0, MXFP4, F16, BF16 are exact; Q4_K/Q5_K/Q4_1 round once.
+ * MXFP4 exponent 255 decodes to NaN (projections.metal:19-23). */
+int oco_dequant(uint32_t format, const void *w, uint64_t count, float *out, oco_stream stream);
+
+/* ---- decode matvec ------------------------------------------------------ */
+
+/* y = W x (+ bias) for every route in p->m, fp32 accumulation.
+ * Replaces the vector kernels `matvec`, `matvec_q8_split`, `matvec_q6k`,
+ * `matvec_q5k`, `matvec_q4`, `matvec_split` (shaders/matrix/vector.metal:66,
+ * 155, 232, 292, 370; q8-dot.metal:39) as chosen by Builder::vector_kernel
+ * (src/weights/pipelines.rs:227-265) and dispatched by
+ * DenseMatrix::apply_row / Bindings::output (compute/matrix.rs:63, 519).
+ *   x: p->m (or tokens, for routed input) rows of p->k elements of x_dtype
+ *   y: p->m * p->n elements of y_dtype (forced f32 when routed non-route-major)
+ *   bias: f32 [experts * n] or NULL when has_bias == 0
+ *   ids: u32 [m] expert per route, or NULL when experts <= 1 */
+int oco_matvec(uint32_t format, const void *w, const void *x, oco_dtype x_dtype, void *y,
+               oco_dtype y_dtype, const float *bias, const uint32_t *ids, const oco_matrix *p,
+               oco_stream stream);
+
+/* ---- prefill matmul ----------------------------------------------------- */
+
+/* Y[m, n] = X[m, k] W^T (+ bias) on MFMA with fp32 accumulation.
+ * Replaces DenseMatrix::apply's tiled plans (compute/matrix.rs:130-379,
+ * `matmul`/`matmul_q4*`/`matmul_tensor_*`, batch.metal:24-79, tensor.metal:9-102).
+ * Operands: MXFP4 weights and bf16 activations enter bf16 MFMA exactly;
+ * other formats decode to f16 (the reference's half(w), tile.metal:16-80)
+ * with activations converted to f16.  X is bf16 or f16 row-major; Y f32 or
+ * bf16.  Uses no workspace. */
+int oco_matmul(uint32_t format, const void *w, const void *x, oco_dtype x_dtype, void *y,
+               oco_dtype y_dtype, const float *bias, const oco_matrix *p, oco_stream stream);
+
+/* ---- routing ------------------------------------------------------------ */
+
+/* Per token: top-k of `experts` logits (ties to the lowest index, non-finite
+ * ranks as -inf), chosen logits rounded to bf16, probabilities bf16 of the
+ * softmax over the chosen k; any non-finite input -> NaN probabilities.
+ * Replaces select_expert_values (shaders/experts/routing.metal:71-94),
+ * generalised to experts <= 256, k <= 8.  ids/probs: [tokens, k]. */
+int oco_route_select(const float *logits, uint32_t tokens, uint32_t experts, uint32_t k,
+                     uint32_t *ids, float *probs, oco_stream stream);
+
+/* Router logits = bf16(x) . bf16(W) + bf16(bias) over `experts` rows of f32
+ * weights [experts, hidden], then oco_route_select.  Replaces `router` and
+ * `router_logits` (routing.metal:96-146).  `logits` (may be NULL) receives
+ * [tokens, experts] f32. */
+int oco_router(const void *x, oco_dtype x_dtype, const float *w, const float *bias,
+               uint32_t tokens, uint32_t hidden, uint32_t experts, uint32_t k, float *logits,
+               uint32_t *ids, float *probs, oco_stream stream);
+
+/* Words of a route plan for `routes` routes over `experts` experts
+ * (src/weights/gpt_oss.rs:63-74). */
+uint64_t oco_route_plan_words(uint32_t routes, uint32_t experts);
+
+/* Per-expert route lists, (expert, first row) tiles of `tile_rows`, two
+ * dispatch grids at words 0-5, expert-sorted offsets and each route's sorted
+ * row: route_plan_64 (routing.metal:4-39) and route_plan_n
+ * (nemotron.metal:238-273).  ids: u32 [routes]. */
+int oco_route_plan(const uint32_t *ids, uint32_t routes, uint32_t experts, uint32_t tile_rows,
+                   uint32_t up_tiles, uint32_t down_tiles, uint32_t *plan, oco_stream stream);
+
+/* ---- routed experts ----------------------------------------------------- */
+
+/* Activation applied between the gate/up and down projections. */
+typedef enum oco_activation {
+    OCO_ACT_SWIGLU_CLIPPED = 0, /* gpt-oss: sigmoid(1.702 g') g' u', g' = min(g,7),
+                                   u' = clamp(u,-6,8) (projections.metal:4-13) */
+    OCO_ACT_SWIGLU = 1          /* silu(g) * u, the dense `gate` kernel
+                                   (elementwise.metal:70-88), in f32 */
+} oco_activation;
+
+/* One expert bank (src/weights/gpt_oss/load.rs:20-40, operands.rs ExpertWeight):
+ * gate/up [experts][ffn][hidden] and down [experts][hidden][ffn] GGUF rows,
+ * f32 biases [experts * rows] or NULL. */
+typedef struct oco_experts {
+    uint32_t format;        /* oco_format of gate/up/down */
+    uint32_t hidden, ffn;   /* model width, expert width */
+    uint32_t experts, k;    /* bank size, routes per token */
+    uint32_t activation;    /* oco_activation */
+    uint32_t up_bias_one;   /* 1: up bias carries +1 (has_bias == 2, gpt-oss) */
+    const void *gate, *up, *down;
+    const float *gate_bias, *up_bias, *down_bias;
+} oco_experts;
+
+/* Workspace bytes oco_experts_apply needs for `tokens` tokens. */
+uint64_t oco_experts_workspace(const oco_experts *w, uint32_t tokens);
+
+/* out[t] = bf16(out[t] + bf16(sum_r p[t,r] * down_{e_r}(act(gate_{e_r} x_t, up_{e_r} x_t)))).
+ * Replaces Bindings::experts (src/weights/compute/feed_forward.rs:107-275):
+ * router outputs (ids, probs [tokens, k]) are inputs here, as produced by
+ * oco_router/oco_route_select; each selected expert's weights are streamed
+ * once per call however many tokens chose it.  x: [tokens, hidden] of
+ * x_dtype; out: [tokens, hidden] bf16 residual (read and written);
+ * `routed` (may be NULL) receives the per-route f32 down outputs
+ * [tokens*k, hidden] before the combine.  workspace: oco_experts_workspace bytes. */
+int oco_experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype,
+                      const uint32_t *ids, const float *probs, uint32_t tokens, uint16_t *out,
+                      float *routed, void *workspace, uint64_t workspace_bytes, oco_stream stream);
+
+/* Single-token fused expansion: select the top-k experts from `logits`
+ * [experts], then gate and up projections of the selected experts with the
+ * activation applied; up_out/act_out [k, ffn] f32; ids/probs [k].
+ * Replaces expert_expand (projections.metal:78-137). */
+int oco_expert_expand(const oco_experts *w, const void *x, oco_dtype x_dtype,
+                      const float *logits, uint32_t *ids, float *probs, float *up_out,
+                      float *act_out, oco_stream stream);
+
+/* Weighted combine with residual: out = bf16(out + bf16(sum_r route_r p_r)).
+ * routes: [tokens*k, hidden] of routes_dtype (bf16 in the reference).
+ * Replaces moe_sum (routing.metal:157-168). */
+int oco_moe_sum(const void *routes, oco_dtype routes_dtype, const float *probs, uint16_t *out,
+                uint32_t hidden, uint32_t tokens, uint32_t k, oco_stream stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* OCO_HIP_H */

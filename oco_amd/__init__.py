@@ -1,0 +1,407 @@
+"""oco_amd: MI355X (gfx950) quantized-weight matrix path of oco.
+
+The product is the native library ``liboco_hip.so`` (HIP kernels behind the C
+ABI in ``include/oco_hip.h``).  This package loads it with ctypes and mirrors
+the reference's operator seam so callers and tests read like oco's own:
+
+- ``WeightFormat`` / ``block_layout``   -> src/tensor.rs:9-38
+- ``DeviceBuffer``                      -> src/gpu/buffer.rs (ReadOnly / BufferView)
+- ``DenseMatrix`` (apply_row / apply)   -> src/weights/operands.rs:4-9, compute/matrix.rs:63,130
+- ``Output``                            -> compute/matrix.rs:519-548 (f32 logits)
+- ``ExpertBank`` / ``Router``           -> operands.rs ExpertWeight/Router, feed_forward.rs:107
+
+There is no CPU fallback: every compute call goes through the HIP library,
+and loading fails loudly when the library is missing.
+"""
+from __future__ import annotations
+
+import ctypes
+import enum
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboco_hip.so")
+
+
+class WeightFormat(enum.IntEnum):
+    """GGUF format codes (src/tensor.rs:9-20)."""
+    F32 = 0
+    F16 = 1
+    Q4_0 = 2
+    Q4_1 = 3
+    Q8_0 = 8
+    Q4K = 12
+    Q5K = 13
+    Q6K = 14
+    Bf16 = 30
+    Mxfp4 = 39
+
+
+class DType(enum.IntEnum):
+    F32 = 0
+    BF16 = 1
+    F16 = 2
+
+
+class Activation(enum.IntEnum):
+    SWIGLU_CLIPPED = 0
+    SWIGLU = 1
+
+
+_BLOCKS = {0: (1, 4), 1: (1, 2), 30: (1, 2), 2: (32, 18), 3: (32, 20), 8: (32, 34),
+           12: (256, 144), 13: (256, 176), 14: (256, 210), 39: (32, 17)}
+
+
+def block_layout(fmt: int) -> tuple[int, int]:
+    """(elements, bytes) per block (src/tensor.rs:24-38)."""
+    return _BLOCKS[int(fmt)]
+
+
+def row_bytes(fmt: int, k: int) -> int:
+    e, b = block_layout(fmt)
+    if k % e:
+        raise ValueError(f"k={k} is not a multiple of the {WeightFormat(fmt).name} block ({e})")
+    return k // e * b
+
+
+class OcoError(RuntimeError):
+    """Raised for a non-zero status from the C ABI (src/error.rs:9-27)."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(f"[{code}] {message}")
+        self.code = code
+
+
+class Matrix(ctypes.Structure):
+    """oco_matrix / Matrix (weights.metal:87-89)."""
+    _fields_ = [(n, ctypes.c_uint32) for n in
+                ("k", "n", "m", "route_major", "routes", "experts", "has_bias")]
+
+
+def as_matrix(p) -> Matrix:
+    """Accept any object with the Matrix fields (e.g. a struct from another module)."""
+    if isinstance(p, Matrix):
+        return p
+    return Matrix(*[int(getattr(p, f)) for f, _ in Matrix._fields_])
+
+
+class ExpertsDesc(ctypes.Structure):
+    """oco_experts."""
+    _fields_ = [("format", ctypes.c_uint32), ("hidden", ctypes.c_uint32), ("ffn", ctypes.c_uint32),
+                ("experts", ctypes.c_uint32), ("k", ctypes.c_uint32),
+                ("activation", ctypes.c_uint32), ("up_bias_one", ctypes.c_uint32),
+                ("gate", ctypes.c_void_p), ("up", ctypes.c_void_p), ("down", ctypes.c_void_p),
+                ("gate_bias", ctypes.c_void_p), ("up_bias", ctypes.c_void_p),
+                ("down_bias", ctypes.c_void_p)]
+
+
+# Every symbol include/oco_hip.h declares, with its ctypes signature.
+_vp, _u32, _u64, _i32, _sz = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int, ctypes.c_size_t
+_MP = ctypes.POINTER(Matrix)
+_EP = ctypes.POINTER(ExpertsDesc)
+SIGNATURES = {
+    "oco_last_error": (ctypes.c_char_p, []),
+    "oco_block_layout": (_i32, [_u32, ctypes.POINTER(_u32), ctypes.POINTER(_u32)]),
+    "oco_row_bytes": (_u64, [_u32, _u32]),
+    "oco_device_open": (_i32, [_i32, ctypes.POINTER(_i32)]),
+    "oco_buffer_alloc": (_i32, [_sz, ctypes.POINTER(_vp)]),
+    "oco_buffer_free": (_i32, [_vp]),
+    "oco_buffer_upload": (_i32, [_vp, _vp, _sz]),
+    "oco_buffer_download": (_i32, [_vp, _vp, _sz]),
+    "oco_buffer_copy": (_i32, [_vp, _vp, _sz, _vp]),
+    "oco_buffer_fill32": (_i32, [_vp, _u32, _sz, _vp]),
+    "oco_stream_create": (_i32, [ctypes.POINTER(_vp)]),
+    "oco_stream_sync": (_i32, [_vp]),
+    "oco_stream_destroy": (_i32, [_vp]),
+    "oco_event_create": (_i32, [ctypes.POINTER(_vp)]),
+    "oco_event_record": (_i32, [_vp, _vp]),
+    "oco_event_elapsed_ms": (_i32, [_vp, _vp, ctypes.POINTER(ctypes.c_float)]),
+    "oco_event_destroy": (_i32, [_vp]),
+    "oco_dequant": (_i32, [_u32, _vp, _u64, _vp, _vp]),
+    "oco_matvec": (_i32, [_u32, _vp, _vp, _i32, _vp, _i32, _vp, _vp, _MP, _vp]),
+    "oco_matmul": (_i32, [_u32, _vp, _vp, _i32, _vp, _i32, _vp, _MP, _vp]),
+    "oco_route_select": (_i32, [_vp, _u32, _u32, _u32, _vp, _vp, _vp]),
+    "oco_router": (_i32, [_vp, _i32, _vp, _vp, _u32, _u32, _u32, _u32, _vp, _vp, _vp, _vp]),
+    "oco_route_plan_words": (_u64, [_u32, _u32]),
+    "oco_route_plan": (_i32, [_vp, _u32, _u32, _u32, _u32, _u32, _vp, _vp]),
+    "oco_experts_workspace": (_u64, [_EP, _u32]),
+    "oco_experts_apply": (_i32, [_EP, _vp, _i32, _vp, _vp, _u32, _vp, _vp, _vp, _u64, _vp]),
+    "oco_expert_expand": (_i32, [_EP, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "oco_moe_sum": (_i32, [_vp, _i32, _vp, _vp, _u32, _u32, _u32, _vp]),
+}
+
+_lib = None
+
+
+def load_library(path: str = LIB_PATH):
+    """Load liboco_hip.so and bind every declared symbol (fails loudly if absent)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise OSError(f"{path} is missing: run __graft_entry__.build() (hipcc for gfx950) first")
+    L = ctypes.CDLL(path)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(L, name, None)
+        if fn is None:  # tests/test_abi.py asserts every declared symbol is exported
+            continue
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+def _check(rc: int) -> None:
+    if rc != 0:
+        raise OcoError(rc, load_library().oco_last_error().decode())
+
+
+_device_open = False
+
+
+def open_device(ordinal: int = 0) -> int:
+    """Gpu::new (src/gpu.rs:41-50): select the device, return its CU count."""
+    global _device_open
+    cu = ctypes.c_int()
+    _check(load_library().oco_device_open(ordinal, ctypes.byref(cu)))
+    _device_open = True
+    return cu.value
+
+
+def _ensure_device():
+    if not _device_open:
+        open_device(0)
+
+
+class Stream:
+    """One HIP stream (the reference's per-session queue, compute.rs:36-55)."""
+
+    def __init__(self):
+        _ensure_device()
+        h = ctypes.c_void_p()
+        _check(load_library().oco_stream_create(ctypes.byref(h)))
+        self.handle = h
+
+    def sync(self):
+        _check(load_library().oco_stream_sync(self.handle))
+
+    def close(self):
+        if self.handle:
+            _check(load_library().oco_stream_destroy(self.handle))
+            self.handle = None
+
+
+class Event:
+    def __init__(self):
+        h = ctypes.c_void_p()
+        _check(load_library().oco_event_create(ctypes.byref(h)))
+        self.handle = h
+
+    def record(self, stream=None):
+        _check(load_library().oco_event_record(self.handle, _stream(stream)))
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = ctypes.c_float()
+        _check(load_library().oco_event_elapsed_ms(self.handle, end.handle, ctypes.byref(ms)))
+        return ms.value
+
+    def __del__(self):
+        try:
+            if self.handle and _lib is not None:
+                _lib.oco_event_destroy(self.handle)
+        except Exception:
+            pass
+
+
+def _stream(s):
+    if s is None:
+        return None
+    return s.handle if isinstance(s, Stream) else s
+
+
+class DeviceBuffer:
+    """Device allocation (src/gpu/buffer.rs BufferView / ReadOnly)."""
+
+    def __init__(self, nbytes: int):
+        _ensure_device()
+        p = ctypes.c_void_p()
+        _check(load_library().oco_buffer_alloc(max(int(nbytes), 1), ctypes.byref(p)))
+        self.ptr = p.value
+        self.nbytes = int(nbytes)
+
+    @classmethod
+    def from_array(cls, a: np.ndarray) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes)
+        b.upload(a)
+        return b
+
+    def upload(self, a: np.ndarray, offset: int = 0):
+        a = np.ascontiguousarray(a)
+        if offset + a.nbytes > self.nbytes:
+            raise ValueError("upload past the end of the buffer")
+        _check(load_library().oco_buffer_upload(self.ptr + offset, a.ctypes.data, a.nbytes))
+
+    def download(self, dtype, count=None, offset: int = 0) -> np.ndarray:
+        dtype = np.dtype(dtype)
+        if count is None:
+            count = (self.nbytes - offset) // dtype.itemsize
+        out = np.empty(count, dtype)
+        if offset + out.nbytes > self.nbytes:
+            raise ValueError("download past the end of the buffer")
+        _check(load_library().oco_buffer_download(out.ctypes.data, self.ptr + offset, out.nbytes))
+        return out
+
+    def fill32(self, pattern: int, stream=None):
+        _check(load_library().oco_buffer_fill32(self.ptr, pattern & 0xFFFFFFFF, self.nbytes // 4,
+                                                _stream(stream)))
+
+    def at(self, offset: int) -> int:
+        return self.ptr + offset
+
+    def free(self):
+        if self.ptr:
+            _check(load_library().oco_buffer_free(self.ptr))
+            self.ptr = 0
+
+    def __del__(self):
+        try:
+            if self.ptr and _lib is not None:
+                _lib.oco_buffer_free(self.ptr)
+        except Exception:
+            pass
+
+
+def _addr(b) -> int | None:
+    if b is None:
+        return None
+    if isinstance(b, DeviceBuffer):
+        return b.ptr
+    return int(b)
+
+
+def synchronize(stream=None):
+    if stream is None:
+        _check(load_library().oco_stream_sync(None))
+    else:
+        _check(load_library().oco_stream_sync(_stream(stream)))
+
+
+# ---- operations (thin wrappers over the C ABI) -------------------------------
+
+def dequant(fmt: int, w, count: int, out, stream=None):
+    _check(load_library().oco_dequant(int(fmt), _addr(w), count, _addr(out), _stream(stream)))
+
+
+def matvec(fmt: int, w, x, y, p: Matrix, x_dtype=DType.F32, y_dtype=DType.F32, bias=None,
+           ids=None, stream=None):
+    _check(load_library().oco_matvec(int(fmt), _addr(w), _addr(x), int(x_dtype), _addr(y),
+                                     int(y_dtype), _addr(bias), _addr(ids), ctypes.byref(as_matrix(p)),
+                                     _stream(stream)))
+
+
+def matmul(fmt: int, w, x, y, p: Matrix, x_dtype=DType.BF16, y_dtype=DType.F32, bias=None,
+           stream=None):
+    _check(load_library().oco_matmul(int(fmt), _addr(w), _addr(x), int(x_dtype), _addr(y),
+                                     int(y_dtype), _addr(bias), ctypes.byref(as_matrix(p)), _stream(stream)))
+
+
+def route_select(logits, tokens: int, experts: int, k: int, ids, probs, stream=None):
+    _check(load_library().oco_route_select(_addr(logits), tokens, experts, k, _addr(ids),
+                                           _addr(probs), _stream(stream)))
+
+
+def router(x, x_dtype, w, bias, tokens, hidden, experts, k, logits, ids, probs, stream=None):
+    _check(load_library().oco_router(_addr(x), int(x_dtype), _addr(w), _addr(bias), tokens, hidden,
+                                     experts, k, _addr(logits), _addr(ids), _addr(probs),
+                                     _stream(stream)))
+
+
+def route_plan_words(routes: int, experts: int) -> int:
+    return int(load_library().oco_route_plan_words(routes, experts))
+
+
+def route_plan(ids, routes, experts, tile_rows, up_tiles, down_tiles, plan, stream=None):
+    _check(load_library().oco_route_plan(_addr(ids), routes, experts, tile_rows, up_tiles,
+                                         down_tiles, _addr(plan), _stream(stream)))
+
+
+def moe_sum(routes, routes_dtype, probs, out, hidden, tokens, k, stream=None):
+    _check(load_library().oco_moe_sum(_addr(routes), int(routes_dtype), _addr(probs), _addr(out),
+                                      hidden, tokens, k, _stream(stream)))
+
+
+# ---- operator mirror -----------------------------------------------------------
+
+class DenseMatrix:
+    """A learned linear map with its GGUF storage (operands.rs:4-9).
+
+    ``input``/``output`` follow oco's [input, output] GGUF shape convention
+    (load.rs:175-186); ``values`` is the device buffer of GGUF rows.
+    """
+
+    def __init__(self, values: DeviceBuffer, fmt: int, input: int, output: int, offset: int = 0):
+        self.values, self.format, self.input, self.output = values, int(fmt), input, output
+        self.offset = offset
+        row_bytes(fmt, input)
+
+    def _w(self):
+        return self.values.ptr + self.offset
+
+    def apply_row(self, x, y, x_dtype=DType.F32, y_dtype=DType.F32, bias=None, rows: int = 1,
+                  stream=None):
+        """Decode path (compute/matrix.rs:63): y[r] = W x[r] for `rows` rows."""
+        p = Matrix(self.input, self.output, rows, 0, 1, 1, 1 if bias is not None else 0)
+        matvec(self.format, self._w(), x, y, p, x_dtype, y_dtype, bias, None, stream)
+
+    def apply(self, x, y, rows: int, x_dtype=DType.BF16, y_dtype=DType.F32, bias=None,
+              stream=None):
+        """Prefill path (compute/matrix.rs:130): Y = X W^T on MFMA."""
+        p = Matrix(self.input, self.output, rows, 0, 1, 1, 1 if bias is not None else 0)
+        matmul(self.format, self._w(), x, y, p, x_dtype, y_dtype, bias, stream)
+
+
+class Output(DenseMatrix):
+    """lm_head scoring in f32 (Bindings::output, compute/matrix.rs:519-548)."""
+
+    def apply_row(self, x, y, x_dtype=DType.F32, y_dtype=DType.F32, bias=None, rows: int = 1,
+                  stream=None):
+        super().apply_row(x, y, x_dtype, DType.F32, bias, rows, stream)
+
+
+class ExpertBank:
+    """Routed expert weights (gpt_oss/load.rs:20-40; Experts/ExpertPlan, feed_forward.rs:34-77)."""
+
+    def __init__(self, fmt: int, hidden: int, ffn: int, experts: int, k: int, gate, up, down,
+                 gate_bias=None, up_bias=None, down_bias=None,
+                 activation=Activation.SWIGLU_CLIPPED, up_bias_one: bool = True):
+        self.desc = ExpertsDesc(int(fmt), hidden, ffn, experts, k, int(activation),
+                                1 if up_bias_one else 0, _addr(gate), _addr(up), _addr(down),
+                                _addr(gate_bias), _addr(up_bias), _addr(down_bias))
+        self._keep = (gate, up, down, gate_bias, up_bias, down_bias)
+        self._workspace = None
+
+    def workspace_bytes(self, tokens: int) -> int:
+        return int(load_library().oco_experts_workspace(ctypes.byref(self.desc), tokens))
+
+    def apply(self, x, x_dtype, ids, probs, tokens: int, out, routed=None, workspace=None,
+              stream=None):
+        """Bindings::experts (feed_forward.rs:107-275) after the router."""
+        need = self.workspace_bytes(tokens)
+        if workspace is None:
+            if self._workspace is None or self._workspace.nbytes < need:
+                self._workspace = DeviceBuffer(max(need, 256))
+            workspace = self._workspace
+        ws_bytes = workspace.nbytes if isinstance(workspace, DeviceBuffer) else need
+        _check(load_library().oco_experts_apply(ctypes.byref(self.desc), _addr(x), int(x_dtype),
+                                                _addr(ids), _addr(probs), tokens, _addr(out),
+                                                _addr(routed), _addr(workspace), ws_bytes,
+                                                _stream(stream)))
+
+    def expand(self, x, x_dtype, logits, ids, probs, up_out, act_out, stream=None):
+        """expert_expand (projections.metal:78-137) for one token."""
+        _check(load_library().oco_expert_expand(ctypes.byref(self.desc), _addr(x), int(x_dtype),
+                                                _addr(logits), _addr(ids), _addr(probs),
+                                                _addr(up_out), _addr(act_out), _stream(stream)))

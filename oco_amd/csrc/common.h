@@ -1,0 +1,132 @@
+// Shared device and host helpers of the gfx950 matrix path.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string.h>
+
+#include "../../include/oco_hip.h"
+
+// ---- host-side status plumbing ---------------------------------------------
+namespace oco {
+int fail(int code, const char *fmt, ...);   // records the message, returns code
+int hip_check(hipError_t e, const char *what);
+int launch_check(const char *what);        // hipGetLastError after a launch
+}  // namespace oco
+
+#define OCO_TRY(expr)              \
+    do {                           \
+        int _rc = (expr);          \
+        if (_rc != OCO_OK) return _rc; \
+    } while (0)
+
+// ---- device helpers ----------------------------------------------------------
+namespace oco {
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float bits_f32(uint32_t u) { return __uint_as_float(u); }
+
+// IEEE half -> float (denormals kept: f16 denormals are enabled on gfx950).
+__device__ __forceinline__ float half_bits_to_f32(uint32_t h) {
+    _Float16 v;
+    uint16_t b = (uint16_t)h;
+    __builtin_memcpy(&v, &b, 2);
+    return (float)v;
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+// float -> bf16 bits, round to nearest even, NaN stays quiet.
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+__device__ __forceinline__ float round_bf16(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }
+
+// Unaligned little-endian loads from GGUF byte streams (gfx950 global
+// loads accept any byte alignment; the compiler emits single dword loads).
+__device__ __forceinline__ uint32_t ld_u8(const uint8_t *p) { return *p; }
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t *p) {
+    uint16_t v;
+    __builtin_memcpy(&v, p, 2);
+    return v;
+}
+__device__ __forceinline__ uint32_t ld_u32(const uint8_t *p) {
+    uint32_t v;
+    __builtin_memcpy(&v, p, 4);
+    return v;
+}
+__device__ __forceinline__ uint2 ld_u64(const uint8_t *p) {
+    uint2 v;
+    __builtin_memcpy(&v, p, 8);
+    return v;
+}
+__device__ __forceinline__ uint4 ld_u128(const uint8_t *p) {
+    uint4 v;
+    __builtin_memcpy(&v, p, 16);
+    return v;
+}
+
+// E8M0 shared exponent: finite powers exact, 0 -> 2^-127, 255 -> NaN
+// (projections.metal:19-23).
+__device__ __forceinline__ float e8m0_scale(uint32_t e) {
+    float s = e == 0 ? bits_f32(0x00400000u) : bits_f32(e << 23);
+    return e == 255 ? bits_f32(0x7fc00000u) : s;
+}
+
+__device__ __forceinline__ uint32_t byte_of(uint32_t w, int i) { return (w >> (8 * i)) & 0xffu; }
+
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// Activation element loads, f32 or bf16 (bits in uint16_t).
+struct bf16_t {
+    uint16_t bits;
+};
+
+template <typename XT>
+struct XLoad;
+template <>
+struct XLoad<float> {
+    // n contiguous values starting at p (n multiple of 4, p 16-byte aligned
+    // whenever k is a multiple of 4).
+    template <int N>
+    __device__ __forceinline__ static void run(const float *p, float *out) {
+#pragma unroll
+        for (int i = 0; i < N; i += 4) {
+            float4 v = *reinterpret_cast<const float4 *>(p + i);
+            out[i] = v.x;
+            out[i + 1] = v.y;
+            out[i + 2] = v.z;
+            out[i + 3] = v.w;
+        }
+    }
+    __device__ __forceinline__ static float one(const float *p, uint64_t i) { return p[i]; }
+};
+template <>
+struct XLoad<bf16_t> {
+    template <int N>
+    __device__ __forceinline__ static void run(const bf16_t *p, float *out) {
+#pragma unroll
+        for (int i = 0; i < N; i += 8) {
+            uint4 v = *reinterpret_cast<const uint4 *>(p + i);
+            uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                out[i + 2 * j] = __uint_as_float(w[j] << 16);
+                out[i + 2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+            }
+        }
+    }
+    __device__ __forceinline__ static float one(const bf16_t *p, uint64_t i) {
+        return bf16_bits_to_f32(p[i].bits);
+    }
+};
+
+}  // namespace oco

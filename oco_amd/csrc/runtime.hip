@@ -1,0 +1,151 @@
+// Runtime seam: status strings, device selection, device memory, streams and
+// events.  Replaces oco's Metal device/buffer/queue layer (src/gpu.rs,
+// src/gpu/buffer.rs, src/gpu/dispatch.rs, src/gpu/profile.rs) with HIP.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "common.h"
+
+namespace oco {
+
+static thread_local char g_error[512] = "";
+
+int fail(int code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_error, sizeof g_error, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int hip_check(hipError_t e, const char *what) {
+    if (e == hipSuccess) return OCO_OK;
+    return fail(e == hipErrorOutOfMemory ? OCO_ERR_MEMORY : OCO_ERR_HIP, "%s: %s", what,
+                hipGetErrorString(e));
+}
+
+int launch_check(const char *what) { return hip_check(hipGetLastError(), what); }
+
+__global__ void fill32_kernel(uint32_t *dst, uint32_t pattern, size_t words) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (; i < words; i += stride) dst[i] = pattern;
+}
+
+}  // namespace oco
+
+using namespace oco;
+
+extern "C" {
+
+const char *oco_last_error(void) { return g_error; }
+
+int oco_block_layout(uint32_t format, uint32_t *elements, uint32_t *bytes) {
+    uint32_t e, b;
+    switch (format) {
+    case OCO_F32: e = 1; b = 4; break;
+    case OCO_F16:
+    case OCO_BF16: e = 1; b = 2; break;
+    case OCO_Q4_0: e = 32; b = 18; break;
+    case OCO_Q4_1: e = 32; b = 20; break;
+    case OCO_Q8_0: e = 32; b = 34; break;
+    case OCO_Q4_K: e = 256; b = 144; break;
+    case OCO_Q5_K: e = 256; b = 176; break;
+    case OCO_Q6_K: e = 256; b = 210; break;
+    case OCO_MXFP4: e = 32; b = 17; break;
+    default: return fail(OCO_ERR_UNSUPPORTED, "unknown GGUF format %u", format);
+    }
+    if (elements) *elements = e;
+    if (bytes) *bytes = b;
+    return OCO_OK;
+}
+
+uint64_t oco_row_bytes(uint32_t format, uint32_t k) {
+    uint32_t e, b;
+    if (oco_block_layout(format, &e, &b) != OCO_OK || k % e) return 0;
+    return (uint64_t)(k / e) * b;
+}
+
+int oco_device_open(int ordinal, int *compute_units) {
+    int count = 0;
+    OCO_TRY(hip_check(hipGetDeviceCount(&count), "hipGetDeviceCount"));
+    if (ordinal < 0 || ordinal >= count)
+        return fail(OCO_ERR_INVALID, "device %d out of range (%d devices)", ordinal, count);
+    OCO_TRY(hip_check(hipSetDevice(ordinal), "hipSetDevice"));
+    if (compute_units) {
+        int cu = 0;
+        OCO_TRY(hip_check(hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, ordinal),
+                          "hipDeviceGetAttribute"));
+        *compute_units = cu;
+    }
+    return OCO_OK;
+}
+
+int oco_buffer_alloc(size_t bytes, void **out) {
+    if (!out) return fail(OCO_ERR_INVALID, "oco_buffer_alloc: null out");
+    *out = nullptr;
+    return hip_check(hipMalloc(out, bytes ? bytes : 1), "hipMalloc");
+}
+
+int oco_buffer_free(void *ptr) { return hip_check(hipFree(ptr), "hipFree"); }
+
+int oco_buffer_upload(void *dst, const void *src, size_t bytes) {
+    return hip_check(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice), "hipMemcpy H2D");
+}
+
+int oco_buffer_download(void *dst, const void *src, size_t bytes) {
+    return hip_check(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost), "hipMemcpy D2H");
+}
+
+int oco_buffer_copy(void *dst, const void *src, size_t bytes, oco_stream stream) {
+    return hip_check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, (hipStream_t)stream),
+                     "hipMemcpyAsync D2D");
+}
+
+int oco_buffer_fill32(void *dst, uint32_t pattern, size_t words, oco_stream stream) {
+    if (!words) return OCO_OK;
+    if (!dst) return fail(OCO_ERR_INVALID, "oco_buffer_fill32: null destination");
+    size_t blocks = (words + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(fill32_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+                       (uint32_t *)dst, pattern, words);
+    return launch_check("fill32");
+}
+
+int oco_stream_create(oco_stream *out) {
+    hipStream_t s;
+    OCO_TRY(hip_check(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreate"));
+    *out = (oco_stream)s;
+    return OCO_OK;
+}
+
+int oco_stream_sync(oco_stream stream) {
+    return hip_check(hipStreamSynchronize((hipStream_t)stream), "hipStreamSynchronize");
+}
+
+int oco_stream_destroy(oco_stream stream) {
+    return hip_check(hipStreamDestroy((hipStream_t)stream), "hipStreamDestroy");
+}
+
+int oco_event_create(oco_event *out) {
+    hipEvent_t e;
+    OCO_TRY(hip_check(hipEventCreate(&e), "hipEventCreate"));
+    *out = (oco_event)e;
+    return OCO_OK;
+}
+
+int oco_event_record(oco_event event, oco_stream stream) {
+    return hip_check(hipEventRecord((hipEvent_t)event, (hipStream_t)stream), "hipEventRecord");
+}
+
+int oco_event_elapsed_ms(oco_event start, oco_event stop, float *ms) {
+    OCO_TRY(hip_check(hipEventSynchronize((hipEvent_t)stop), "hipEventSynchronize"));
+    return hip_check(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop),
+                     "hipEventElapsedTime");
+}
+
+int oco_event_destroy(oco_event event) {
+    return hip_check(hipEventDestroy((hipEvent_t)event), "hipEventDestroy");
+}
+
+}  // extern "C"

@@ -1,0 +1,190 @@
+"""ctypes view of the C oracle (oracle/oco_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, by ``__graft_entry__.smoke()``
+as the checker, and by bench.py's ``cpu_baseline`` leg.  The product library
+(``oco_amd``) never imports this module.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboco_oracle.so")
+
+F32, F16, Q4_0, Q4_1, Q8_0, Q4_K, Q5_K, Q6_K, BF16, MXFP4 = 0, 1, 2, 3, 8, 12, 13, 14, 30, 39
+DT_F32, DT_BF16, DT_F16 = 0, 1, 2
+FORMATS = {"f32": F32, "f16": F16, "q4_0": Q4_0, "q4_1": Q4_1, "q8_0": Q8_0, "q4_k": Q4_K,
+           "q5_k": Q5_K, "q6_k": Q6_K, "bf16": BF16, "mxfp4": MXFP4}
+
+
+class Matrix(ctypes.Structure):
+    """shaders/matrix/weights.metal:87-89"""
+    _fields_ = [(name, ctypes.c_uint32) for name in
+                ("k", "n", "m", "route_major", "routes", "experts", "has_bias")]
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-B", "-C", HERE, "liboco_oracle.so"], check=True)
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        vp, u32, u64, i32 = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int
+        L.oo_block_layout.argtypes = [u32, ctypes.POINTER(u32), ctypes.POINTER(u32)]
+        L.oo_fp16.argtypes = [ctypes.c_uint16]
+        L.oo_fp16.restype = ctypes.c_float
+        L.oo_f32_to_bf16.argtypes = [ctypes.c_float]
+        L.oo_f32_to_bf16.restype = ctypes.c_uint16
+        L.oo_f32_to_f16.argtypes = [ctypes.c_float]
+        L.oo_f32_to_f16.restype = ctypes.c_uint16
+        L.oo_dequant.argtypes = [u32, vp, u64, vp]
+        L.oo_matvec_f64.argtypes = [u32, vp, vp, i32, vp, vp, ctypes.POINTER(Matrix), vp, vp]
+        L.oo_matvec_f32.argtypes = [u32, vp, vp, i32, vp, vp, ctypes.POINTER(Matrix), vp, i32, i32]
+        L.oo_select_experts.argtypes = [vp, u32, u32, vp, vp]
+        L.oo_swiglu_clipped.argtypes = [ctypes.c_float, ctypes.c_float]
+        L.oo_swiglu_clipped.restype = ctypes.c_float
+        L.oo_route_plan_words.argtypes = [u32, u32]
+        L.oo_route_plan_words.restype = u64
+        L.oo_route_plan.argtypes = [vp, u32, u32, u32, u32, u32, vp]
+        L.oo_route_plan.restype = u64
+        L.oo_moe_sum.argtypes = [vp, vp, vp, u32, u32, u32]
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray):
+    return a.ctypes.data_as(ctypes.c_void_p) if a is not None else None
+
+
+def block_layout(fmt: int) -> tuple[int, int]:
+    e, b = ctypes.c_uint32(), ctypes.c_uint32()
+    if lib().oo_block_layout(fmt, ctypes.byref(e), ctypes.byref(b)):
+        raise ValueError(f"unknown format {fmt}")
+    return e.value, b.value
+
+
+def dequant(fmt: int, w: np.ndarray, count: int) -> np.ndarray:
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    out = np.empty(count, np.float32)
+    rc = lib().oo_dequant(fmt, _p(w), count, _p(out))
+    if rc:
+        raise ValueError(f"oo_dequant failed: {rc}")
+    return out
+
+
+def _x_dtype(x: np.ndarray) -> int:
+    if x.dtype == np.float32:
+        return DT_F32
+    if x.dtype == np.uint16:  # bf16 bits
+        return DT_BF16
+    raise TypeError(x.dtype)
+
+
+def matvec_f64(fmt, w, x, p: Matrix, bias=None, ids=None, xdt=None):
+    """fp64 y (routes*n) and magnitude sum|w x| + |b| per output."""
+    w = np.ascontiguousarray(w, np.uint8)
+    x = np.ascontiguousarray(x)
+    y = np.empty(p.m * p.n, np.float64)
+    mag = np.empty(p.m * p.n, np.float64)
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    i = None if ids is None else np.ascontiguousarray(ids, np.uint32)
+    rc = lib().oo_matvec_f64(fmt, _p(w), _p(x), _x_dtype(x) if xdt is None else xdt, _p(b), _p(i),
+                             ctypes.byref(p), _p(y), _p(mag))
+    if rc:
+        raise ValueError(rc)
+    return y, mag
+
+
+def matvec_f32(fmt, w, x, p: Matrix, bias=None, ids=None, y_bf16=False, threads=1):
+    w = np.ascontiguousarray(w, np.uint8)
+    x = np.ascontiguousarray(x)
+    f32_out = (not y_bf16) or (p.experts > 1 and not p.route_major)
+    y = np.empty(p.m * p.n, np.float32 if f32_out else np.uint16)
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    i = None if ids is None else np.ascontiguousarray(ids, np.uint32)
+    rc = lib().oo_matvec_f32(fmt, _p(w), _p(x), _x_dtype(x), _p(b), _p(i), ctypes.byref(p), _p(y),
+                             DT_F32 if not y_bf16 else DT_BF16, threads)
+    if rc:
+        raise ValueError(rc)
+    return y
+
+
+def select_experts(logits: np.ndarray, k: int):
+    """Per-token top-k with softmax over the selected (routing.metal:71-94)."""
+    logits = np.ascontiguousarray(logits, np.float32)
+    tokens, experts = logits.shape
+    ids = np.empty((tokens, k), np.uint32)
+    probs = np.empty((tokens, k), np.float32)
+    for t in range(tokens):
+        row = np.ascontiguousarray(logits[t])
+        rc = lib().oo_select_experts(_p(row), experts, k, _p(ids[t]), _p(probs[t]))
+        if rc:
+            raise ValueError(rc)
+    return ids, probs
+
+
+def swiglu_clipped(g: float, u: float) -> float:
+    return lib().oo_swiglu_clipped(g, u)
+
+
+def route_plan(ids: np.ndarray, experts: int, tile_rows: int, up_tiles: int, down_tiles: int):
+    ids = np.ascontiguousarray(ids, np.uint32).ravel()
+    words = lib().oo_route_plan_words(ids.size, experts)
+    plan = np.zeros(words, np.uint32)
+    tiles = lib().oo_route_plan(_p(ids), ids.size, experts, tile_rows, up_tiles, down_tiles, _p(plan))
+    return plan, int(tiles)
+
+
+def route_plan_words(routes: int, experts: int) -> int:
+    return int(lib().oo_route_plan_words(routes, experts))
+
+
+def moe_sum(routes_bf16: np.ndarray, probs: np.ndarray, out_bf16: np.ndarray, k: int) -> np.ndarray:
+    out = np.array(out_bf16, np.uint16, copy=True)
+    batch, hidden = out.shape
+    r = np.ascontiguousarray(routes_bf16, np.uint16)
+    p = np.ascontiguousarray(probs, np.float32)
+    lib().oo_moe_sum(_p(r), _p(p), _p(out), hidden, batch, k)
+    return out
+
+
+# --- scalar conversions (vectorised in numpy, exactly as the C helpers) ------
+
+def bf16_to_f32(bits: np.ndarray) -> np.ndarray:
+    return (np.asarray(bits, np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16(x: np.ndarray) -> np.ndarray:
+    """Round to nearest even; NaN stays quiet NaN."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
+    return r
+
+
+def relative_l2(actual: np.ndarray, expected: np.ndarray) -> float:
+    a = np.asarray(actual, np.float64).ravel()
+    e = np.asarray(expected, np.float64).ravel()
+    den = np.linalg.norm(e)
+    return float(np.linalg.norm(a - e) / (den if den > 0 else 1.0))
+
+
+def roundoff_bound(expected, magnitude, k: int, stored_bf16: bool):
+    """gamma_{2k+8} * sum|w x| plus bf16 storage (matrix_precision.rs:136-142)."""
+    unit = 2.0 ** -24
+    ops = 2 * k + 8
+    gamma = ops * unit / (1 - ops * unit)
+    storage = 2.0 ** -8 if stored_bf16 else 0.0
+    return (1 + storage) * gamma * np.asarray(magnitude) + storage * np.abs(np.asarray(expected))

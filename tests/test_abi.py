@@ -1,0 +1,46 @@
+"""CPU checks of the C-ABI boundary: the library exists, loads, and exports
+every symbol include/oco_hip.h declares (no compute calls without a GPU)."""
+import ctypes
+import os
+import re
+
+import oco_amd
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    text = open(os.path.join(ROOT, "include", "oco_hip.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(oco_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_operator_surface():
+    syms = declared_symbols()
+    for need in ["oco_dequant", "oco_matvec", "oco_matmul", "oco_route_select", "oco_router",
+                 "oco_route_plan", "oco_experts_apply", "oco_expert_expand", "oco_moe_sum"]:
+        assert need in syms
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(oco_amd.LIB_PATH)
+    missing = [s for s in declared_symbols() if not hasattr(lib, s)]
+    assert not missing, missing
+
+
+def test_python_binding_covers_the_header():
+    assert set(declared_symbols()) == set(oco_amd.SIGNATURES)
+
+
+def test_host_helpers_without_gpu():
+    lib = oco_amd.load_library()
+    e, b = ctypes.c_uint32(), ctypes.c_uint32()
+    for fmt, layout in [(8, (32, 34)), (12, (256, 144)), (14, (256, 210)), (39, (32, 17)),
+                        (0, (1, 4)), (30, (1, 2)), (13, (256, 176)), (2, (32, 18)), (3, (32, 20))]:
+        assert lib.oco_block_layout(fmt, ctypes.byref(e), ctypes.byref(b)) == 0
+        assert (e.value, b.value) == layout == oco_amd.block_layout(fmt)
+    assert lib.oco_block_layout(77, ctypes.byref(e), ctypes.byref(b)) == 2
+    assert b"77" in lib.oco_last_error()
+    assert lib.oco_row_bytes(39, 2880) == 1530
+    assert lib.oco_row_bytes(12, 100) == 0
+    assert lib.oco_route_plan_words(68, 32) == 6 + 2 * (5 + 32) + 32 * 69 + 32 + 68

@@ -1,0 +1,195 @@
+"""GPU parity of dequantization and decode matvec against the C oracle.
+
+Bars (from the task's north star):
+- dequantized weights bit-exact with the oracle (NaN positions equal);
+- matvec outputs within relative L2 1e-5 of the fp64 oracle, and every
+  element within the reference's roundoff bound gamma_{2K+8} sum|w x| plus
+  bf16 storage rounding (matrix_precision.rs:136-142) where stored bf16.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+import packers as P
+from _util import Guarded, rel_l2, same_bits_nan_aware, say, upload_at_offset
+
+pytestmark = pytest.mark.gpu
+
+ALL_FORMATS = [P.F32, P.F16, P.BF16, P.Q4_0, P.Q4_1, P.Q8_0, P.Q4_K, P.Q5_K, P.Q6_K, O.MXFP4]
+
+
+def gpu_dequant(oco, fmt, data, count, offset=0):
+    buf, ptr = upload_at_offset(oco, data, offset)
+    out = Guarded(oco, count * 4)
+    oco.dequant(fmt, ptr, count, out.ptr)
+    oco.synchronize()
+    return out.read(np.float32)
+
+
+@pytest.mark.parametrize("fmt", ALL_FORMATS)
+def test_dequant_random_bytes_bit_exact(lib, fmt):
+    """Random bytes reach every code, subnormal/Inf/NaN scale and E8M0 0/255."""
+    say("dequant random bytes fmt", fmt)
+    e, b = O.block_layout(fmt)
+    nblocks = 4096 // max(e, 1) * 8 if e > 1 else 4096
+    data = np.random.default_rng(fmt).integers(0, 256, nblocks * b, dtype=np.uint8)
+    count = nblocks * e
+    for offset in (0, 7):
+        got = gpu_dequant(lib, fmt, data, count, offset)
+        same_bits_nan_aware(got, O.dequant(fmt, data, count))
+
+
+@pytest.mark.parametrize("fmt", [P.F32, P.F16, P.BF16, P.Q4_0, P.Q4_1, P.Q8_0, P.Q4_K, P.Q5_K, P.Q6_K])
+def test_dequant_reference_packer_golden(lib, fmt):
+    import os
+    say("dequant golden fmt", fmt)
+    f = np.load(os.path.join(os.path.dirname(__file__), "golden", f"dense_{fmt}.npz"))
+    got = gpu_dequant(lib, fmt, f["bytes"], f["coefficients"].size)
+    np.testing.assert_array_equal(got, f["coefficients"].astype(np.float32))
+
+
+def test_dequant_mxfp4_reference_packer(lib):
+    say("dequant mxfp4 packer")
+    k, n = 2880, 5
+    data, coeffs = P.mxfp4_decode_weights(k, n)
+    w = np.frombuffer(data, np.uint8)[P.WEIGHT_OFFSET:]
+    got = gpu_dequant(lib, O.MXFP4, w, coeffs.size, offset=P.WEIGHT_OFFSET)
+    np.testing.assert_array_equal(got.astype(np.float64), coeffs)
+
+
+def test_dequant_synthetic_baseline_tensors(lib):
+    from oco_amd import synth
+    for fmt, rows, k in [(8, 64, 4096), (39, 64, 2880), (12, 64, 4096), (14, 64, 12288)]:
+        say("dequant synth", fmt, rows, k)
+        data = synth.weights(fmt, rows, k, seed=11)
+        got = gpu_dequant(lib, fmt, data, rows * k)
+        same_bits_nan_aware(got, O.dequant(fmt, data, rows * k))
+
+
+def run_matvec(oco, fmt, data, x, p, x_bf16=False, y_bf16=False, bias=None, ids=None, offset=0):
+    wbuf, wptr = upload_at_offset(oco, data, offset)
+    xb = oco.DeviceBuffer.from_array(x)
+    routed_f32 = p.experts > 1 and not p.route_major
+    out_bf16 = y_bf16 and not routed_f32
+    y = Guarded(oco, p.m * p.n * (2 if out_bf16 else 4))
+    bb = oco.DeviceBuffer.from_array(np.asarray(bias, np.float32)) if bias is not None else None
+    ib = oco.DeviceBuffer.from_array(np.asarray(ids, np.uint32)) if ids is not None else None
+    oco.matvec(fmt, wptr, xb, y.ptr, p, oco.DType.BF16 if x_bf16 else oco.DType.F32,
+               oco.DType.BF16 if y_bf16 else oco.DType.F32, bb, ib)
+    oco.synchronize()
+    got = y.read(np.uint16 if out_bf16 else np.float32)
+    return O.bf16_to_f32(got) if out_bf16 else got, out_bf16
+
+
+def check_matvec(oco, fmt, data, x, p, **kw):
+    got, stored_bf16 = run_matvec(oco, fmt, data, x, p, **kw)
+    want, mag = O.matvec_f64(fmt, np.asarray(data, np.uint8), x, p, bias=kw.get("bias"),
+                             ids=kw.get("ids"))
+    assert np.all(np.isfinite(got))
+    err = rel_l2(got, want)
+    tol = 1e-5 if not stored_bf16 else 4e-3
+    assert err <= tol, f"relL2 {err:.3e} > {tol}"
+    bound = O.roundoff_bound(want, mag, p.k, stored_bf16)
+    bad = np.nonzero(np.abs(got - want) > bound)[0]
+    assert bad.size == 0, f"{bad.size} outputs beyond the roundoff bound, first {bad[:4]}"
+    return err
+
+
+SHAPES = {  # BASELINE shapes (lm_head is covered by its own row-slice test)
+    P.Q8_0: (4096, 4096), O.MXFP4: (5760, 2880), P.Q4_K: (12288, 4096), P.Q6_K: (4096, 12288),
+}
+
+
+@pytest.mark.parametrize("fmt", [P.Q8_0, O.MXFP4, P.Q4_K, P.Q6_K])
+def test_matvec_baseline_shapes_f32(lib, fmt):
+    from oco_amd import synth
+    n, k = SHAPES[fmt]
+    say("matvec baseline", fmt, n, k)
+    data = synth.weights(fmt, n, k, seed=1)
+    x = synth.activations(2, k)
+    err = check_matvec(lib, fmt, data, x, O.Matrix(k, n, 1, 0, 1, 1, 0))
+    say(f"  relL2 {err:.2e}")
+
+
+@pytest.mark.parametrize("fmt", ALL_FORMATS)
+@pytest.mark.parametrize("n", [1, 33, 257])
+def test_matvec_reference_packer_tails(lib, fmt, n):
+    """K=512 with SIMD-tail row counts (matrix_precision.rs:19-107), bf16 inputs."""
+    k = 512
+    say("matvec packer", fmt, n)
+    if fmt == O.MXFP4:
+        data, _ = P.mxfp4_expert_weights(k, n, 1, 1)
+        data = np.frombuffer(data, np.uint8)[P.WEIGHT_OFFSET:]
+    else:
+        data, _ = P.dense_weights(fmt, n, k)
+        data = np.frombuffer(data, np.uint8)
+    x = P.dense_input(2, k)
+    p = O.Matrix(k, n, 2, 0, 1, 1, 0)
+    check_matvec(lib, fmt, data, x, p, x_bf16=True)
+    check_matvec(lib, fmt, data, x, p, x_bf16=True, y_bf16=True)
+
+
+@pytest.mark.parametrize("fmt", [O.MXFP4, P.Q8_0, P.Q4_K, P.Q6_K])
+def test_matvec_routed_semantics(lib, fmt):
+    """experts > 1: rows through ids[route], input route/routes, f32 output,
+    has_bias 2 adds bf16(bias + 1) (vector.metal:76-78, 140-146)."""
+    from oco_amd import synth
+    E, n, k = 6, 45, 512
+    data = synth.weights(fmt, E * n, k, seed=3)
+    ids = np.array([3, 0, 5, 1, 1, 4, 2, 0], np.uint32)
+    rng = np.random.default_rng(5)
+    bias = rng.normal(size=E * n).astype(np.float32)
+    x = synth.activations(4, 2 * k).reshape(2, k)
+    for has_bias in (0, 1, 2):
+        say("matvec routed", fmt, has_bias)
+        p = O.Matrix(k, n, 8, 0, 4, E, has_bias)
+        check_matvec(lib, fmt, data, x, p, bias=bias if has_bias else None, ids=ids, y_bf16=True)
+    xr = synth.activations(6, 8 * k).reshape(8, k)
+    p = O.Matrix(k, n, 8, 1, 4, E, 1)
+    check_matvec(lib, fmt, data, xr, p, bias=bias, ids=ids)
+
+
+def test_matvec_mxfp4_unaligned_and_nan_header(lib):
+    """Weights at byte offset 7; E8M0 255 makes its row NaN (mxfp4.rs:205-233)."""
+    from oco_amd import synth
+    n, k = 33, 2880
+    data = synth.weights(O.MXFP4, n, k, seed=9).copy()
+    x = synth.activations(10, k)
+    p = O.Matrix(k, n, 1, 0, 1, 1, 0)
+    say("matvec mxfp4 offset 7")
+    check_matvec(lib, O.MXFP4, data, x, p, offset=7)
+    data[0] = 255
+    got, _ = run_matvec(lib, O.MXFP4, data, x, p, offset=7)
+    assert np.isnan(got[0]) and np.all(np.isfinite(got[1:]))
+
+
+def test_matvec_lm_head_row_slices(lib):
+    """lm_head [151936 x 4096] Q6_K with f32 output: the full matrix on the
+    GPU, checked against the oracle on its first and last 1024 rows."""
+    from oco_amd import synth
+    n, k = 151936, 4096
+    say("matvec lm_head")
+    data = synth.weights(P.Q6_K, n, k, seed=21)
+    x = synth.activations(22, k)
+    got, _ = run_matvec(lib, P.Q6_K, data, x, O.Matrix(k, n, 1, 0, 1, 1, 0))
+    rb = k // 256 * 210
+    for lo in (0, n - 1024):
+        sl = data[lo * rb:(lo + 1024) * rb]
+        want, mag = O.matvec_f64(P.Q6_K, sl, x, O.Matrix(k, 1024, 1, 0, 1, 1, 0))
+        assert rel_l2(got[lo:lo + 1024], want) <= 1e-5
+        assert np.all(np.abs(got[lo:lo + 1024] - want) <= O.roundoff_bound(want, mag, k, False))
+
+
+def test_matvec_exact_integer_answers(lib):
+    """All-ones weights, x = 1 and 2 -> K and 2K exactly (compute/tests.rs:40-80)."""
+    k, n = 4096, 100
+    for fmt, block in [(P.F32, None), (P.Q8_0, None)]:
+        if fmt == P.F32:
+            data = np.ones(n * k, np.float32).view(np.uint8)
+        else:
+            blk = np.frombuffer((0x3C00).to_bytes(2, "little") + bytes([1] * 32), np.uint8)
+            data = np.tile(blk, n * k // 32)
+        for xv in (1.0, 2.0):
+            say("matvec exact", fmt, xv)
+            got, _ = run_matvec(lib, fmt, data, np.full(k, xv, np.float32), O.Matrix(k, n, 1, 0, 1, 1, 0))
+            np.testing.assert_array_equal(got, np.full(n, k * xv, np.float32))
