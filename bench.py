@@ -1,0 +1,249 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X quantized-weight matrix path.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--no-extra] [--no-cpu]
+
+Prints ONE JSON line.  The headline (``value``) is the workload BASELINE's
+metric is quoted on at one GPU: the MXFP4 decode matvec at gpt-oss-20b's
+expert shape (weight [5760 x 2880], one f32 activation vector, fp32
+accumulation), in GB/s of streamed weight bytes.  A step is one launch of
+the fused dequantize+matvec over one weight copy; inputs are resident in HBM
+before timing starts.  The weight is replicated into enough distinct copies
+(> 512 MiB) that successive steps rotate through them, so the 256 MB
+Infinity Cache cannot serve repeats (the reference rotates weight copies for
+the same reason, dense_bench.rs:220-250).  The K timed steps are one
+captured HIP graph, replayed after W warmup steps, bracketed by device
+synchronisation; HIP events on the launch stream time the region.
+
+``extra`` carries the other BASELINE configs measured the same way.
+``cpu_baseline`` times the scalar C oracle (dequantize-then-fp32-dot, the
+"port" of the reference's semantics) on the host on the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, AMD published
+MALL_BYTES = 256 * 2 ** 20     # Infinity Cache
+ROTATE_BYTES = 512 * 2 ** 20   # distinct weight bytes a timed step sequence cycles through
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class Workload:
+    name = ""
+    unit = "GB/s"
+    bound = "hbm"
+
+    def setup(self, oco, stream):
+        raise NotImplementedError
+
+    def launch(self, i: int):
+        raise NotImplementedError
+
+    def work_per_step(self) -> float:  # algorithmic bytes (hbm) or flops (mfma)
+        raise NotImplementedError
+
+
+class Matvec(Workload):
+    """Fused dequantize + matvec over rotated weight copies."""
+
+    def __init__(self, name, fmt, n, k, seed=1, label=None):
+        self.name, self.fmt, self.n, self.k, self.seed = name, fmt, n, k, seed
+        self.label = label or name
+
+    def setup(self, oco, stream):
+        from oco_amd import synth
+        self.oco, self.stream = oco, stream
+        data = synth.weights(self.fmt, self.n, self.k, self.seed)
+        self.bytes = data.nbytes
+        self.copies = max(1, math.ceil(ROTATE_BYTES / self.bytes))
+        self.w = oco.DeviceBuffer(self.bytes * self.copies)
+        self.w.upload(data)
+        for c in range(1, self.copies):
+            oco.load_library().oco_buffer_copy(self.w.ptr + c * self.bytes, self.w.ptr, self.bytes,
+                                               stream.handle)
+        stream.sync()
+        self.x = oco.DeviceBuffer.from_array(synth.activations(self.seed + 1, self.k))
+        self.y = oco.DeviceBuffer(self.n * 4)
+        self.p = oco.Matrix(self.k, self.n, 1, 0, 1, 1, 0)
+
+    def launch(self, i):
+        self.oco.matvec(self.fmt, self.w.ptr + (i % self.copies) * self.bytes, self.x, self.y,
+                        self.p, stream=self.stream)
+
+    def work_per_step(self):
+        return float(self.bytes)
+
+
+class MatvecStack(Workload):
+    """Qwen3-8B-shaped decode stack: ffn_up/gate Q4_K, ffn_down Q6_K, lm_head Q6_K."""
+    name = "qwen3_8b_q4km_decode_stack"
+
+    def setup(self, oco, stream):
+        from oco_amd import synth
+        self.oco, self.stream = oco, stream
+        self.mats = []
+        for fmt, n, k, seed in [(12, 12288, 4096, 31), (12, 12288, 4096, 32), (14, 4096, 12288, 33),
+                                (14, 151936, 4096, 34)]:
+            data = synth.weights(fmt, n, k, seed)
+            self.mats.append((fmt, n, k, oco.DeviceBuffer.from_array(data), data.nbytes))
+        self.bytes = sum(m[4] for m in self.mats)
+        self.x = oco.DeviceBuffer.from_array(synth.activations(35, 12288))
+        self.h = oco.DeviceBuffer(151936 * 4)
+
+    def launch(self, i):
+        for fmt, n, k, w, nb in self.mats:
+            self.oco.matvec(fmt, w, self.x, self.h, self.oco.Matrix(k, n, 1, 0, 1, 1, 0),
+                            stream=self.stream)
+
+    def work_per_step(self):
+        return float(self.bytes)
+
+
+WORKLOADS = {
+    "mxfp4_decode_matvec_5760x2880": lambda: Matvec("mxfp4_decode_matvec_5760x2880", 39, 5760, 2880),
+    "q8_0_matvec_4096x4096": lambda: Matvec("q8_0_matvec_4096x4096", 8, 4096, 4096),
+    "q4_k_matvec_12288x4096": lambda: Matvec("q4_k_matvec_12288x4096", 12, 12288, 4096),
+    "q6_k_matvec_4096x12288": lambda: Matvec("q6_k_matvec_4096x12288", 14, 4096, 12288),
+    "q6_k_lm_head_151936x4096": lambda: Matvec("q6_k_lm_head_151936x4096", 14, 151936, 4096),
+    "qwen3_8b_q4km_decode_stack": MatvecStack,
+}
+HEADLINE = "mxfp4_decode_matvec_5760x2880"
+
+
+def time_workload(oco, wl: Workload, steps: int, warmup: int):
+    stream = oco.Stream()
+    wl.setup(oco, stream)
+    if warmup:
+        warm = oco.Graph(stream, lambda: [wl.launch(i) for i in range(warmup)])
+        warm.launch()
+    graph = oco.Graph(stream, lambda: [wl.launch(warmup + i) for i in range(steps)])
+    stream.sync()
+    oco.synchronize()
+    start, stop = oco.Event(), oco.Event()
+    start.record(stream)
+    graph.launch()
+    stop.record(stream)
+    ms = start.elapsed_ms(stop)
+    stream.sync()
+    oco.synchronize()
+    per_step_s = ms / 1e3 / steps
+    work = wl.work_per_step()
+    achieved = work / per_step_s / 1e9
+    return {"ms_per_step": ms / steps, "achieved": achieved, "work": work}
+
+
+def cpu_baseline(budget_s: float = 10.0):
+    """Scalar C oracle (dequantize-then-fp32-dot) on host cores, same workload."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    from oco_amd import synth
+    n, k = 5760, 2880
+    w = synth.weights(39, n, k, 1)
+    x = synth.activations(2, k)
+    threads = min(16, os.cpu_count() or 1)
+    p = O.Matrix(k, n, 1, 0, 1, 1, 0)
+    t0 = time.perf_counter()
+    O.matvec_f32(39, w, x, p, threads=threads)
+    first = time.perf_counter() - t0
+    reps = max(1, int(budget_s / max(first, 1e-6)))
+    best = first
+    end = time.perf_counter() + budget_s
+    done = 1
+    while done < reps and time.perf_counter() < end:
+        t0 = time.perf_counter()
+        O.matvec_f32(39, w, x, p, threads=threads)
+        best = min(best, time.perf_counter() - t0)
+        done += 1
+    return {"value": round(w.nbytes / best / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"full MXFP4 5760x2880 matvec (8,812,800 weight bytes), best of {done} runs "
+                      f"over ~{budget_s:.0f} s, OpenMP {threads} threads, C oracle -O3"}
+
+
+def load_traffic(name: str):
+    path = os.path.join(ROOT, "profiles", f"{name}_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("traffic_bytes")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--workload", default=HEADLINE, choices=sorted(WORKLOADS))
+    ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build runs its kernels on a single MI355X "
+              "(multi-GPU sharding is design-only); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import oco_amd as oco
+    cus = oco.open_device(0)
+    log(f"device 0: {cus} CUs")
+
+    wl = WORKLOADS[args.workload]()
+    log(f"timing {wl.name}: {args.steps} steps after {args.warmup} warmup")
+    r = time_workload(oco, wl, args.steps, args.warmup)
+    value = r["achieved"]
+    traffic = load_traffic(wl.name)
+    out = {
+        "metric": "weight GB/s (% of HBM peak) for decode matvec",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(r["ms_per_step"], 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded GGUF-layout weights, N(0,1) activations)",
+        "config": {"workload": wl.name, "format": "MXFP4", "n": 5760, "k": 2880, "batch": 1,
+                   "weight_bytes": int(r["work"]), "rotated_copies": getattr(wl, "copies", 1)},
+        "roofline": {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(value / HBM_PEAK_GBS, 4), "traffic": traffic},
+    }
+    if not args.no_extra:
+        extra = []
+        for name in ["q8_0_matvec_4096x4096", "q4_k_matvec_12288x4096", "q6_k_matvec_4096x12288",
+                     "q6_k_lm_head_151936x4096", "qwen3_8b_q4km_decode_stack"]:
+            if name == wl.name:
+                continue
+            w2 = WORKLOADS[name]()
+            steps = max(20, min(args.steps, 200))
+            log(f"timing {name}: {steps} steps")
+            r2 = time_workload(oco, w2, steps, min(args.warmup, 10))
+            extra.append({"workload": name, "value": round(r2["achieved"], 2), "unit": "GB/s",
+                          "ms_per_step": round(r2["ms_per_step"], 6),
+                          "frac": round(r2["achieved"] / HBM_PEAK_GBS, 4),
+                          "work_bytes": int(r2["work"])})
+            del w2
+        out["extra"] = extra
+    if not args.no_cpu:
+        log("cpu baseline (C oracle)")
+        out["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -120,6 +120,16 @@ int oco_event_record(oco_event event, oco_stream stream);
 int oco_event_elapsed_ms(oco_event start, oco_event stop, float *ms);
 int oco_event_destroy(oco_event event);
 
+/* Stream capture into a replayable HIP graph, for launch-bound sequences of
+ * short kernels (the reference encodes a whole token's dispatches into one
+ * command buffer, src/weights/compute/submission.rs:21-107).  Calls between
+ * begin and end are recorded, not run; the library records no memset nodes. */
+typedef void *oco_graph;
+int oco_graph_begin(oco_stream stream);
+int oco_graph_end(oco_stream stream, oco_graph *out);
+int oco_graph_launch(oco_graph graph, oco_stream stream);
+int oco_graph_destroy(oco_graph graph);
+
 /* ---- dequantization ----------------------------------------------------- */
 
 /* Decode `count` coefficients (a multiple of the block's elements) of a GGUF

@@ -119,6 +119,10 @@ SIGNATURES = {
     "oco_event_record": (_i32, [_vp, _vp]),
     "oco_event_elapsed_ms": (_i32, [_vp, _vp, ctypes.POINTER(ctypes.c_float)]),
     "oco_event_destroy": (_i32, [_vp]),
+    "oco_graph_begin": (_i32, [_vp]),
+    "oco_graph_end": (_i32, [_vp, ctypes.POINTER(_vp)]),
+    "oco_graph_launch": (_i32, [_vp, _vp]),
+    "oco_graph_destroy": (_i32, [_vp]),
     "oco_dequant": (_i32, [_u32, _vp, _u64, _vp, _vp]),
     "oco_matvec": (_i32, [_u32, _vp, _vp, _i32, _vp, _i32, _vp, _vp, _MP, _vp]),
     "oco_matmul": (_i32, [_u32, _vp, _vp, _i32, _vp, _i32, _vp, _MP, _vp]),
@@ -211,6 +215,31 @@ class Event:
         try:
             if self.handle and _lib is not None:
                 _lib.oco_event_destroy(self.handle)
+        except Exception:
+            pass
+
+
+class Graph:
+    """Captured launches replayed natively (stream capture into a HIP graph)."""
+
+    def __init__(self, stream: "Stream", record):
+        _check(load_library().oco_graph_begin(stream.handle))
+        try:
+            record()
+        finally:
+            h = ctypes.c_void_p()
+            rc = load_library().oco_graph_end(stream.handle, ctypes.byref(h))
+        _check(rc)
+        self.handle = h
+        self.stream = stream
+
+    def launch(self):
+        _check(load_library().oco_graph_launch(self.handle, self.stream.handle))
+
+    def __del__(self):
+        try:
+            if self.handle and _lib is not None:
+                _lib.oco_graph_destroy(self.handle)
         except Exception:
             pass
 

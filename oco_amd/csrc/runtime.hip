@@ -148,4 +148,29 @@ int oco_event_destroy(oco_event event) {
     return hip_check(hipEventDestroy((hipEvent_t)event), "hipEventDestroy");
 }
 
+int oco_graph_begin(oco_stream stream) {
+    if (!stream) return fail(OCO_ERR_INVALID, "oco_graph_begin: capture needs a created stream");
+    return hip_check(hipStreamBeginCapture((hipStream_t)stream, hipStreamCaptureModeThreadLocal),
+                     "hipStreamBeginCapture");
+}
+
+int oco_graph_end(oco_stream stream, oco_graph *out) {
+    hipGraph_t g;
+    OCO_TRY(hip_check(hipStreamEndCapture((hipStream_t)stream, &g), "hipStreamEndCapture"));
+    hipGraphExec_t exec;
+    int rc = hip_check(hipGraphInstantiate(&exec, g, nullptr, nullptr, 0), "hipGraphInstantiate");
+    hipGraphDestroy(g);
+    if (rc != OCO_OK) return rc;
+    *out = (oco_graph)exec;
+    return OCO_OK;
+}
+
+int oco_graph_launch(oco_graph graph, oco_stream stream) {
+    return hip_check(hipGraphLaunch((hipGraphExec_t)graph, (hipStream_t)stream), "hipGraphLaunch");
+}
+
+int oco_graph_destroy(oco_graph graph) {
+    return hip_check(hipGraphExecDestroy((hipGraphExec_t)graph), "hipGraphExecDestroy");
+}
+
 }  // extern "C"
