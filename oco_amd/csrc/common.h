@@ -69,6 +69,39 @@ __device__ __forceinline__ uint4 ld_u128(const uint8_t *p) {
     return v;
 }
 
+// Streamed weight bytes are read through a buffer resource: loads carry the
+// nontemporal hint (read once per call, so they should not displace the
+// activations from L2/MALL), accept any byte offset, and return zero past
+// `bytes` (so tail rows need no clamping).  Offsets are 32-bit: one
+// resource covers at most 4 GiB, so kernels build one per row group.
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+struct WSrc {
+    __amdgpu_buffer_rsrc_t r;
+    __device__ __forceinline__ WSrc(const uint8_t *base, uint64_t bytes) {
+        uint32_t n = bytes > 0xffffffffull ? 0xffffffffu : (uint32_t)bytes;
+        r = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(base), 0, n, 0x00020000);
+    }
+    static constexpr int NT = 2;  // cache policy: nontemporal
+    __device__ __forceinline__ uint32_t u8(uint32_t off) const {
+        return __builtin_amdgcn_raw_buffer_load_b8(r, off, 0, NT);
+    }
+    __device__ __forceinline__ uint32_t u16(uint32_t off) const {
+        return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, NT);
+    }
+    __device__ __forceinline__ uint32_t u32(uint32_t off) const {
+        return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, NT);
+    }
+    __device__ __forceinline__ uint2 u64(uint32_t off) const {
+        u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, NT);
+        return make_uint2(v.x, v.y);
+    }
+    __device__ __forceinline__ uint4 u128(uint32_t off) const {
+        u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, NT);
+        return make_uint4(v.x, v.y, v.z, v.w);
+    }
+};
+
 // E8M0 shared exponent: finite powers exact, 0 -> 2^-127, 255 -> NaN
 // (projections.metal:19-23).
 __device__ __forceinline__ float e8m0_scale(uint32_t e) {
@@ -78,11 +111,22 @@ __device__ __forceinline__ float e8m0_scale(uint32_t e) {
 
 __device__ __forceinline__ uint32_t byte_of(uint32_t w, int i) { return (w >> (8 * i)) & 0xffu; }
 
-template <typename T>
-__device__ __forceinline__ T wave_sum(T v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+// Full wave64 sum, result in every lane: DPP butterflies inside each
+// 16-lane row (quad_perm [1,0,3,2], [2,3,0,1], row_ror 4, row_ror 8), then
+// gfx950's permlane16/32 swaps across rows.  All VALU, no LDS round trips.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dpp_f32<0xB1>(v);
+    v += dpp_f32<0x4E>(v);
+    v += dpp_f32<0x124>(v);
+    v += dpp_f32<0x128>(v);
+    auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(s16[0]) + __uint_as_float(s16[1]);
+    auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(s32[0]) + __uint_as_float(s32[1]);
 }
 
 // Activation element loads, f32 or bf16 (bits in uint16_t).

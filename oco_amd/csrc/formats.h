@@ -96,9 +96,9 @@ struct Piece<OCO_Q8_0> {
         XLoad<XT>::template run<8>(xr + block * 32 + piece * 8, x.v);
         x.sum = ((x.v[0] + x.v[1]) + (x.v[2] + x.v[3])) + ((x.v[4] + x.v[5]) + (x.v[6] + x.v[7]));
     }
-    __device__ __forceinline__ static float dot(const uint8_t *b, int piece, const X &x) {
-        uint2 q = ld_u64(b + 2 + piece * 8);
-        float d = half_bits_to_f32(ld_u16(b));
+    __device__ __forceinline__ static float dot(const WSrc &w, uint32_t b, int piece, const X &x) {
+        uint2 q = w.u64(b + 2 + piece * 8);
+        float d = half_bits_to_f32(w.u16(b));
         // Signed codes as unsigned bytes q + 128: sum q x = sum (q+128) x - 128 sum x.
         uint32_t u0 = q.x ^ 0x80808080u, u1 = q.y ^ 0x80808080u;
         float s0 = 0.f, s1 = 0.f;
@@ -134,9 +134,9 @@ struct Piece<OCO_MXFP4> {
         s0 = fmaf(v.x, x.lo[base + I], s0);
         s1 = fmaf(v.y, x.hi[base + I], s1);
     }
-    __device__ __forceinline__ static float dot(const uint8_t *b, int piece, const X &x) {
-        uint32_t e = ld_u8(b);
-        uint2 q = ld_u64(b + 1 + piece * 8);
+    __device__ __forceinline__ static float dot(const WSrc &w, uint32_t b, int piece, const X &x) {
+        uint32_t e = w.u8(b);
+        uint2 q = w.u64(b + 1 + piece * 8);
         float s0 = 0.f, s1 = 0.f;
         pair<0>(q.x, x, 0, s0, s1);
         pair<1>(q.x, x, 0, s0, s1);
@@ -177,12 +177,12 @@ struct KQuant4 {
         x.sum_lo = a;
         x.sum_hi = c;
     }
-    __device__ __forceinline__ static float dot(const uint8_t *b, int piece, const X &x) {
+    __device__ __forceinline__ static float dot(const WSrc &w, uint32_t b, int piece, const X &x) {
         int g = piece >> 1, l0 = (piece & 1) * 16;
-        uint4 hdr = ld_u128(b);
-        uint4 qs = ld_u128(b + (FMT == OCO_Q4_K ? 16 : 48) + 16 * piece);
+        uint4 hdr = w.u128(b);
+        uint4 qs = w.u128(b + (FMT == OCO_Q4_K ? 16 : 48) + 16 * piece);
         uint4 qh;
-        if (FMT == OCO_Q5_K) qh = ld_u128(b + 16 + l0);
+        if (FMT == OCO_Q5_K) qh = w.u128(b + 16 + l0);
         // scales[12] = bytes 4..15 of the block = hdr.y, hdr.z, hdr.w.
         uint32_t s0 = 2 * g, s1 = 2 * g + 1;
         uint32_t sc0, mn0, sc1, mn1;
@@ -216,12 +216,12 @@ struct KQuant4 {
             }
         }
         float d = half_bits_to_f32(hdr.x & 0xffffu), dmin = half_bits_to_f32(hdr.x >> 16);
-        uint32_t w[4] = {qs.x, qs.y, qs.z, qs.w};
+        uint32_t c[4] = {qs.x, qs.y, qs.z, qs.w};
         float a0 = 0.f, a1 = 0.f;
         if (FMT == OCO_Q4_K) {
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                uint32_t lo = w[j] & 0x0f0f0f0fu, hi = (w[j] >> 4) & 0x0f0f0f0fu;
+                uint32_t lo = c[j] & 0x0f0f0f0fu, hi = (c[j] >> 4) & 0x0f0f0f0fu;
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     a0 = fmaf(ub(lo, i), x.lo[4 * j + i], a0);
@@ -232,8 +232,8 @@ struct KQuant4 {
             uint32_t h[4] = {qh.x, qh.y, qh.z, qh.w};
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                uint32_t lo = (w[j] & 0x0f0f0f0fu) | (((h[j] >> s0) & 0x01010101u) << 4);
-                uint32_t hi = ((w[j] >> 4) & 0x0f0f0f0fu) | (((h[j] >> s1) & 0x01010101u) << 4);
+                uint32_t lo = (c[j] & 0x0f0f0f0fu) | (((h[j] >> s0) & 0x01010101u) << 4);
+                uint32_t hi = ((c[j] >> 4) & 0x0f0f0f0fu) | (((h[j] >> s1) & 0x01010101u) << 4);
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     a0 = fmaf(ub(lo, i), x.lo[4 * j + i], a0);
@@ -270,13 +270,13 @@ struct Piece<OCO_Q6_K> {
                        ((x.v[q][4] + x.v[q][5]) + (x.v[q][6] + x.v[q][7]));
         }
     }
-    __device__ __forceinline__ static float dot(const uint8_t *b, int piece, const X &x) {
+    __device__ __forceinline__ static float dot(const WSrc &w, uint32_t b, int piece, const X &x) {
         int h = piece >> 2, l0 = (piece & 3) * 8;
-        uint2 ql0 = ld_u64(b + h * 64 + l0);       // quarters 0 (low) and 2 (high)
-        uint2 ql1 = ld_u64(b + h * 64 + 32 + l0);  // quarters 1 (low) and 3 (high)
-        uint2 qh = ld_u64(b + 128 + h * 32 + l0);
-        uint2 scw = ld_u64(b + 192 + h * 8 + (l0 >> 4));  // scales of quarters at bytes 0,2,4,6
-        float d = half_bits_to_f32(ld_u16(b + 208));
+        uint2 ql0 = w.u64(b + h * 64 + l0);       // quarters 0 (low) and 2 (high)
+        uint2 ql1 = w.u64(b + h * 64 + 32 + l0);  // quarters 1 (low) and 3 (high)
+        uint2 qh = w.u64(b + 128 + h * 32 + l0);
+        uint2 scw = w.u64(b + 192 + h * 8 + (l0 >> 4));  // scales of quarters at bytes 0,2,4,6
+        float d = half_bits_to_f32(w.u16(b + 208));
         float r = 0.f;
 #pragma unroll
         for (int q = 0; q < 4; q++) {
@@ -317,14 +317,14 @@ struct Q4Legacy {
         for (int i = 0; i < 8; i++) s += x.lo[i] + x.hi[i];
         x.sum = s;
     }
-    __device__ __forceinline__ static float dot(const uint8_t *b, int piece, const X &x) {
-        uint2 q = ld_u64(b + CODES + piece * 8);
-        float d = half_bits_to_f32(ld_u16(b));
-        uint32_t w[2] = {q.x, q.y};
+    __device__ __forceinline__ static float dot(const WSrc &w, uint32_t b, int piece, const X &x) {
+        uint2 q = w.u64(b + CODES + piece * 8);
+        float d = half_bits_to_f32(w.u16(b));
+        uint32_t c[2] = {q.x, q.y};
         float a = 0.f;
 #pragma unroll
         for (int j = 0; j < 2; j++) {
-            uint32_t lo = w[j] & 0x0f0f0f0fu, hi = (w[j] >> 4) & 0x0f0f0f0fu;
+            uint32_t lo = c[j] & 0x0f0f0f0fu, hi = (c[j] >> 4) & 0x0f0f0f0fu;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 a = fmaf(ub(lo, i), x.lo[4 * j + i], a);
@@ -332,7 +332,7 @@ struct Q4Legacy {
             }
         }
         if (FMT == OCO_Q4_0) return d * fmaf(-8.f, x.sum, a);
-        return fmaf(d, a, half_bits_to_f32(ld_u16(b + 2)) * x.sum);
+        return fmaf(d, a, half_bits_to_f32(w.u16(b + 2)) * x.sum);
     }
 };
 template <>
@@ -352,18 +352,18 @@ struct Plain {
     __device__ __forceinline__ static void load_x(const XT *xr, uint32_t block, int, X &x) {
         XLoad<XT>::template run<E>(xr + block * E, x.v);
     }
-    __device__ __forceinline__ static float dot(const uint8_t *b, int, const X &x) {
-        uint4 q = ld_u128(b);
-        uint32_t w[4] = {q.x, q.y, q.z, q.w};
+    __device__ __forceinline__ static float dot(const WSrc &w, uint32_t b, int, const X &x) {
+        uint4 q = w.u128(b);
+        uint32_t c[4] = {q.x, q.y, q.z, q.w};
         float a = 0.f;
         if (FMT == OCO_F32) {
 #pragma unroll
-            for (int i = 0; i < 4; i++) a = fmaf(__uint_as_float(w[i]), x.v[i], a);
+            for (int i = 0; i < 4; i++) a = fmaf(__uint_as_float(c[i]), x.v[i], a);
         } else {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                float lo = FMT == OCO_F16 ? half_bits_to_f32(w[i] & 0xffffu) : __uint_as_float(w[i] << 16);
-                float hi = FMT == OCO_F16 ? half_bits_to_f32(w[i] >> 16) : __uint_as_float(w[i] & 0xffff0000u);
+                float lo = FMT == OCO_F16 ? half_bits_to_f32(c[i] & 0xffffu) : __uint_as_float(c[i] << 16);
+                float hi = FMT == OCO_F16 ? half_bits_to_f32(c[i] >> 16) : __uint_as_float(c[i] & 0xffff0000u);
                 a = fmaf(lo, x.v[2 * i], a);
                 a = fmaf(hi, x.v[2 * i + 1], a);
             }

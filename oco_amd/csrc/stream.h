@@ -1,0 +1,283 @@
+// Tile decoders for the streaming matvec: GGUF blocks decoded from an LDS
+// copy of the weight rows, against activations staged in LDS.
+//
+// Every format here splits a row into 32-coefficient pieces (a piece is one
+// lane's unit of work: a whole Q8_0/MXFP4 block, or one eighth of a Q4_K /
+// Q6_K super-block).  Activations are staged once per workgroup in
+// piece-major order: run t (4 floats) of piece p lives at float4 index
+// t * PT + p, PT = pieces per row, so the 32 lanes of a half-wavefront, which
+// hold consecutive pieces, read consecutive 16-byte words (no bank
+// conflicts), and the two halves, which hold different rows of the same
+// pieces, read identical words (broadcast).  Per-piece activation sums the
+// affine terms need are staged beside them.
+#pragma once
+#include "formats.h"
+
+namespace oco {
+
+// N bytes (N a multiple of 4) from an LDS address of any alignment.  gfx950
+// serves a ds_read that is not naturally aligned about ten times slower than
+// an aligned one, so this reads the covering dwords aligned (the compiler
+// pairs them into ds_read2_b32) and realigns them with v_alignbyte_b32.
+template <int N>
+__device__ __forceinline__ void lds_bytes(const uint8_t *p, uint32_t *out) {
+    const uint32_t a = (uint32_t)(uintptr_t)p & 3u;
+    const uint32_t *d = reinterpret_cast<const uint32_t *>(p - a);
+    uint32_t w[N / 4 + 1];
+#pragma unroll
+    for (int i = 0; i <= N / 4; i++) w[i] = d[i];
+#pragma unroll
+    for (int i = 0; i < N / 4; i++) out[i] = __builtin_amdgcn_alignbyte(w[i + 1], w[i], a);
+}
+__device__ __forceinline__ uint4 lds_u128(const uint8_t *p) {
+    uint32_t o[4];
+    lds_bytes<16>(p, o);
+    return make_uint4(o[0], o[1], o[2], o[3]);
+}
+__device__ __forceinline__ uint2 lds_u64(const uint8_t *p) {
+    uint32_t o[2];
+    lds_bytes<8>(p, o);
+    return make_uint2(o[0], o[1]);
+}
+__device__ __forceinline__ uint32_t lds_u16(const uint8_t *p) {
+    uint32_t o[1];
+    lds_bytes<4>(p, o);
+    return o[0] & 0xffffu;
+}
+
+template <int FMT>
+struct Tile;
+
+// MXFP4: piece = block {e, 16 code bytes}; code byte i holds columns i (low
+// nibble) and 16 + i (high nibble) of the block.  gfx950's
+// v_cvt_scalef32_pk_f32_fp4 decodes two E2M1 codes per instruction.
+template <>
+struct Tile<OCO_MXFP4> {
+    static constexpr int BLOCK = 32, BYTES = 17, P = 1, NSUM = 0;
+    struct Raw {
+        uint4 q;
+        uint32_t e;
+    };
+    __device__ __forceinline__ static void map(uint32_t f, uint32_t &p, uint32_t &t) {
+        p = f >> 3;
+        t = f & 7;
+    }
+    __device__ __forceinline__ static void sums(const float *, float *) {}
+    __device__ __forceinline__ static Raw load(const uint8_t *blk, int) {
+        Raw r;
+        r.e = blk[0];
+        r.q = lds_u128(blk + 1);
+        return r;
+    }
+    template <int I>
+    __device__ __forceinline__ static void pair(uint32_t w, const float *x, int j, float &s0, float &s1) {
+        f32x2 v = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, I);
+        s0 = fmaf(v.x, x[4 * j + I], s0);
+        s1 = fmaf(v.y, x[16 + 4 * j + I], s1);
+    }
+    __device__ __forceinline__ static float dot(const Raw &r, const float *x, const float *) {
+        float s0 = 0.f, s1 = 0.f;
+        const uint32_t w[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            pair<0>(w[j], x, j, s0, s1);
+            pair<1>(w[j], x, j, s0, s1);
+            pair<2>(w[j], x, j, s0, s1);
+            pair<3>(w[j], x, j, s0, s1);
+        }
+        return (s0 + s1) * e8m0_scale(r.e);
+    }
+};
+
+// Q8_0: piece = block {f16 d, int8 q[32]}.  Codes enter as unsigned bytes
+// q + 128 (exact), corrected by 128 * sum(x).
+template <>
+struct Tile<OCO_Q8_0> {
+    static constexpr int BLOCK = 32, BYTES = 34, P = 1, NSUM = 1;
+    struct Raw {
+        uint4 a, b;
+        uint32_t d;
+    };
+    __device__ __forceinline__ static void map(uint32_t f, uint32_t &p, uint32_t &t) {
+        p = f >> 3;
+        t = f & 7;
+    }
+    __device__ __forceinline__ static void sums(const float *x, float *s) {
+        float a = 0.f;
+#pragma unroll
+        for (int i = 0; i < 32; i++) a += x[i];
+        s[0] = a;
+    }
+    __device__ __forceinline__ static Raw load(const uint8_t *blk, int) {
+        Raw r;
+        r.d = lds_u16(blk);
+        uint32_t o[8];
+        lds_bytes<32>(blk + 2, o);
+        r.a = make_uint4(o[0], o[1], o[2], o[3]);
+        r.b = make_uint4(o[4], o[5], o[6], o[7]);
+        return r;
+    }
+    __device__ __forceinline__ static float dot(const Raw &r, const float *x, const float *s) {
+        const uint32_t w[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
+        float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; j += 2) {
+            uint32_t u0 = w[j] ^ 0x80808080u, u1 = w[j + 1] ^ 0x80808080u;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                a0 = fmaf(ub(u0, i), x[4 * j + i], a0);
+                a1 = fmaf(ub(u1, i), x[4 * j + 4 + i], a1);
+            }
+        }
+        return half_bits_to_f32(r.d) * fmaf(-128.f, s[0], a0 + a1);
+    }
+};
+
+// Q4_K: piece c of a super-block = qs bytes 16c..16c+15; low nibbles are
+// columns 64g + 16(c&1) + i of sub-block 2g, high nibbles columns
+// 64g + 32 + 16(c&1) + i of sub-block 2g+1 (g = c/2).  The 16-byte header
+// (d, dmin, 6-bit scales/mins) is read by all eight lanes of the block.
+template <>
+struct Tile<OCO_Q4_K> {
+    static constexpr int BLOCK = 256, BYTES = 144, P = 8, NSUM = 2;
+    struct Raw {
+        uint4 hdr, qs;
+    };
+    __device__ __forceinline__ static void map(uint32_t f, uint32_t &p, uint32_t &t) {
+        uint32_t b = f >> 6, rem = f & 63, g = rem >> 4, w = rem & 15;
+        uint32_t odd = (w & 7) >> 2;
+        p = b * 8 + 2 * g + odd;
+        t = (w >> 3) * 4 + (w & 3);
+    }
+    __device__ __forceinline__ static void sums(const float *x, float *s) {
+        float a = 0.f, b = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            a += x[i];
+            b += x[16 + i];
+        }
+        s[0] = a;
+        s[1] = b;
+    }
+    __device__ __forceinline__ static Raw load(const uint8_t *blk, int c) {
+        Raw r;
+        r.hdr = lds_u128(blk);
+        r.qs = lds_u128(blk + 16 + 16 * c);
+        return r;
+    }
+    __device__ __forceinline__ static float dot(const Raw &r, const float *x, const float *s, int c) {
+        const uint32_t g = (uint32_t)c >> 1;
+        uint32_t sb[12];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            sb[i] = byte_of(r.hdr.y, i);
+            sb[4 + i] = byte_of(r.hdr.z, i);
+            sb[8 + i] = byte_of(r.hdr.w, i);
+        }
+        // (scale, min) of sub-blocks 2g and 2g+1 (weights.metal:70-71).
+        uint32_t sc0, mn0, sc1, mn1;
+        if (g < 2) {
+            sc0 = sb[2 * g] & 63u;
+            mn0 = sb[2 * g + 4] & 63u;
+            sc1 = sb[2 * g + 1] & 63u;
+            mn1 = sb[2 * g + 5] & 63u;
+        } else {
+            uint32_t s0 = 2 * g, s1 = s0 + 1;
+            sc0 = (sb[s0 + 4] & 15u) | ((sb[s0 - 4] >> 6) << 4);
+            mn0 = (sb[s0 + 4] >> 4) | ((sb[s0] >> 6) << 4);
+            sc1 = (sb[s1 + 4] & 15u) | ((sb[s1 - 4] >> 6) << 4);
+            mn1 = (sb[s1 + 4] >> 4) | ((sb[s1] >> 6) << 4);
+        }
+        const uint32_t w[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
+        float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            uint32_t lo = w[j] & 0x0f0f0f0fu, hi = (w[j] >> 4) & 0x0f0f0f0fu;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                a0 = fmaf(ub(lo, i), x[4 * j + i], a0);
+                a1 = fmaf(ub(hi, i), x[16 + 4 * j + i], a1);
+            }
+        }
+        float d = half_bits_to_f32(r.hdr.x & 0xffffu), dmin = half_bits_to_f32(r.hdr.x >> 16);
+        float v = fmaf(d * (float)sc0, a0, -(dmin * (float)mn0) * s[0]);
+        return fmaf(d * (float)sc1, a1, fmaf(-(dmin * (float)mn1), s[1], v));
+    }
+};
+
+// Q6_K: piece c covers half h = c/4 and columns l0 = 8(c&3) .. l0+7 of each
+// 32-column quarter q (coefficient 128h + 32q + l).
+template <>
+struct Tile<OCO_Q6_K> {
+    static constexpr int BLOCK = 256, BYTES = 210, P = 8, NSUM = 4;
+    struct Raw {
+        uint2 ql0, ql1, qh, sc;
+        uint32_t d;
+    };
+    __device__ __forceinline__ static void map(uint32_t f, uint32_t &p, uint32_t &t) {
+        uint32_t b = f >> 6, rem = f & 63, h = rem >> 5, r2 = rem & 31, q = r2 >> 3, w = r2 & 7;
+        p = b * 8 + 4 * h + (w >> 1);
+        t = 2 * q + (w & 1);
+    }
+    __device__ __forceinline__ static void sums(const float *x, float *s) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            float a = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; i++) a += x[8 * q + i];
+            s[q] = a;
+        }
+    }
+    __device__ __forceinline__ static Raw load(const uint8_t *blk, int c) {
+        const int h = c >> 2, l0 = (c & 3) * 8;
+        Raw r;
+        r.ql0 = lds_u64(blk + h * 64 + l0);
+        r.ql1 = lds_u64(blk + h * 64 + 32 + l0);
+        r.qh = lds_u64(blk + 128 + h * 32 + l0);
+        r.sc = lds_u64(blk + 192 + h * 8 + (l0 >> 4));
+        r.d = lds_u16(blk + 208);
+        return r;
+    }
+    __device__ __forceinline__ static float dot(const Raw &r, const float *x, const float *s, int) {
+        float acc = 0.f;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const uint2 src = (q & 1) ? r.ql1 : r.ql0;
+            const int shift = (q >> 1) * 4;
+            float a = 0.f;
+#pragma unroll
+            for (int half = 0; half < 2; half++) {
+                uint32_t lw = half ? src.y : src.x, hw = half ? r.qh.y : r.qh.x;
+                uint32_t code = ((lw >> shift) & 0x0f0f0f0fu) | (((hw >> (2 * q)) & 0x03030303u) << 4);
+#pragma unroll
+                for (int i = 0; i < 4; i++) a = fmaf(ub(code, i), x[8 * q + 4 * half + i], a);
+            }
+            uint32_t sw = q < 2 ? r.sc.x : r.sc.y;
+            float sc = (float)(int8_t)((sw >> (16 * (q & 1))) & 0xffu);
+            acc = fmaf(sc, fmaf(-32.f, s[q], a), acc);
+        }
+        return half_bits_to_f32(r.d) * acc;
+    }
+};
+
+// Uniform call shape for formats whose dot ignores the piece index.
+template <int FMT>
+__device__ __forceinline__ float tile_dot(const typename Tile<FMT>::Raw &r, const float *x,
+                                          const float *s, int c) {
+    if constexpr (FMT == OCO_Q4_K || FMT == OCO_Q6_K)
+        return Tile<FMT>::dot(r, x, s, c);
+    else
+        return Tile<FMT>::dot(r, x, s);
+}
+
+// Sum over each 32-lane half of the wavefront (both halves independently).
+__device__ __forceinline__ float half_sum(float v) {
+    v += dpp_f32<0xB1>(v);
+    v += dpp_f32<0x4E>(v);
+    v += dpp_f32<0x124>(v);
+    v += dpp_f32<0x128>(v);
+    auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(s16[0]) + __uint_as_float(s16[1]);
+}
+
+}  // namespace oco
