@@ -192,7 +192,10 @@ uint64_t oco_route_plan_words(uint32_t routes, uint32_t experts);
 /* Per-expert route lists, (expert, first row) tiles of `tile_rows`, two
  * dispatch grids at words 0-5, expert-sorted offsets and each route's sorted
  * row: route_plan_64 (routing.metal:4-39) and route_plan_n
- * (nemotron.metal:238-273).  ids: u32 [routes]. */
+ * (nemotron.metal:238-273).  ids: u32 [routes].  The tile area holds
+ * ceil(routes/16) + experts tiles, so tile_rows must be >= 16.  Words not
+ * listed above (unused tile slots, list entries past each count) are left
+ * untouched, as in the reference. */
 int oco_route_plan(const uint32_t *ids, uint32_t routes, uint32_t experts, uint32_t tile_rows,
                    uint32_t up_tiles, uint32_t down_tiles, uint32_t *plan, oco_stream stream);
 
@@ -243,7 +246,8 @@ int oco_expert_expand(const oco_experts *w, const void *x, oco_dtype x_dtype,
                       float *act_out, oco_stream stream);
 
 /* Weighted combine with residual: out = bf16(out + bf16(sum_r route_r p_r)).
- * routes: [tokens*k, hidden] of routes_dtype (bf16 in the reference).
+ * routes: [tokens*k, hidden] of routes_dtype (bf16 in the reference; f32
+ * route values are rounded to bf16 before weighting, as stored there).
  * Replaces moe_sum (routing.metal:157-168). */
 int oco_moe_sum(const void *routes, oco_dtype routes_dtype, const float *probs, uint16_t *out,
                 uint32_t hidden, uint32_t tokens, uint32_t k, oco_stream stream);

@@ -1,0 +1,443 @@
+// Routed expert path for decode: gate/up projections of the selected experts
+// with the activation fused, the down projection, and the weighted combine.
+// Replaces oco's Bindings::experts (src/weights/compute/feed_forward.rs:
+// 107-275) with its kernels expert_expand (projections.metal:78-137),
+// matvec_mxfp4 (:140-182) and moe_sum (routing.metal:157-168).
+//
+// Each workgroup takes one tile of the route plan -- one expert and up to T
+// of the routes that chose it -- and streams that expert's rows once through
+// the LDS tile path of the decode matvec (stream.h), applying every row to
+// all of the tile's routes.  An expert picked by several tokens is therefore
+// read from HBM once per call, not once per route; experts nobody picked are
+// never touched.
+#include <stdio.h>
+#include <stdlib.h>
+
+#include <algorithm>
+
+#include "route.h"
+#include "stream.h"
+
+namespace oco {
+
+struct MoeArgs {
+    const uint8_t *w[2];     // gated: {gate, up}; otherwise {down, unused}
+    const float *bias[2];    // per-matrix f32 biases [experts * n] or null
+    const void *x;           // activations
+    uint32_t x_bf16;         // activation element type
+    uint32_t input_div;      // route -> activation row: route / input_div
+    float *out0, *out1;      // gated: activation, up (may be null); otherwise y
+    const uint32_t *ids;     // [routes] expert per route (no plan, no logits)
+    const float *logits;     // single token: select the experts in-kernel
+    uint32_t *ids_out;       // with logits: selected ids / probabilities
+    float *probs_out;
+    const uint32_t *plan;    // route plan (tile = (expert, first row)) or null (tile = route)
+    uint32_t k, n, experts, topk, routes;
+    uint64_t row_bytes;
+    uint32_t ngroups;
+    uint32_t act, up_one;
+};
+
+__device__ __forceinline__ float activation(uint32_t act, float g, float u) {
+    if ((__float_as_uint(g) & 0x7f800000u) == 0x7f800000u || (__float_as_uint(u) & 0x7f800000u) == 0x7f800000u)
+        return __uint_as_float(0x7fc00000u);
+    if (act == OCO_ACT_SWIGLU_CLIPPED) {  // projections.metal:4-13
+        g = fminf(g, 7.0f);
+        u = fminf(fmaxf(u, -6.0f), 8.0f);
+        float e = expf(-fabsf(g) * 1.702f);
+        float sig = (g < 0 ? e : 1.0f) / (1.0f + e);
+        return sig * g * u;
+    }
+    float e = expf(-fabsf(g));  // silu(g) * u (elementwise.metal:70-88, in f32)
+    float sig = (g < 0 ? e : 1.0f) / (1.0f + e);
+    return sig * g * u;
+}
+
+constexpr uint32_t PLAN_TILE = 16;  // routes per route-plan tile (its minimum, see oco_route_plan)
+
+template <int FMT, bool GATED, int T, int NPL>
+__global__ __launch_bounds__(256) void moe_kernel(MoeArgs a) {
+    using Tl = Tile<FMT>;
+    constexpr int NM = GATED ? 2 : 1;             // matrices streamed together
+    constexpr int LPR = (NPL * 32 * Tl::BYTES / Tl::P + 32 + 1023) / 1024;
+    constexpr int TROWS = 2 * NM;                 // tile rows per wavefront (R = 1 per half)
+    constexpr int TILE = TROWS * LPR * 1024;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const uint32_t K = a.k, PT = K / Tl::BLOCK * Tl::P;
+    float4 *xs4 = reinterpret_cast<float4 *>(smem);                       // [T][8][PT]
+    float *xsum = reinterpret_cast<float *>(smem + (size_t)T * K * 4);   // [T][NSUM][PT]
+    uint8_t *tiles = smem + (size_t)T * K * 4 + (size_t)T * Tl::NSUM * PT * 4;
+    __shared__ uint32_t sel_ids[8], tile_routes[T], tile_meta[2];
+    __shared__ float sel_probs[8];
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, half = lane >> 5, c = lane & 31;
+
+    // Which expert and which routes this workgroup serves.
+    if (threadIdx.x < 64) {
+        if (a.logits) {
+            select_topk<1>(a.logits, a.experts, a.topk, sel_ids, sel_probs);
+            if (lane == 0) {
+                const uint32_t y = blockIdx.y;
+                tile_meta[0] = sel_ids[y];
+                tile_meta[1] = 1;
+                tile_routes[0] = y;
+                if (blockIdx.x == 0 && blockIdx.y == 0 && a.ids_out)
+                    for (uint32_t r = 0; r < a.topk; r++) {
+                        a.ids_out[r] = sel_ids[r];
+                        a.probs_out[r] = sel_probs[r];
+                    }
+            }
+        } else if (a.plan) {
+            if (lane == 0) {
+                // Plan tiles hold up to PLAN_TILE routes; each is served as
+                // PLAN_TILE / T sub-tiles of T routes.
+                const uint32_t y = blockIdx.y / (PLAN_TILE / T), sub = blockIdx.y % (PLAN_TILE / T);
+                const uint32_t ntiles = a.plan[1];
+                uint32_t count = 0, expert = 0;
+                if (y < ntiles) {
+                    expert = a.plan[6 + 2 * y];
+                    const uint32_t first = a.plan[7 + 2 * y] + sub * T;
+                    const uint64_t grouped = 6 + 2 * ((uint64_t)(a.routes + 15) / 16 + a.experts);
+                    const uint64_t base = grouped + (uint64_t)expert * (a.routes + 1);
+                    const uint32_t total = a.plan[base];
+                    count = first < total ? min((uint32_t)T, total - first) : 0u;
+                    for (uint32_t j = 0; j < count; j++) tile_routes[j] = a.plan[base + 1 + first + j];
+                }
+                tile_meta[0] = expert;
+                tile_meta[1] = count;
+            }
+        } else if (lane == 0) {
+            tile_meta[0] = a.ids[blockIdx.y];
+            tile_meta[1] = 1;
+            tile_routes[0] = blockIdx.y;
+        }
+    }
+    __syncthreads();
+    const uint32_t expert = tile_meta[0], count = tile_meta[1];
+    if (count == 0) return;  // uniform across the workgroup
+
+    // Buffer resources over this expert's rows of each matrix (16-byte aligned
+    // base; range rounded up to the next 16 bytes, see the decode matvec).
+    __amdgpu_buffer_rsrc_t rs[NM];
+    uint32_t shift[NM];
+#pragma unroll
+    for (int m = 0; m < NM; m++) {
+        const uint8_t *eb = a.w[m] + (uint64_t)expert * a.n * a.row_bytes;
+        const uintptr_t al = (uintptr_t)eb & ~(uintptr_t)15;
+        shift[m] = (uint32_t)((uintptr_t)eb & 15);
+        const uint64_t span = ((uint64_t)a.n * a.row_bytes + shift[m] + 15) & ~15ull;
+        rs[m] = __builtin_amdgcn_make_buffer_rsrc((void *)al, 0, (uint32_t)std::min<uint64_t>(span, 0xffffffffull),
+                                                  0x00020000);
+    }
+    const uint32_t row_span = (uint32_t)a.row_bytes, pieces = PT;
+    u32x4 regs[TROWS * LPR];
+    // Tile row i: matrix i / 2, row (group rows) wave*2 + i % 2.
+    auto row_offset = [&](uint32_t g, int i) -> uint32_t {
+        const uint32_t row = g * 8 + wave * 2 + (i & 1);
+        return (uint32_t)(shift[i >> 1] + (uint64_t)row * a.row_bytes);
+    };
+    auto issue = [&](uint32_t g) {
+#pragma unroll
+        for (int i = 0; i < TROWS; i++) {
+            const uint32_t off = row_offset(g, i), start = off & ~15u, need = (off & 15u) + row_span;
+#pragma unroll
+            for (int u = 0; u < LPR; u++) {
+                const uint32_t j = (uint32_t)(u * 64 + lane);
+                regs[i * LPR + u] = 16 * j < need
+                                        ? __builtin_amdgcn_raw_buffer_load_b128(rs[i >> 1], start + 16 * j, 0, 2)
+                                        : u32x4{0, 0, 0, 0};
+            }
+        }
+    };
+    uint32_t g = blockIdx.x;
+    if (g < a.ngroups) issue(g);
+
+    // Stage each route's activation row (piece-major) and its piece sums.
+    for (uint32_t j = 0; j < count; j++) {
+        const uint32_t in = tile_routes[j] / a.input_div;
+        for (uint32_t f = threadIdx.x; f < K / 4; f += 256) {
+            float v[4];
+            if (!a.x_bf16) {
+                float4 t = reinterpret_cast<const float4 *>(a.x)[(uint64_t)in * (K / 4) + f];
+                v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+            } else {
+                uint2 t = reinterpret_cast<const uint2 *>(a.x)[(uint64_t)in * (K / 4) + f];
+                v[0] = __uint_as_float(t.x << 16); v[1] = __uint_as_float(t.x & 0xffff0000u);
+                v[2] = __uint_as_float(t.y << 16); v[3] = __uint_as_float(t.y & 0xffff0000u);
+            }
+            uint32_t pp, tt;
+            Tl::map(f, pp, tt);
+            xs4[(j * 8 + tt) * PT + pp] = make_float4(v[0], v[1], v[2], v[3]);
+        }
+    }
+    if constexpr (Tl::NSUM > 0) {
+        __syncthreads();
+        for (uint32_t q = threadIdx.x; q < count * PT; q += 256) {
+            const uint32_t j = q / PT, pp = q % PT;
+            float xv[32], sv[Tl::NSUM > 0 ? Tl::NSUM : 1];
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                float4 v = xs4[(j * 8 + t) * PT + pp];
+                xv[4 * t] = v.x; xv[4 * t + 1] = v.y; xv[4 * t + 2] = v.z; xv[4 * t + 3] = v.w;
+            }
+            Tl::sums(xv, sv);
+#pragma unroll
+            for (int s = 0; s < Tl::NSUM; s++) xsum[(j * Tl::NSUM + s) * PT + pp] = sv[s];
+        }
+    }
+    __syncthreads();
+
+    uint8_t *tile = tiles + (size_t)wave * TILE;
+    for (; g < a.ngroups; g += gridDim.x) {
+#pragma unroll
+        for (int i = 0; i < TROWS * LPR; i++) reinterpret_cast<u32x4 *>(tile)[i * 64 + lane] = regs[i];
+        uint32_t rbase[NM];
+#pragma unroll
+        for (int m = 0; m < NM; m++) {
+            const int i = 2 * m + half;
+            rbase[m] = i * LPR * 1024 + (row_offset(g, i) & 15u);
+        }
+        if (g + gridDim.x < a.ngroups) issue(g + gridDim.x);
+
+        float acc[NM][T];
+#pragma unroll
+        for (int m = 0; m < NM; m++)
+#pragma unroll
+            for (int j = 0; j < T; j++) acc[m][j] = 0.f;
+#pragma unroll
+        for (int s = 0; s < NPL; s++) {
+            const uint32_t pl = c + 32 * s;
+            if (pl < pieces) {
+                const uint32_t blk = pl / Tl::P, cc = pl % Tl::P;
+                typename Tl::Raw raw[NM];
+#pragma unroll
+                for (int m = 0; m < NM; m++) raw[m] = Tl::load(tile + rbase[m] + blk * Tl::BYTES, cc);
+#pragma unroll
+                for (int j = 0; j < T; j++) {
+                    if ((uint32_t)j < count) {
+                        float xv[32], sv[Tl::NSUM > 0 ? Tl::NSUM : 1];
+#pragma unroll
+                        for (int t = 0; t < 8; t++) {
+                            float4 v = xs4[(j * 8 + t) * PT + pl];
+                            xv[4 * t] = v.x; xv[4 * t + 1] = v.y; xv[4 * t + 2] = v.z; xv[4 * t + 3] = v.w;
+                        }
+#pragma unroll
+                        for (int q = 0; q < Tl::NSUM; q++) sv[q] = xsum[(j * Tl::NSUM + q) * PT + pl];
+#pragma unroll
+                        for (int m = 0; m < NM; m++) acc[m][j] += tile_dot<FMT>(raw[m], xv, sv, cc);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < NM; m++)
+#pragma unroll
+            for (int j = 0; j < T; j++) acc[m][j] = half_sum(acc[m][j]);
+
+        const uint32_t row = g * 8 + wave * 2 + half;
+        if (c < count && row < a.n) {
+            float v0 = acc[0][0], v1 = NM > 1 ? acc[NM - 1][0] : 0.f;
+#pragma unroll
+            for (int j = 1; j < T; j++)
+                if (c == (uint32_t)j) {
+                    v0 = acc[0][j];
+                    v1 = acc[NM - 1][j];
+                }
+            const uint32_t route = tile_routes[c];
+            const uint64_t bi = (uint64_t)expert * a.n + row, o = (uint64_t)route * a.n + row;
+            if (a.bias[0]) v0 += round_bf16(a.bias[0][bi]);
+            if (GATED) {
+                if (a.bias[1]) v1 += round_bf16(a.bias[1][bi] + (a.up_one ? 1.0f : 0.0f));
+                else if (a.up_one) v1 += 1.0f;
+                a.out0[o] = activation(a.act, v0, v1);
+                if (a.out1) a.out1[o] = v1;
+            } else {
+                a.out0[o] = v0;
+            }
+        }
+    }
+}
+
+typedef void (*MoeFn)(MoeArgs);
+constexpr int MOE_T = 4;  // routes per tile
+
+template <int FMT, bool GATED>
+static MoeFn moe_pick(int npl) {
+    switch (npl) {
+    case 1: return moe_kernel<FMT, GATED, MOE_T, 1>;
+    case 2: return moe_kernel<FMT, GATED, MOE_T, 2>;
+    case 3: return moe_kernel<FMT, GATED, MOE_T, 3>;
+    case 4: return moe_kernel<FMT, GATED, MOE_T, 4>;
+    }
+    return nullptr;
+}
+
+static MoeFn moe_pick_format(uint32_t fmt, bool gated, int npl) {
+    switch (fmt) {
+    case OCO_MXFP4: return gated ? moe_pick<OCO_MXFP4, true>(npl) : moe_pick<OCO_MXFP4, false>(npl);
+    case OCO_Q4_K: return gated ? moe_pick<OCO_Q4_K, true>(npl) : moe_pick<OCO_Q4_K, false>(npl);
+    case OCO_Q6_K: return gated ? moe_pick<OCO_Q6_K, true>(npl) : moe_pick<OCO_Q6_K, false>(npl);
+    case OCO_Q8_0: return gated ? moe_pick<OCO_Q8_0, true>(npl) : moe_pick<OCO_Q8_0, false>(npl);
+    }
+    return nullptr;
+}
+
+static int device_cus() {
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        hipGetDevice(&dev);
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+        if (cus <= 0) cus = 256;
+    }
+    return cus;
+}
+
+// Launch one grouped projection over `tiles` tiles.
+static int moe_launch(uint32_t fmt, bool gated, MoeArgs a, uint32_t tiles, uint32_t parallel_tiles,
+                      hipStream_t stream) {
+    uint32_t be, bb;
+    OCO_TRY(oco_block_layout(fmt, &be, &bb));
+    if (a.k % be || a.k % 32) return fail(OCO_ERR_INVALID, "experts: k=%u is not block aligned", a.k);
+    const uint32_t P = (fmt == OCO_Q4_K || fmt == OCO_Q6_K) ? 8 : 1;
+    const uint32_t pieces = a.k / be * P;
+    const int npl = (int)((pieces + 31) / 32);
+    MoeFn fn = npl <= 4 ? moe_pick_format(fmt, gated, npl) : nullptr;
+    if (!fn)
+        return fail(OCO_ERR_UNSUPPORTED, "experts: format %u with k=%u has no routed kernel (rows over %u bytes)",
+                    fmt, a.k, 4 * 32 * bb / P);
+    a.row_bytes = oco_row_bytes(fmt, a.k);
+    a.ngroups = (a.n + 7) / 8;
+    const uint32_t nsum = fmt == OCO_Q8_0 ? 1 : fmt == OCO_Q4_K ? 2 : fmt == OCO_Q6_K ? 4 : 0;
+    const int lpr = (npl * 32 * (int)bb / (int)P + 32 + 1023) / 1024;
+    const size_t lds = (size_t)MOE_T * a.k * 4 + (size_t)MOE_T * nsum * (a.k / 32) * 4 +
+                       4 * (size_t)(2 * (gated ? 2 : 1) * lpr * 1024);
+    if (lds > 150 * 1024) return fail(OCO_ERR_UNSUPPORTED, "experts: k=%u needs %zu bytes of LDS", a.k, lds);
+    if (lds > 64 * 1024)
+        OCO_TRY(hip_check(hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+                          "hipFuncSetAttribute"));
+    const uint32_t target = 2 * device_cus();
+    uint32_t gx = std::max<uint32_t>(1, target / std::max<uint32_t>(1, parallel_tiles));
+    gx = std::min(gx, a.ngroups);
+    hipLaunchKernelGGL(fn, dim3(gx, tiles), dim3(256), lds, stream, a);
+    return launch_check("experts projection");
+}
+
+static int check_bank(const oco_experts *w) {
+    if (!w) return fail(OCO_ERR_INVALID, "experts: null descriptor");
+    if (!w->gate || !w->up || !w->down) return fail(OCO_ERR_INVALID, "experts: null weights");
+    if (w->experts == 0 || w->experts > 256 || w->k == 0 || w->k > 8 || w->k > w->experts)
+        return fail(OCO_ERR_INVALID, "experts: need 0 < k <= 8, k <= experts <= 256");
+    if (w->activation > OCO_ACT_SWIGLU) return fail(OCO_ERR_INVALID, "experts: unknown activation");
+    if (w->hidden == 0 || w->ffn == 0) return fail(OCO_ERR_INVALID, "experts: empty geometry");
+    return OCO_OK;
+}
+
+static uint64_t align256(uint64_t v) { return (v + 255) & ~255ull; }
+
+}  // namespace oco
+
+using namespace oco;
+
+extern "C" {
+
+uint64_t oco_experts_workspace(const oco_experts *w, uint32_t tokens) {
+    if (!w) return 0;
+    const uint64_t routes = (uint64_t)tokens * w->k;
+    return align256(oco_route_plan_words((uint32_t)routes, w->experts) * 4) + align256(routes * w->ffn * 4) +
+           align256(routes * w->hidden * 4);
+}
+
+int oco_experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype, const uint32_t *ids,
+                      const float *probs, uint32_t tokens, uint16_t *out, float *routed, void *workspace,
+                      uint64_t workspace_bytes, oco_stream stream) {
+    OCO_TRY(check_bank(w));
+    if (!tokens) return OCO_OK;
+    if (!x || !ids || !probs || !out || !workspace) return fail(OCO_ERR_INVALID, "oco_experts_apply: null pointer");
+    if (x_dtype != OCO_DT_F32 && x_dtype != OCO_DT_BF16)
+        return fail(OCO_ERR_UNSUPPORTED, "oco_experts_apply: activations must be f32 or bf16");
+    if (workspace_bytes < oco_experts_workspace(w, tokens))
+        return fail(OCO_ERR_INVALID, "oco_experts_apply: workspace of %llu bytes, need %llu",
+                    (unsigned long long)workspace_bytes, (unsigned long long)oco_experts_workspace(w, tokens));
+    hipStream_t s = (hipStream_t)stream;
+    const uint32_t routes = tokens * w->k;
+    uint8_t *ws = (uint8_t *)workspace;
+    uint32_t *plan = (uint32_t *)ws;
+    float *act = (float *)(ws + align256(oco_route_plan_words(routes, w->experts) * 4));
+    float *down = routed ? routed : (float *)((uint8_t *)act + align256((uint64_t)routes * w->ffn * 4));
+
+    uint32_t tiles = routes, parallel = routes;
+    const uint32_t *use_plan = nullptr;
+    if (tokens > 1) {
+        OCO_TRY(oco_route_plan(ids, routes, w->experts, PLAN_TILE, 0, 0, plan, stream));
+        use_plan = plan;
+        tiles = ((routes + PLAN_TILE - 1) / PLAN_TILE + w->experts) * (PLAN_TILE / MOE_T);
+        parallel = std::min(routes, w->experts);
+    }
+    MoeArgs a = {};
+    a.w[0] = (const uint8_t *)w->gate;
+    a.w[1] = (const uint8_t *)w->up;
+    a.bias[0] = w->gate_bias;
+    a.bias[1] = w->up_bias;
+    a.x = x;
+    a.x_bf16 = x_dtype == OCO_DT_BF16;
+    a.input_div = w->k;
+    a.out0 = act;
+    a.out1 = nullptr;
+    a.ids = ids;
+    a.plan = use_plan;
+    a.k = w->hidden;
+    a.n = w->ffn;
+    a.experts = w->experts;
+    a.topk = w->k;
+    a.routes = routes;
+    a.act = w->activation;
+    a.up_one = w->up_bias_one;
+    OCO_TRY(moe_launch(w->format, true, a, tiles, parallel, s));
+
+    MoeArgs d = a;
+    d.w[0] = (const uint8_t *)w->down;
+    d.w[1] = nullptr;
+    d.bias[0] = w->down_bias;
+    d.bias[1] = nullptr;
+    d.x = act;
+    d.x_bf16 = 0;
+    d.input_div = 1;
+    d.out0 = down;
+    d.k = w->ffn;
+    d.n = w->hidden;
+    OCO_TRY(moe_launch(w->format, false, d, tiles, parallel, s));
+    return oco_moe_sum(down, OCO_DT_F32, probs, out, w->hidden, tokens, w->k, stream);
+}
+
+int oco_expert_expand(const oco_experts *w, const void *x, oco_dtype x_dtype, const float *logits, uint32_t *ids,
+                      float *probs, float *up_out, float *act_out, oco_stream stream) {
+    OCO_TRY(check_bank(w));
+    if (!x || !logits || !ids || !probs || !act_out) return fail(OCO_ERR_INVALID, "oco_expert_expand: null pointer");
+    if (w->experts > 64) return fail(OCO_ERR_UNSUPPORTED, "oco_expert_expand: fused selection covers <= 64 experts");
+    if (x_dtype != OCO_DT_F32 && x_dtype != OCO_DT_BF16)
+        return fail(OCO_ERR_UNSUPPORTED, "oco_expert_expand: activations must be f32 or bf16");
+    MoeArgs a = {};
+    a.w[0] = (const uint8_t *)w->gate;
+    a.w[1] = (const uint8_t *)w->up;
+    a.bias[0] = w->gate_bias;
+    a.bias[1] = w->up_bias;
+    a.x = x;
+    a.x_bf16 = x_dtype == OCO_DT_BF16;
+    a.input_div = w->k;
+    a.out0 = act_out;
+    a.out1 = up_out;
+    a.logits = logits;
+    a.ids_out = ids;
+    a.probs_out = probs;
+    a.k = w->hidden;
+    a.n = w->ffn;
+    a.experts = w->experts;
+    a.topk = w->k;
+    a.routes = w->k;
+    a.act = w->activation;
+    a.up_one = w->up_bias_one;
+    return moe_launch(w->format, true, a, w->k, w->k, (hipStream_t)stream);
+}
+
+}  // extern "C"

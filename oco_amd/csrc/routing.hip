@@ -1,0 +1,195 @@
+// Routing for the expert path: top-k selection, router logits, per-expert
+// route plans and the weighted combine.  Replaces oco's
+// shaders/experts/routing.metal (select_expert_values :71-94, router
+// :96-128, router_logits :131-146, route_plan_64 :4-39, moe_sum :157-168) and
+// nemotron.metal's route_plan_n (:238-273).
+#include <algorithm>
+
+#include "route.h"
+
+namespace oco {
+
+template <int PER>
+__global__ __launch_bounds__(64) void route_select_kernel(const float *logits, uint32_t tokens,
+                                                          uint32_t experts, uint32_t k, uint32_t *ids,
+                                                          float *probs) {
+    const uint32_t t = blockIdx.x;
+    if (t >= tokens) return;
+    select_topk<PER>(logits + (uint64_t)t * experts, experts, k, ids + (uint64_t)t * k,
+                     probs + (uint64_t)t * k);
+}
+
+// Router logits = sum_k bf16(x) bf16(W[e]) + bf16(bias[e]) (routing.metal:96-146):
+// one wavefront per (token, expert), fp32 FMA accumulation.
+template <typename XT>
+__global__ __launch_bounds__(256) void router_logits_kernel(const XT *x, const float *w, const float *bias,
+                                                            uint32_t tokens, uint32_t hidden,
+                                                            uint32_t experts, float *logits) {
+    const uint32_t wave = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (wave >= tokens * experts) return;
+    const uint32_t t = wave / experts, e = wave % experts;
+    float acc = 0.f;
+    for (uint32_t i = lane; i < hidden; i += 64) {
+        float xv = XLoad<XT>::one(x + (uint64_t)t * hidden, i);
+        if constexpr (sizeof(XT) == 4) xv = round_bf16(xv);
+        acc = fmaf(xv, round_bf16(w[(uint64_t)e * hidden + i]), acc);
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) logits[(uint64_t)t * experts + e] = acc + (bias ? round_bf16(bias[e]) : 0.f);
+}
+
+// Route plan (routing.metal:4-39, nemotron.metal:238-273) by one workgroup:
+// per-expert route lists in route order, expert-sorted first rows, each
+// route's sorted row, (expert, first list row) tiles of `tile_rows`, and the
+// two dispatch grids at words 0-5.  Counts go through LDS; lists are
+// written by one thread per expert.
+__global__ __launch_bounds__(256) void route_plan_kernel(const uint32_t *ids, uint32_t routes,
+                                                         uint32_t experts, uint32_t tile_rows,
+                                                         uint32_t up_tiles, uint32_t down_tiles,
+                                                         uint32_t *plan) {
+    extern __shared__ uint32_t counts[];  // [experts] counts, [experts] offsets
+    const uint64_t grouped = 6 + 2 * ((uint64_t)(routes + 15) / 16 + experts);
+    const uint64_t sorted = grouped + (uint64_t)experts * (routes + 1);
+    for (uint32_t e = threadIdx.x; e < experts; e += blockDim.x) {
+        uint32_t count = 0;
+        const uint64_t base = grouped + (uint64_t)e * (routes + 1);
+        for (uint32_t i = 0; i < routes; i++)
+            if (ids[i] == e) plan[base + 1 + count++] = i;
+        plan[base] = count;
+        counts[e] = count;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t tiles = 0, offset = 0;
+        for (uint32_t e = 0; e < experts; e++) {
+            counts[experts + e] = offset;
+            plan[sorted + e] = offset;
+            offset += counts[e];
+            for (uint32_t b = 0; b < counts[e]; b += tile_rows) {
+                plan[6 + 2 * (uint64_t)tiles] = e;
+                plan[6 + 2 * (uint64_t)tiles + 1] = b;
+                tiles++;
+            }
+        }
+        plan[0] = up_tiles;
+        plan[1] = tiles;
+        plan[2] = 1;
+        plan[3] = down_tiles;
+        plan[4] = tiles;
+        plan[5] = 1;
+    }
+    __syncthreads();
+    for (uint32_t e = threadIdx.x; e < experts; e += blockDim.x) {
+        const uint64_t base = grouped + (uint64_t)e * (routes + 1);
+        const uint32_t count = counts[e], offset = counts[experts + e];
+        for (uint32_t i = 0; i < count; i++) plan[sorted + experts + plan[base + 1 + i]] = offset + i;
+    }
+}
+
+// out[t, d] = bf16(out + bf16(sum_r route[t*k + r, d] * p[t, r])), the sum in
+// route order in fp32 (routing.metal:157-168).  The reference stores route
+// outputs as bf16, so f32 route values are rounded to bf16 first.
+template <typename RT>
+__global__ __launch_bounds__(256) void moe_sum_kernel(const RT *routes, const float *probs, uint16_t *out,
+                                                      uint32_t hidden, uint32_t tokens, uint32_t k) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (uint64_t)hidden * tokens) return;
+    const uint64_t t = i / hidden, d = i % hidden;
+    float s = 0.f;
+    for (uint32_t r = 0; r < k; r++) {
+        float v;
+        if constexpr (sizeof(RT) == 4)
+            v = round_bf16(routes[(t * k + r) * hidden + d]);
+        else
+            v = bf16_bits_to_f32(routes[(t * k + r) * hidden + d].bits);
+        s = fmaf(v, probs[t * k + r], s);
+    }
+    out[i] = f32_to_bf16_bits(bf16_bits_to_f32(out[i]) + round_bf16(s));
+}
+
+}  // namespace oco
+
+using namespace oco;
+
+extern "C" {
+
+int oco_route_select(const float *logits, uint32_t tokens, uint32_t experts, uint32_t k, uint32_t *ids,
+                     float *probs, oco_stream stream) {
+    if (!tokens) return OCO_OK;
+    if (!logits || !ids || !probs) return fail(OCO_ERR_INVALID, "oco_route_select: null pointer");
+    if (experts == 0 || experts > 256 || k == 0 || k > 8 || k > experts)
+        return fail(OCO_ERR_INVALID, "oco_route_select: need 0 < k <= 8, k <= experts <= 256");
+    hipStream_t s = (hipStream_t)stream;
+    if (experts <= 64)
+        hipLaunchKernelGGL(route_select_kernel<1>, dim3(tokens), dim3(64), 0, s, logits, tokens, experts, k, ids, probs);
+    else if (experts <= 128)
+        hipLaunchKernelGGL(route_select_kernel<2>, dim3(tokens), dim3(64), 0, s, logits, tokens, experts, k, ids, probs);
+    else
+        hipLaunchKernelGGL(route_select_kernel<4>, dim3(tokens), dim3(64), 0, s, logits, tokens, experts, k, ids, probs);
+    return launch_check("oco_route_select");
+}
+
+int oco_router(const void *x, oco_dtype x_dtype, const float *w, const float *bias, uint32_t tokens,
+               uint32_t hidden, uint32_t experts, uint32_t k, float *logits, uint32_t *ids, float *probs,
+               oco_stream stream) {
+    if (!tokens) return OCO_OK;
+    if (!x || !w || !ids || !probs) return fail(OCO_ERR_INVALID, "oco_router: null pointer");
+    if (experts == 0 || experts > 256 || k == 0 || k > 8 || k > experts)
+        return fail(OCO_ERR_INVALID, "oco_router: need 0 < k <= 8, k <= experts <= 256");
+    hipStream_t s = (hipStream_t)stream;
+    float *l = logits;
+    if (!l) {
+        // Caller did not ask for the logits: keep them in a per-call allocation.
+        OCO_TRY(hip_check(hipMallocAsync((void **)&l, (size_t)tokens * experts * 4, s), "hipMallocAsync"));
+    }
+    uint32_t waves = tokens * experts;
+    if (x_dtype == OCO_DT_F32)
+        hipLaunchKernelGGL(router_logits_kernel<float>, dim3((waves + 3) / 4), dim3(256), 0, s,
+                           (const float *)x, w, bias, tokens, hidden, experts, l);
+    else if (x_dtype == OCO_DT_BF16)
+        hipLaunchKernelGGL(router_logits_kernel<bf16_t>, dim3((waves + 3) / 4), dim3(256), 0, s,
+                           (const bf16_t *)x, w, bias, tokens, hidden, experts, l);
+    else
+        return fail(OCO_ERR_UNSUPPORTED, "oco_router: activations must be f32 or bf16");
+    OCO_TRY(launch_check("oco_router logits"));
+    int rc = oco_route_select(l, tokens, experts, k, ids, probs, stream);
+    if (!logits) hipFreeAsync(l, s);
+    return rc;
+}
+
+uint64_t oco_route_plan_words(uint32_t routes, uint32_t experts) {
+    return 6 + 2 * ((uint64_t)(routes + 15) / 16 + experts) + (uint64_t)experts * (routes + 1) + experts +
+           routes;
+}
+
+int oco_route_plan(const uint32_t *ids, uint32_t routes, uint32_t experts, uint32_t tile_rows,
+                   uint32_t up_tiles, uint32_t down_tiles, uint32_t *plan, oco_stream stream) {
+    if (!ids || !plan) return fail(OCO_ERR_INVALID, "oco_route_plan: null pointer");
+    if (experts == 0 || experts > 4096 || tile_rows < 16)
+        return fail(OCO_ERR_INVALID,
+                    "oco_route_plan: need 0 < experts <= 4096 and tile_rows >= 16 (the plan holds ceil(routes/16) + "
+                    "experts tiles)");
+    hipLaunchKernelGGL(route_plan_kernel, dim3(1), dim3(256), (size_t)experts * 8, (hipStream_t)stream, ids,
+                       routes, experts, tile_rows, up_tiles, down_tiles, plan);
+    return launch_check("oco_route_plan");
+}
+
+int oco_moe_sum(const void *routes, oco_dtype routes_dtype, const float *probs, uint16_t *out,
+                uint32_t hidden, uint32_t tokens, uint32_t k, oco_stream stream) {
+    uint64_t n = (uint64_t)hidden * tokens;
+    if (!n) return OCO_OK;
+    if (!routes || !probs || !out) return fail(OCO_ERR_INVALID, "oco_moe_sum: null pointer");
+    hipStream_t s = (hipStream_t)stream;
+    unsigned grid = (unsigned)((n + 255) / 256);
+    if (routes_dtype == OCO_DT_F32)
+        hipLaunchKernelGGL(moe_sum_kernel<float>, dim3(grid), dim3(256), 0, s, (const float *)routes, probs,
+                           out, hidden, tokens, k);
+    else if (routes_dtype == OCO_DT_BF16)
+        hipLaunchKernelGGL(moe_sum_kernel<bf16_t>, dim3(grid), dim3(256), 0, s, (const bf16_t *)routes, probs,
+                           out, hidden, tokens, k);
+    else
+        return fail(OCO_ERR_UNSUPPORTED, "oco_moe_sum: routes must be f32 or bf16");
+    return launch_check("oco_moe_sum");
+}
+
+}  // extern "C"

@@ -374,6 +374,8 @@ uint64_t oo_route_plan_words(uint32_t routes, uint32_t experts) {
  * first row in expert-sorted order; then each route's sorted row. */
 uint64_t oo_route_plan(const uint32_t *ids, uint32_t routes, uint32_t experts, uint32_t tile_rows,
                        uint32_t up_tiles, uint32_t down_tiles, uint32_t *plan) {
+    if (tile_rows < 16) /* the tile area holds ceil(routes/16) + experts tiles */
+        return (uint64_t)-1;
     uint64_t grouped = 6 + 2 * ((uint64_t)(routes + 15) / 16 + experts);
     uint64_t sorted = grouped + (uint64_t)experts * (routes + 1);
     uint32_t tiles = 0, offset = 0;

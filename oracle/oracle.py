@@ -143,6 +143,8 @@ def route_plan(ids: np.ndarray, experts: int, tile_rows: int, up_tiles: int, dow
     words = lib().oo_route_plan_words(ids.size, experts)
     plan = np.zeros(words, np.uint32)
     tiles = lib().oo_route_plan(_p(ids), ids.size, experts, tile_rows, up_tiles, down_tiles, _p(plan))
+    if tiles == 2 ** 64 - 1:
+        raise ValueError("tile_rows must be >= 16")
     return plan, int(tiles)
 
 
@@ -188,3 +190,90 @@ def roundoff_bound(expected, magnitude, k: int, stored_bf16: bool):
     gamma = ops * unit / (1 - ops * unit)
     storage = 2.0 ** -8 if stored_bf16 else 0.0
     return (1 + storage) * gamma * np.asarray(magnitude) + storage * np.abs(np.asarray(expected))
+
+
+# --- composed references for the expert path and prefill ----------------------
+
+def expert_rows(fmt: int, w: np.ndarray, expert: int, n: int, k: int) -> np.ndarray:
+    """Rows of one expert of a bank [experts][n][k rows of GGUF blocks], fp64."""
+    rb = k // block_layout(fmt)[0] * block_layout(fmt)[1]
+    sl = np.ascontiguousarray(np.asarray(w, np.uint8)[expert * n * rb:(expert + 1) * n * rb])
+    return dequant(fmt, sl, n * k).astype(np.float64).reshape(n, k)
+
+
+def bf16_round(x) -> np.ndarray:
+    return bf16_to_f32(f32_to_bf16(np.asarray(x, np.float32))).astype(np.float64)
+
+
+def swiglu_clipped_f64(g, u):
+    """projections.metal:4-13 in fp64: sigmoid(1.702 g') g' u', g' = min(g, 7), u' = clamp(u, -6, 8)."""
+    g = np.minimum(g, 7.0)
+    u = np.clip(u, -6.0, 8.0)
+    return g / (1.0 + np.exp(-1.702 * g)) * u
+
+
+def swiglu_f64(g, u):
+    """silu(g) * u (elementwise.metal:70-88 without its bf16 storage)."""
+    return g / (1.0 + np.exp(-g)) * u
+
+
+def experts_reference(fmt, hidden, ffn, gate, up, down, x, ids, probs, residual_bf16,
+                      gate_bias=None, up_bias=None, down_bias=None, activation=0, up_one=True,
+                      act_override=None):
+    """Bindings::experts (feed_forward.rs:107-275) in fp64 after routing:
+    per route r of token t = r / k with expert e = ids[r]:
+      g = gate_e . x_t + bf16(gate_bias), u = up_e . x_t + bf16(up_bias + 1)
+      a = act(g, u); y_r = down_e . a + bf16(down_bias)
+    out[t] = bf16(residual + bf16(sum_r bf16(y_r) p_r))   (routing.metal:157-168).
+    `act_override` (routes x ffn) feeds the down projection with given values
+    (the GPU's own f32 activations), as the reference's test does (mxfp4.rs:458-470)."""
+    x = np.asarray(x)
+    xf = bf16_to_f32(x).astype(np.float64) if x.dtype == np.uint16 else x.astype(np.float64)
+    tokens = xf.shape[0]
+    ids = np.asarray(ids, np.uint32).reshape(-1)
+    k = ids.size // tokens
+    routes = ids.size
+    act = np.zeros((routes, ffn))
+    upv = np.zeros((routes, ffn))
+    gat = np.zeros((routes, ffn))
+    mag_up = np.zeros((routes, ffn))
+    y = np.zeros((routes, hidden))
+    mag_y = np.zeros((routes, hidden))
+    cache = {}
+    for r in range(routes):
+        e = int(ids[r])
+        if e not in cache:
+            cache[e] = (expert_rows(fmt, gate, e, ffn, hidden), expert_rows(fmt, up, e, ffn, hidden),
+                        expert_rows(fmt, down, e, hidden, ffn))
+        G, U, D = cache[e]
+        xt = xf[r // k]
+        gb = bf16_round(gate_bias[e * ffn:(e + 1) * ffn]) if gate_bias is not None else 0.0
+        ub = (bf16_round(up_bias[e * ffn:(e + 1) * ffn] + (1.0 if up_one else 0.0)) if up_bias is not None
+              else (1.0 if up_one else 0.0))
+        gat[r] = G @ xt + gb
+        upv[r] = U @ xt + ub
+        mag_up[r] = np.abs(U) @ np.abs(xt) + np.abs(ub)
+        act[r] = (swiglu_clipped_f64 if activation == 0 else swiglu_f64)(gat[r], upv[r])
+        a_in = act[r] if act_override is None else np.asarray(act_override[r], np.float64)
+        db = bf16_round(down_bias[e * hidden:(e + 1) * hidden]) if down_bias is not None else 0.0
+        y[r] = D @ a_in + db
+        mag_y[r] = np.abs(D) @ np.abs(a_in) + np.abs(db)
+    p = np.asarray(probs, np.float64).reshape(tokens, k)
+    yb = bf16_round(y).reshape(tokens, k, hidden)
+    s = np.einsum("tkh,tk->th", yb, p)
+    res = bf16_to_f32(np.asarray(residual_bf16, np.uint16)).astype(np.float64)
+    out = f32_to_bf16((res + bf16_round(s)).astype(np.float32))
+    return {"gate": gat, "up": upv, "up_mag": mag_up, "act": act, "down": y, "down_mag": mag_y, "out": out}
+
+
+def matmul_reference(fmt, w, x, n, k, half_operands: bool):
+    """Y = X W^T in fp64 (matrix_precision.rs:119-142): optionally with both
+    operands rounded to f16 first (the reference's tiled kernels' half(w),
+    half(x)), and sum |w x| for the roundoff bound."""
+    W = dequant(fmt, w, n * k).astype(np.float64).reshape(n, k)
+    x = np.asarray(x)
+    X = bf16_to_f32(x).astype(np.float64) if x.dtype == np.uint16 else x.astype(np.float64)
+    if half_operands:
+        W = W.astype(np.float16).astype(np.float64)
+        X = X.astype(np.float16).astype(np.float64)
+    return X @ W.T, np.abs(X) @ np.abs(W).T

@@ -1,0 +1,233 @@
+"""GPU parity of the routing and routed-expert path against the oracle.
+
+Known answers and fixtures from the reference's own tests
+(src/weights/dispatch_tests/mxfp4.rs): logits_selecting([3,0,2,1]), the
+MXFP4 decode packer at K=2880/N=33 with the unaligned byte offset, the
+E8M0=255 NaN rule, and the batch-17/257 id pattern with overfull experts.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+import packers as P
+from _util import Guarded, rel_l2, say, upload_at_offset
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(oco, a):
+    return oco.DeviceBuffer.from_array(np.ascontiguousarray(a))
+
+
+# ---- routing ------------------------------------------------------------------
+
+@pytest.mark.parametrize("tokens,experts,k", [(1, 32, 4), (16, 32, 4), (257, 32, 4), (512, 128, 8),
+                                              (3, 5, 5), (7, 256, 8)])
+def test_route_select_matches_oracle(lib, tokens, experts, k):
+    say("route_select", tokens, experts, k)
+    rng = np.random.default_rng(tokens * 1000 + experts)
+    logits = rng.normal(size=(tokens, experts)).astype(np.float32)
+    logits[0, :4] = 0.5  # a tie at the top: lowest index wins
+    ids_b, probs_b = lib.DeviceBuffer(tokens * k * 4), lib.DeviceBuffer(tokens * k * 4)
+    lib.route_select(dev(lib, logits), tokens, experts, k, ids_b, probs_b)
+    lib.synchronize()
+    ids, probs = ids_b.download(np.uint32).reshape(tokens, k), probs_b.download(np.float32).reshape(tokens, k)
+    want_ids, want_probs = O.select_experts(logits, k)
+    np.testing.assert_array_equal(ids, want_ids)
+    # probabilities are bf16: equal up to one bf16 step (exp is not bit-pinned)
+    np.testing.assert_allclose(probs, want_probs, rtol=2 ** -7, atol=0)
+
+
+def test_route_select_known_answer_and_nan(lib):
+    logits = np.stack([P.logits_selecting([3, 0, 2, 1]), np.zeros(32, np.float32),
+                       np.where(np.arange(32) == 5, np.nan, 0.0).astype(np.float32)])
+    ids_b, probs_b = lib.DeviceBuffer(3 * 16), lib.DeviceBuffer(3 * 16)
+    lib.route_select(dev(lib, logits), 3, 32, 4, ids_b, probs_b)
+    lib.synchronize()
+    ids, probs = ids_b.download(np.uint32).reshape(3, 4), probs_b.download(np.float32).reshape(3, 4)
+    assert list(ids[0]) == [3, 0, 2, 1]
+    assert list(ids[1]) == [0, 1, 2, 3] and np.all(probs[1] == 0.25)
+    assert np.all(ids[2] < 32) and np.all(np.isnan(probs[2]))
+
+
+def test_router_logits(lib):
+    tokens, hidden, experts, k = 5, 2880, 32, 4
+    rng = np.random.default_rng(11)
+    x = rng.normal(size=(tokens, hidden)).astype(np.float32)
+    w = (rng.normal(size=(experts, hidden)) * 0.02).astype(np.float32)
+    b = rng.normal(size=experts).astype(np.float32)
+    lb, ib, pb = lib.DeviceBuffer(tokens * experts * 4), lib.DeviceBuffer(tokens * k * 4), lib.DeviceBuffer(tokens * k * 4)
+    lib.router(dev(lib, x), lib.DType.F32, dev(lib, w), dev(lib, b), tokens, hidden, experts, k, lb, ib, pb)
+    lib.synchronize()
+    got = lb.download(np.float32).reshape(tokens, experts)
+    want = O.bf16_round(x) @ O.bf16_round(w).T + O.bf16_round(b)
+    assert rel_l2(got, want) < 1e-5
+    want_ids, _ = O.select_experts(got, k)
+    np.testing.assert_array_equal(ib.download(np.uint32).reshape(tokens, k), want_ids)
+
+
+@pytest.mark.parametrize("batch,experts,tile", [(1, 32, 16), (17, 32, 64), (257, 32, 64), (512, 128, 16)])
+def test_route_plan_bit_exact(lib, batch, experts, tile):
+    say("route_plan", batch, experts, tile)
+    if experts == 32 and batch > 1:
+        ids = P.expert_ids(batch)
+    elif batch == 1:
+        ids = np.array([3, 0, 2, 1], np.uint32)
+    else:
+        ids = np.random.default_rng(3).integers(0, experts, batch * 8).astype(np.uint32)
+    routes = ids.size
+    words = lib.route_plan_words(routes, experts)
+    assert words == O.route_plan_words(routes, experts)
+    out = Guarded(lib, words * 4)
+    lib.route_plan(dev(lib, ids), routes, experts, tile, 9, 5, out.ptr)
+    lib.synchronize()
+    want, tiles = O.route_plan(ids, experts, tile, 9, 5)
+    got = out.read(np.uint32)
+    # Defined words: grids, used tile pairs, each list's count and entries,
+    # sorted offsets and route rows (unused slots are unspecified).
+    defined = np.zeros(words, bool)
+    defined[:6 + 2 * tiles] = True
+    grouped = 6 + 2 * ((routes + 15) // 16 + experts)
+    for e in range(experts):
+        base = grouped + e * (routes + 1)
+        defined[base:base + 1 + want[base]] = True
+    defined[grouped + experts * (routes + 1):] = True
+    np.testing.assert_array_equal(got[defined], want[defined])
+
+
+def test_moe_sum(lib):
+    hidden, tokens, k = 2880, 16, 4
+    rng = np.random.default_rng(5)
+    routes = O.f32_to_bf16(rng.normal(size=(tokens * k, hidden)).astype(np.float32))
+    probs = O.bf16_round(rng.dirichlet(np.ones(k), size=tokens)).astype(np.float32)
+    resid = O.f32_to_bf16(rng.normal(size=(tokens, hidden)).astype(np.float32))
+    outb = dev(lib, resid)
+    lib.moe_sum(dev(lib, routes), lib.DType.BF16, dev(lib, probs), outb, hidden, tokens, k)
+    lib.synchronize()
+    got = outb.download(np.uint16).reshape(tokens, hidden)
+    want = O.moe_sum(routes, probs, resid, k)
+    # fp32 sums may differ by fused rounding: at most one bf16 step apart
+    diff = np.abs(got.astype(np.int32) - want.astype(np.int32))
+    assert diff.max() <= 1 and (diff > 0).mean() < 0.01
+
+
+# ---- expert projections -------------------------------------------------------
+
+def bank(oco, fmt, experts, hidden, ffn, seed):
+    from oco_amd import synth
+    g = synth.weights(fmt, experts * ffn, hidden, seed)
+    u = synth.weights(fmt, experts * ffn, hidden, seed + 1)
+    d = synth.weights(fmt, experts * hidden, ffn, seed + 2)
+    rng = np.random.default_rng(seed)
+    gb = (rng.normal(size=experts * ffn) * 0.1).astype(np.float32)
+    ub = (rng.normal(size=experts * ffn) * 0.1).astype(np.float32)
+    db = (rng.normal(size=experts * hidden) * 0.1).astype(np.float32)
+    return (g, u, d, gb, ub, db), [dev(oco, a) for a in (g, u, d, gb, ub, db)]
+
+
+def test_expert_expand_reference_fixture(lib):
+    """expert_expand at K=2880, N=33 on the reference's MXFP4 packer, weights at
+    byte offset 7, ids [3,0,2,1] chosen from logits (mxfp4.rs:46-179)."""
+    k, n = 2880, 33
+    data, coeffs = P.mxfp4_decode_weights(k, n)
+    body = np.frombuffer(data, np.uint8)[P.WEIGHT_OFFSET:]
+    wbuf, wptr = upload_at_offset(lib, body, P.WEIGHT_OFFSET)
+    x = P.mxfp4_decode_input(k)[:k]
+    xb = O.f32_to_bf16(x)
+    bias = np.array([((P.noise(i + 151) % 997) - 498) / 509.0 for i in range(4 * n)], np.float32)
+    bias32 = np.zeros(32 * n, np.float32)
+    bias32[:4 * n] = bias
+    ids = [3, 0, 2, 1]
+    bk = lib.ExpertBank(39, k, n, 32, 4, wptr, wptr, wptr, dev(lib, bias32), dev(lib, bias32), None)
+    up, act = Guarded(lib, 4 * n * 4), Guarded(lib, 4 * n * 4)
+    ib, pb = lib.DeviceBuffer(16), lib.DeviceBuffer(16)
+    bk.expand(dev(lib, xb), lib.DType.BF16, dev(lib, P.logits_selecting(ids)), ib, pb, up.ptr, act.ptr)
+    lib.synchronize()
+    assert list(ib.download(np.uint32)) == ids
+    W = coeffs.reshape(4, n, k)
+    xf = O.bf16_to_f32(xb).astype(np.float64)
+    got_up, got_act = up.read(np.float32).reshape(4, n), act.read(np.float32).reshape(4, n)
+    for r, e in enumerate(ids):
+        ub = O.bf16_round(bias[e * n:(e + 1) * n] + 1.0)
+        gb = O.bf16_round(bias[e * n:(e + 1) * n])
+        want_up = W[e] @ xf + ub
+        mag = np.abs(W[e]) @ np.abs(xf) + np.abs(ub)
+        assert np.all(np.abs(got_up[r] - want_up) <= O.roundoff_bound(want_up, mag, k, False))
+        want_act = O.swiglu_clipped_f64(W[e] @ xf + gb, want_up)
+        assert np.all(np.abs(got_act[r] - want_act) <= 1e-3 * np.maximum(np.abs(want_act), 1.0))
+    # E8M0 255 in the first selected expert's first block propagates NaN (mxfp4.rs:205-233)
+    bad = body.copy()
+    bad[ids[0] * n * (k // 32) * 17] = 255
+    wbuf.upload(bad, P.WEIGHT_OFFSET)
+    bk.expand(dev(lib, xb), lib.DType.BF16, dev(lib, P.logits_selecting(ids)), ib, pb, up.ptr, act.ptr)
+    lib.synchronize()
+    assert np.isnan(up.read(np.float32)[0])
+
+
+@pytest.mark.parametrize("fmt", [39, 12])
+@pytest.mark.parametrize("tokens", [1, 4, 16])
+def test_experts_apply_matches_oracle(lib, fmt, tokens):
+    """Full routed layer after the router: gate/up + clipped SwiGLU + down +
+    weighted combine with residual, batches 1/4/16 (BASELINE cfg 4 shapes
+    scaled down to hidden = ffn = 512)."""
+    E, hidden, ffn, k = 32, 512, 512, 4
+    say("experts_apply", fmt, tokens)
+    host, devs = bank(lib, fmt, E, hidden, ffn, seed=40 + tokens)
+    g, u, d, gb, ub, db = host
+    rng = np.random.default_rng(tokens)
+    x = rng.normal(size=(tokens, hidden)).astype(np.float32)
+    ids, probs = O.select_experts(rng.normal(size=(tokens, E)).astype(np.float32), k)
+    resid = O.f32_to_bf16(rng.normal(size=(tokens, hidden)).astype(np.float32))
+    act = 0 if fmt == 39 else 1
+    bk = lib.ExpertBank(fmt, hidden, ffn, E, k, *devs, activation=act, up_bias_one=(fmt == 39))
+    outb = dev(lib, resid)
+    routed = Guarded(lib, tokens * k * hidden * 4)
+    bk.apply(dev(lib, x), lib.DType.F32, dev(lib, ids), dev(lib, probs), tokens, outb, routed=routed.ptr)
+    lib.synchronize()
+    got_out = outb.download(np.uint16).reshape(tokens, hidden)
+    got_routed = routed.read(np.float32).reshape(tokens * k, hidden)
+    ref = O.experts_reference(fmt, hidden, ffn, g, u, d, x, ids, probs, resid, gb, ub, db,
+                              activation=act, up_one=(fmt == 39))
+    assert rel_l2(got_routed, ref["down"]) < 1e-4
+    diff = np.abs(O.bf16_to_f32(got_out).astype(np.float64) - O.bf16_to_f32(ref["out"]))
+    assert np.all(diff <= 2 ** -6 * np.abs(O.bf16_to_f32(ref["out"])) + 1e-2)
+
+
+def test_experts_overfull_tiles(lib):
+    """Batch 257 with ids [31, t%15, 15+t%8, 30]: experts 30/31 own 257 routes each,
+    spanning many tiles (mxfp4.rs:309-482)."""
+    E, hidden, ffn, k, tokens = 32, 96, 96, 4, 257
+    say("experts overfull")
+    host, devs = bank(lib, 39, E, hidden, ffn, seed=77)
+    g, u, d, gb, ub, db = host
+    rng = np.random.default_rng(7)
+    x = rng.normal(size=(tokens, hidden)).astype(np.float32)
+    ids = P.expert_ids(tokens).reshape(tokens, k)
+    probs = np.full((tokens, k), 0.25, np.float32)
+    resid = np.zeros((tokens, hidden), np.uint16)
+    bk = lib.ExpertBank(39, hidden, ffn, E, k, *devs)
+    outb = dev(lib, resid)
+    routed = Guarded(lib, tokens * k * hidden * 4)
+    bk.apply(dev(lib, x), lib.DType.F32, dev(lib, ids), dev(lib, probs), tokens, outb, routed=routed.ptr)
+    lib.synchronize()
+    ref = O.experts_reference(39, hidden, ffn, g, u, d, x, ids, probs, resid, gb, ub, db)
+    assert rel_l2(routed.read(np.float32).reshape(-1, hidden), ref["down"]) < 1e-4
+
+
+def test_experts_full_shape_batch4(lib):
+    """gpt-oss-20b shape: 32 experts, hidden = ffn = 2880, MXFP4, top-4, batch 4."""
+    E, hidden, ffn, k, tokens = 32, 2880, 2880, 4, 4
+    say("experts full shape")
+    host, devs = bank(lib, 39, E, hidden, ffn, seed=5)
+    g, u, d, gb, ub, db = host
+    rng = np.random.default_rng(9)
+    x = rng.normal(size=(tokens, hidden)).astype(np.float32)
+    ids, probs = O.select_experts(rng.normal(size=(tokens, E)).astype(np.float32), k)
+    resid = O.f32_to_bf16(rng.normal(size=(tokens, hidden)).astype(np.float32))
+    bk = lib.ExpertBank(39, hidden, ffn, E, k, *devs)
+    outb = dev(lib, resid)
+    routed = Guarded(lib, tokens * k * hidden * 4)
+    bk.apply(dev(lib, x), lib.DType.F32, dev(lib, ids), dev(lib, probs), tokens, outb, routed=routed.ptr)
+    lib.synchronize()
+    ref = O.experts_reference(39, hidden, ffn, g, u, d, x, ids, probs, resid, gb, ub, db)
+    assert rel_l2(routed.read(np.float32).reshape(-1, hidden), ref["down"]) < 1e-4
