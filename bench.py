@@ -113,6 +113,107 @@ class MatvecStack(Workload):
         return float(self.bytes)
 
 
+class MoeDecode(Workload):
+    """gpt-oss-20b expert layer: 32 experts, gate/up [2880 x 2880] and down
+    [2880 x 2880] MXFP4, top-4 of softmax(N(0,1) logits), clipped SwiGLU,
+    weighted combine with residual; `tokens` per step.  Two copies of the
+    bank (2 x 423 MB) and 64 routing tables rotate so successive steps miss
+    the Infinity Cache.  Work = distinct experts hit x 13,219,200 bytes."""
+
+    def __init__(self, tokens):
+        self.tokens = tokens
+        self.name = f"moe_decode_gpt_oss_b{tokens}"
+
+    def setup(self, oco, stream):
+        import numpy as np
+        from oco_amd import synth
+        self.oco, self.stream = oco, stream
+        E, h, f, k = 32, 2880, 2880, 4
+        self.k = k
+        banks = _BANKS.get("gpt_oss")
+        if banks is None:
+            banks = _BANKS["gpt_oss"] = self._banks(oco, E, h, f, k)
+        self.banks = banks
+        self.tables = []
+        distinct = []
+        rng = np.random.default_rng(1234)
+        for t in range(64):
+            logits = rng.normal(size=(self.tokens, E)).astype(np.float32)
+            ids, probs = _select(logits, k)
+            distinct.append(len(set(ids.ravel().tolist())))
+            self.tables.append((oco.DeviceBuffer.from_array(ids), oco.DeviceBuffer.from_array(probs)))
+        self.distinct = float(np.mean(distinct))
+        self.x = [oco.DeviceBuffer.from_array(synth.activations(200 + i, self.tokens * h)) for i in range(4)]
+        self.out = oco.DeviceBuffer.from_array(np.zeros(self.tokens * h, np.uint16))
+        self.ws = oco.DeviceBuffer(banks[0].workspace_bytes(self.tokens))
+        self.expert_bytes = 3 * f * (h // 32) * 17
+
+    @staticmethod
+    def _banks(oco, E, h, f, k):
+        from oco_amd import synth
+        banks = []
+        for c in range(2):
+            g = synth.weights(39, E * f, h, 100 + 3 * c)
+            u = synth.weights(39, E * f, h, 101 + 3 * c)
+            d = synth.weights(39, E * h, f, 102 + 3 * c)
+            rng = np.random.default_rng(c)
+            bias = [oco.DeviceBuffer.from_array((rng.normal(size=E * n) * 0.1).astype(np.float32))
+                    for n in (f, f, h)]
+            bufs = [oco.DeviceBuffer.from_array(a) for a in (g, u, d)]
+            banks.append(oco.ExpertBank(39, h, f, E, k, *bufs, *bias))
+            del g, u, d
+        return banks
+
+    def launch(self, i):
+        ids, probs = self.tables[i % 64]
+        self.banks[i % 2].apply(self.x[i % 4], self.oco.DType.F32, ids, probs, self.tokens, self.out,
+                                workspace=self.ws, stream=self.stream)
+
+    def work_per_step(self):
+        return self.distinct * self.expert_bytes
+
+
+_BANKS = {}
+
+
+def _select(logits, k):
+    """Top-k with softmax over the selected (host-side routing tables for the bench)."""
+    import numpy as np
+    order = np.argsort(-logits, axis=1, kind="stable")[:, :k]
+    chosen = np.take_along_axis(logits, order, axis=1)
+    p = np.exp(chosen - chosen[:, :1])
+    return order.astype(np.uint32), (p / p.sum(axis=1, keepdims=True)).astype(np.float32)
+
+
+class Prefill(Workload):
+    """Dense prefill Y = X W^T on MFMA: weight [n x k] GGUF, `m` bf16 tokens."""
+    bound = "mfma"
+    unit = "TFLOP/s"
+
+    def __init__(self, name, fmt, n, k, m):
+        self.name, self.fmt, self.n, self.k, self.m = name, fmt, n, k, m
+
+    def setup(self, oco, stream):
+        from oco_amd import synth
+        self.oco, self.stream = oco, stream
+        w = synth.weights(self.fmt, self.n, self.k, 7)
+        self.bytes = w.nbytes
+        self.copies = max(1, math.ceil(ROTATE_BYTES / self.bytes))
+        self.w = oco.DeviceBuffer(self.bytes * self.copies)
+        for c in range(self.copies):
+            self.w.upload(w, c * self.bytes)
+        self.x = oco.DeviceBuffer.from_array(synth.bf16_bits(synth.activations(8, self.m * self.k)))
+        self.y = oco.DeviceBuffer(self.m * self.n * 4)
+        self.p = oco.Matrix(self.k, self.n, self.m, 0, 1, 1, 0)
+
+    def launch(self, i):
+        self.oco.matmul(self.fmt, self.w.ptr + (i % self.copies) * self.bytes, self.x, self.y, self.p,
+                        stream=self.stream)
+
+    def work_per_step(self):
+        return 2.0 * self.m * self.n * self.k
+
+
 WORKLOADS = {
     "mxfp4_decode_matvec_5760x2880": lambda: Matvec("mxfp4_decode_matvec_5760x2880", 39, 5760, 2880),
     "q8_0_matvec_4096x4096": lambda: Matvec("q8_0_matvec_4096x4096", 8, 4096, 4096),
@@ -120,7 +221,12 @@ WORKLOADS = {
     "q6_k_matvec_4096x12288": lambda: Matvec("q6_k_matvec_4096x12288", 14, 4096, 12288),
     "q6_k_lm_head_151936x4096": lambda: Matvec("q6_k_lm_head_151936x4096", 14, 151936, 4096),
     "qwen3_8b_q4km_decode_stack": MatvecStack,
+    "moe_decode_gpt_oss_b1": lambda: MoeDecode(1),
+    "moe_decode_gpt_oss_b4": lambda: MoeDecode(4),
+    "moe_decode_gpt_oss_b16": lambda: MoeDecode(16),
+    "prefill_mxfp4_5760x2880_m512": lambda: Prefill("prefill_mxfp4_5760x2880_m512", 39, 5760, 2880, 512),
 }
+PEAK_TFLOPS = {"bf16": 2500.0, "fp4": 10100.0}
 HEADLINE = "mxfp4_decode_matvec_5760x2880"
 
 
@@ -142,7 +248,7 @@ def time_workload(oco, wl: Workload, steps: int, warmup: int):
     oco.synchronize()
     per_step_s = ms / 1e3 / steps
     work = wl.work_per_step()
-    achieved = work / per_step_s / 1e9
+    achieved = work / per_step_s / (1e12 if wl.unit == "TFLOP/s" else 1e9)
     return {"ms_per_step": ms / steps, "achieved": achieved, "work": work}
 
 
@@ -226,17 +332,23 @@ def main():
     if not args.no_extra:
         extra = []
         for name in ["q8_0_matvec_4096x4096", "q4_k_matvec_12288x4096", "q6_k_matvec_4096x12288",
-                     "q6_k_lm_head_151936x4096", "qwen3_8b_q4km_decode_stack"]:
+                     "q6_k_lm_head_151936x4096", "qwen3_8b_q4km_decode_stack", "moe_decode_gpt_oss_b1",
+                     "moe_decode_gpt_oss_b4", "moe_decode_gpt_oss_b16", "prefill_mxfp4_5760x2880_m512"]:
             if name == wl.name:
                 continue
             w2 = WORKLOADS[name]()
             steps = max(20, min(args.steps, 200))
             log(f"timing {name}: {steps} steps")
             r2 = time_workload(oco, w2, steps, min(args.warmup, 10))
-            extra.append({"workload": name, "value": round(r2["achieved"], 2), "unit": "GB/s",
-                          "ms_per_step": round(r2["ms_per_step"], 6),
-                          "frac": round(r2["achieved"] / HBM_PEAK_GBS, 4),
-                          "work_bytes": int(r2["work"])})
+            entry = {"workload": name, "value": round(r2["achieved"], 2), "unit": w2.unit,
+                     "ms_per_step": round(r2["ms_per_step"], 6)}
+            if w2.unit == "GB/s":
+                entry.update(frac=round(r2["achieved"] / HBM_PEAK_GBS, 4), work_bytes=int(r2["work"]))
+            else:
+                entry.update(frac_bf16_mfma=round(r2["achieved"] / PEAK_TFLOPS["bf16"], 4),
+                             frac_fp4_mfma=round(r2["achieved"] / PEAK_TFLOPS["fp4"], 4),
+                             work_flops=int(r2["work"]))
+            extra.append(entry)
             del w2
         out["extra"] = extra
     if not args.no_cpu:
