@@ -296,6 +296,8 @@ def main():
     ap.add_argument("--workload", default=HEADLINE, choices=sorted(WORKLOADS))
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run 10 device copies of 256 MiB (counter calibration for traffic)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build runs its kernels on a single MI355X "
@@ -305,6 +307,15 @@ def main():
     import oco_amd as oco
     cus = oco.open_device(0)
     log(f"device 0: {cus} CUs")
+    if args.calibrate_copy:
+        n = 256 * 2 ** 20
+        src, dst = oco.DeviceBuffer(n), oco.DeviceBuffer(n)
+        src.fill32(0x01020304)
+        for _ in range(10):
+            oco.load_library().oco_buffer_copy(dst.ptr, src.ptr, n, None)
+        oco.synchronize()
+        print(json.dumps({"calibrate_copy_bytes": n, "copies": 10}))
+        return
 
     wl = WORKLOADS[args.workload]()
     log(f"timing {wl.name}: {args.steps} steps after {args.warmup} warmup")
