@@ -322,10 +322,12 @@ def main():
     r = time_workload(oco, wl, args.steps, args.warmup)
     value = r["achieved"]
     traffic = load_traffic(wl.name)
+    is_flops = wl.unit == "TFLOP/s"
     out = {
-        "metric": "weight GB/s (% of HBM peak) for decode matvec",
+        "metric": ("prefill TFLOP/s (% MFMA)" if is_flops
+                   else "weight GB/s (% of HBM peak) for decode matvec"),
         "value": round(value, 2),
-        "unit": "GB/s",
+        "unit": wl.unit,
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
@@ -333,12 +335,16 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "bf16 MFMA, f32 accumulation" if is_flops else "f32",
         "data": "synthetic (seeded GGUF-layout weights, N(0,1) activations)",
-        "config": {"workload": wl.name, "format": "MXFP4", "n": 5760, "k": 2880, "batch": 1,
-                   "weight_bytes": int(r["work"]), "rotated_copies": getattr(wl, "copies", 1)},
-        "roofline": {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(value / HBM_PEAK_GBS, 4), "traffic": traffic},
+        "config": {"workload": wl.name, "format": getattr(wl, "fmt", None), "n": getattr(wl, "n", None),
+                   "k": getattr(wl, "k", None), "batch": getattr(wl, "m", getattr(wl, "tokens", 1)),
+                   ("flops" if is_flops else "weight_bytes"): int(r["work"]),
+                   "rotated_copies": getattr(wl, "copies", 1)},
+        "roofline": {"bound": wl.bound, "achieved": round(value, 2),
+                     "peak": PEAK_TFLOPS["bf16"] if is_flops else HBM_PEAK_GBS, "unit": wl.unit,
+                     "frac": round(value / (PEAK_TFLOPS["bf16"] if is_flops else HBM_PEAK_GBS), 4),
+                     "traffic": traffic},
     }
     if not args.no_extra:
         extra = []

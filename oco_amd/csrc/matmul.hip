@@ -10,9 +10,10 @@
 // (tile.metal:16-80) -- and the activations convert to f16, on
 // v_mfma_f32_16x16x32_f16.  Accumulation is fp32.
 //
-// Tile: a 256-thread workgroup computes 64 activation rows x 64 weight rows;
-// each wavefront owns a 32 x 32 quadrant as 2 x 2 MFMA blocks.  K advances
-// 32 at a time (one Q8_0/MXFP4 block, an eighth of a K-quant super-block).
+// Tile: a 256-thread workgroup computes 128 activation rows x 64 weight rows
+// with K steps of 128 (see matmul_kernel).
+#include <stdlib.h>
+
 #include "formats.h"
 
 namespace oco {
@@ -53,94 +54,299 @@ struct BlockShape {
                                    : FMT == OCO_Q4_K ? 144 : FMT == OCO_Q5_K ? 176 : FMT == OCO_Q6_K ? 210 : 17;
 };
 
+__device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) { return (uint32_t)lo | ((uint32_t)hi << 16); }
+
+// One thread's share of a weight tile step: a 32-coefficient piece of one
+// row, decoded to MFMA operand bits as four runs of eight consecutive
+// columns.  `col0[r]` receives each run's first column within the 128-wide
+// K step; out[4r .. 4r+3] its eight 16-bit operands.  Loading (global reads
+// of the piece's bytes) and decoding are separate so the loads of later
+// steps can be in flight while the current step is decoded.
+//   32-blocks (Q8_0, MXFP4, Q4_0, Q4_1, BF16, F16, F32): piece c = block c of
+//     the step, runs at 32c + 8r.
+//   K-quants: the step is half a super-block; piece c is the lane
+//     decomposition of the streaming decoder (piece c + 4 * half).
 template <int FMT, bool BF>
-__global__ __launch_bounds__(256) void matmul_kernel(MatmulArgs a) {
-    constexpr int BM = 64, BN = 64, BK = 32, LD = BK + 8;  // LDS row stride in 16-bit words (80 bytes)
-    __shared__ __attribute__((aligned(16))) uint16_t xs[BM * LD];
-    __shared__ __attribute__((aligned(16))) uint16_t ws[BN * LD];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const uint32_t m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-    const int tm = (wave >> 1) * 32, tn = (wave & 1) * 32;
-    const int srow = tid >> 2, schunk = (tid & 3) * 8;  // staging: 64 rows x 4 chunks of 8
-
-    f32x4 acc[2][2];
-#pragma unroll
-    for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    const uint32_t xrow = m0 + srow, wrow = n0 + srow;
-    const uint8_t *wr = a.w + (uint64_t)min(wrow, a.n - 1) * a.row_bytes;
-    for (uint32_t k0 = 0; k0 < a.k; k0 += BK) {
-        // Activations: 8 consecutive values of one row per thread.
-        uint16_t xv[8];
-        if (xrow < a.m) {
-            uint4 raw = *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(a.x) +
-                                                         (uint64_t)xrow * a.k + k0 + schunk);
-            const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                uint16_t lo = (uint16_t)(w4[i] & 0xffffu), hi = (uint16_t)(w4[i] >> 16);
-                if (!BF && !a.x_f16) {  // bf16 -> f16
-                    lo = operand_bits<false>(bf16_bits_to_f32(lo));
-                    hi = operand_bits<false>(bf16_bits_to_f32(hi));
-                }
-                xv[2 * i] = lo;
-                xv[2 * i + 1] = hi;
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; i++) xv[i] = 0;
+struct PrefillPiece {
+    static constexpr uint32_t BE = BlockShape<FMT>::BE, BB = BlockShape<FMT>::BB;
+    struct Raw {
+        uint32_t w[FMT == OCO_Q4_K || FMT == OCO_Q6_K ? 8 : FMT == OCO_MXFP4 ? 5 : 1];
+        const uint8_t *row;
+    };
+    __device__ __forceinline__ static Raw load(const uint8_t *row, uint32_t k0, int c) {
+        Raw r;
+        r.row = row;
+        if constexpr (FMT == OCO_MXFP4 && BF) {
+            const uint8_t *b = row + (uint64_t)(k0 / 32 + c) * BB;
+            const uint4 q = ld_u128(b + 1);
+            r.w[0] = q.x; r.w[1] = q.y; r.w[2] = q.z; r.w[3] = q.w;
+            r.w[4] = ld_u8(b);
+        } else if constexpr (FMT == OCO_Q4_K) {
+            const uint32_t cc = (k0 % 256) / 128 * 4 + c;
+            const uint8_t *b = row + (uint64_t)(k0 / 256) * BB;
+            const uint4 hdr = ld_u128(b), qs = ld_u128(b + 16 + 16 * cc);
+            r.w[0] = hdr.x; r.w[1] = hdr.y; r.w[2] = hdr.z; r.w[3] = hdr.w;
+            r.w[4] = qs.x; r.w[5] = qs.y; r.w[6] = qs.z; r.w[7] = qs.w;
+        } else if constexpr (FMT == OCO_Q6_K) {
+            const uint32_t hb = (k0 % 256) / 128, l0 = 8 * c;
+            const uint8_t *b = row + (uint64_t)(k0 / 256) * BB;
+            const uint2 ql0 = ld_u64(b + hb * 64 + l0), ql1 = ld_u64(b + hb * 64 + 32 + l0),
+                        qh = ld_u64(b + 128 + hb * 32 + l0);
+            r.w[0] = ql0.x; r.w[1] = ql0.y; r.w[2] = ql1.x; r.w[3] = ql1.y; r.w[4] = qh.x; r.w[5] = qh.y;
+            // four quarter scales (bytes 0, 2, 4, 6 of this 8-byte window) and d
+            const uint2 scw = ld_u64(b + 192 + hb * 8 + (l0 >> 4));
+            r.w[6] = (scw.x & 0xffu) | ((scw.x >> 8) & 0xff00u) | ((scw.y << 16) & 0xff0000u) | ((scw.y << 8) & 0xff000000u);
+            r.w[7] = ld_u16(b + 208);
         }
-        // Weights: decode 8 coefficients of one row.
-        uint16_t wv[8];
-        {
-            constexpr uint32_t BE = BlockShape<FMT>::BE, BB = BlockShape<FMT>::BB;
+        return r;
+    }
+    __device__ __forceinline__ static void decode(const Raw &r, uint32_t k0, int c, uint32_t *out, uint32_t *col0) {
+        if constexpr (FMT == OCO_MXFP4 && BF) {
+            const float scale = e8m0_scale(r.w[4]);
+            uint32_t pk[16];  // byte i -> (column i, column 16 + i)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+                bf16x2 v0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(r.w[j], scale, 0);
+                bf16x2 v1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(r.w[j], scale, 1);
+                bf16x2 v2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(r.w[j], scale, 2);
+                bf16x2 v3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(r.w[j], scale, 3);
+                __builtin_memcpy(&pk[4 * j], &v0, 4);
+                __builtin_memcpy(&pk[4 * j + 1], &v1, 4);
+                __builtin_memcpy(&pk[4 * j + 2], &v2, 4);
+                __builtin_memcpy(&pk[4 * j + 3], &v3, 4);
+            }
 #pragma unroll
             for (int i = 0; i < 8; i++) {
-                const uint32_t col = k0 + schunk + i;
-                wv[i] = operand_bits<BF>(decode_scalar(FMT, wr + (uint64_t)(col / BE) * BB, col % BE));
+                out[i] = __builtin_amdgcn_perm(pk[2 * i + 1], pk[2 * i], 0x05040100u);      // columns 2i, 2i+1
+                out[8 + i] = __builtin_amdgcn_perm(pk[2 * i + 1], pk[2 * i], 0x07060302u);  // columns 16+2i, 17+2i
             }
-        }
-        __syncthreads();  // previous step's fragments are consumed
-        *reinterpret_cast<uint4 *>(&xs[srow * LD + schunk]) =
-            make_uint4(xv[0] | (uint32_t)xv[1] << 16, xv[2] | (uint32_t)xv[3] << 16, xv[4] | (uint32_t)xv[5] << 16,
-                       xv[6] | (uint32_t)xv[7] << 16);
-        *reinterpret_cast<uint4 *>(&ws[srow * LD + schunk]) =
-            make_uint4(wv[0] | (uint32_t)wv[1] << 16, wv[2] | (uint32_t)wv[3] << 16, wv[4] | (uint32_t)wv[5] << 16,
-                       wv[6] | (uint32_t)wv[7] << 16);
-        __syncthreads();
-        // Fragments: lane l holds row/column l % 16, k = 8 (l / 16) .. + 8.
-        const int fr = lane & 15, fk = (lane >> 4) * 8;
-        uint4 af[2], bfm[2];
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-            af[i] = *reinterpret_cast<const uint4 *>(&xs[(tm + i * 16 + fr) * LD + fk]);
-            bfm[i] = *reinterpret_cast<const uint4 *>(&ws[(tn + i * 16 + fr) * LD + fk]);
-        }
+            for (int q = 0; q < 4; q++) col0[q] = 32 * c + 8 * q;
+        } else if constexpr (FMT == OCO_Q4_K) {
+            const uint32_t cc = (k0 % 256) / 128 * 4 + c, g = cc >> 1, odd = cc & 1;
+            uint8_t sb[12];
 #pragma unroll
-        for (int i = 0; i < 2; i++)
+            for (int i = 0; i < 4; i++) {
+                sb[i] = (uint8_t)byte_of(r.w[1], i);
+                sb[4 + i] = (uint8_t)byte_of(r.w[2], i);
+                sb[8 + i] = (uint8_t)byte_of(r.w[3], i);
+            }
+            uint32_t sc0, mn0, sc1, mn1;
+            kquant_scale_min(sb, 2 * g, sc0, mn0);
+            kquant_scale_min(sb, 2 * g + 1, sc1, mn1);
+            const float d = half_bits_to_f32(r.w[0] & 0xffffu), dmin = half_bits_to_f32(r.w[0] >> 16);
+            const float a0 = d * (float)sc0, m0 = dmin * (float)mn0, a1 = d * (float)sc1, m1 = dmin * (float)mn1;
 #pragma unroll
-            for (int j = 0; j < 2; j++) {
-                if constexpr (BF) {
-                    bf16x8 av, bv;
-                    __builtin_memcpy(&av, &af[i], 16);
-                    __builtin_memcpy(&bv, &bfm[j], 16);
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, acc[i][j], 0, 0, 0);
-                } else {
-                    f16x8 av, bv;
-                    __builtin_memcpy(&av, &af[i], 16);
-                    __builtin_memcpy(&bv, &bfm[j], 16);
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc[i][j], 0, 0, 0);
+            for (int j = 0; j < 4; j++) {
+                uint16_t lo[4], hi[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const uint32_t byte = byte_of(r.w[4 + j], i);
+                    lo[i] = operand_bits<BF>(__fsub_rn(__fmul_rn(a0, (float)(byte & 15u)), m0));
+                    hi[i] = operand_bits<BF>(__fsub_rn(__fmul_rn(a1, (float)(byte >> 4)), m1));
                 }
+                out[2 * j] = pack2(lo[0], lo[1]);
+                out[2 * j + 1] = pack2(lo[2], lo[3]);
+                out[8 + 2 * j] = pack2(hi[0], hi[1]);
+                out[8 + 2 * j + 1] = pack2(hi[2], hi[3]);
             }
+            const uint32_t base = 64 * g + 16 * odd - (k0 % 256) / 128 * 128;
+            col0[0] = base;
+            col0[1] = base + 8;
+            col0[2] = base + 32;
+            col0[3] = base + 40;
+        } else if constexpr (FMT == OCO_Q6_K) {
+            const uint32_t l0 = 8 * c;
+            const float d = half_bits_to_f32(r.w[7]);
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const uint32_t lw0 = (q & 1) ? r.w[2] : r.w[0], lw1 = (q & 1) ? r.w[3] : r.w[1];
+                const int shift = (q >> 1) * 4;
+                const float sc = d * (float)(int8_t)byte_of(r.w[6], q);
+                uint16_t v[8];
+#pragma unroll
+                for (int half = 0; half < 2; half++) {
+                    const uint32_t lw = half ? lw1 : lw0, hw = half ? r.w[5] : r.w[4];
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int code =
+                            (int)(((lw >> (8 * i + shift)) & 15u) | (((hw >> (8 * i + 2 * q)) & 3u) << 4)) - 32;
+                        v[4 * half + i] = operand_bits<BF>(__fmul_rn(sc, (float)code));
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < 4; i++) out[4 * q + i] = pack2(v[2 * i], v[2 * i + 1]);
+                col0[q] = 32 * q + l0;
+            }
+        } else {
+            // Generic: decode each coefficient of the 32 columns 32c .. 32c+31.
+            const uint32_t kbase = k0 + 32 * c;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const uint32_t col = kbase + 2 * i;
+                uint16_t v0 = operand_bits<BF>(decode_scalar(FMT, r.row + (uint64_t)(col / BE) * BB, col % BE));
+                uint16_t v1 =
+                    operand_bits<BF>(decode_scalar(FMT, r.row + (uint64_t)((col + 1) / BE) * BB, (col + 1) % BE));
+                out[i] = pack2(v0, v1);
+            }
+#pragma unroll
+            for (int q = 0; q < 4; q++) col0[q] = 32 * c + 8 * q;
+        }
+    }
+};
+
+// Tile BM activation rows x BN weight rows, K step 128.  Four wavefronts in
+// a 2 x 2 grid, each (BM/2) x (BN/2) as blocks of v_mfma_f32_16x16x32.
+// Two LDS buffers: while the MFMAs of step s read buffer s % 2, the same
+// wavefronts decode step s+1 (loaded into registers a step earlier) into the
+// other buffer, and the loads for step s+2 are in flight; one barrier per
+// step.  Weight piece p = tid + 256 u goes to row p % BN, piece p / BN, so a
+// wavefront's 64 lanes write 64 different rows (conflict-free LDS stores).
+template <int FMT, bool BF, int BM, int BN>
+struct Stage {
+    static constexpr int XPT = BM * 16 / 256, WPT = BN * 4 / 256;
+    uint4 x[XPT];
+    typename PrefillPiece<FMT, BF>::Raw w[WPT];
+};
+
+template <int FMT, bool BF, int BM, int BN>
+__global__ __launch_bounds__(256) void matmul_kernel(MatmulArgs a) {
+    using PP = PrefillPiece<FMT, BF>;
+    using ST = Stage<FMT, BF, BM, BN>;
+    constexpr int BK = 128, LD = BK + 8;  // LDS row stride: 136 halves (272 bytes, conflict-free fragments)
+    constexpr int MI = BM / 32, NJ = BN / 32, XPT = ST::XPT, WPT = ST::WPT;
+    constexpr int XS = BM * LD, WS = BN * LD;
+    extern __shared__ __attribute__((aligned(16))) uint16_t lds[];  // [2][XS] then [2][WS]
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const uint32_t m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int tm = (wave >> 1) * (BM / 2), tn = (wave & 1) * (BN / 2);
+
+    f32x4 acc[MI][NJ];
+#pragma unroll
+    for (int i = 0; i < MI; i++)
+#pragma unroll
+        for (int j = 0; j < NJ; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const uint16_t *xg = reinterpret_cast<const uint16_t *>(a.x);
+    const uint8_t *wr[WPT];
+    int wrow[WPT], wpc[WPT];
+#pragma unroll
+    for (int u = 0; u < WPT; u++) {
+        const int p = tid + 256 * u;
+        wrow[u] = p % BN;
+        wpc[u] = p / BN;
+        wr[u] = a.w + (uint64_t)min(n0 + wrow[u], a.n - 1) * a.row_bytes;
+    }
+
+    auto load = [&](ST &st, uint32_t k0) {
+#pragma unroll
+        for (int i = 0; i < XPT; i++) {
+            const int chunk = tid + 256 * i, r = chunk >> 4, cc = (chunk & 15) * 8;
+            const uint32_t row = m0 + r;
+            st.x[i] = row < a.m && k0 + cc < a.k
+                          ? *reinterpret_cast<const uint4 *>(xg + (uint64_t)row * a.k + k0 + cc)
+                          : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < WPT; u++)  // 32-block formats: the last step may cover a partial 128
+            if (k0 + 32 * wpc[u] < a.k) st.w[u] = PP::load(wr[u], k0, wpc[u]);
+    };
+    auto store = [&](const ST &st, uint32_t k0, int buf) {
+        uint16_t *xs = lds + buf * XS;
+        uint16_t *ws = lds + 2 * XS + buf * WS;
+#pragma unroll
+        for (int i = 0; i < XPT; i++) {
+            const int chunk = tid + 256 * i, r = chunk >> 4, cc = (chunk & 15) * 8;
+            uint4 v = st.x[i];
+            if (!BF && !a.x_f16) {  // bf16 activations -> f16 operands
+                uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    w4[j] = pack2(operand_bits<false>(bf16_bits_to_f32(w4[j] & 0xffffu)),
+                                  operand_bits<false>(bf16_bits_to_f32(w4[j] >> 16)));
+                v = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+            }
+            *reinterpret_cast<uint4 *>(&xs[r * LD + cc]) = v;
+        }
+#pragma unroll
+        for (int u = 0; u < WPT; u++) {
+            uint32_t out[16], col0[4];
+            if (k0 + 32 * wpc[u] < a.k) {
+                PP::decode(st.w[u], k0, wpc[u], out, col0);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 16; i++) out[i] = 0;
+#pragma unroll
+                for (int q = 0; q < 4; q++) col0[q] = 32 * wpc[u] + 8 * q;
+            }
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                *reinterpret_cast<uint4 *>(&ws[wrow[u] * LD + col0[q]]) =
+                    make_uint4(out[4 * q], out[4 * q + 1], out[4 * q + 2], out[4 * q + 3]);
+        }
+    };
+    auto mfma_step = [&](int buf) {
+        const uint16_t *xs = lds + buf * XS;
+        const uint16_t *ws = lds + 2 * XS + buf * WS;
+        const int fr = lane & 15, fk = (lane >> 4) * 8;
+#pragma unroll
+        for (int kk = 0; kk < BK; kk += 32) {
+            uint4 af[MI], bfm[NJ];
+#pragma unroll
+            for (int i = 0; i < MI; i++) af[i] = *reinterpret_cast<const uint4 *>(&xs[(tm + i * 16 + fr) * LD + kk + fk]);
+#pragma unroll
+            for (int j = 0; j < NJ; j++) bfm[j] = *reinterpret_cast<const uint4 *>(&ws[(tn + j * 16 + fr) * LD + kk + fk]);
+#pragma unroll
+            for (int i = 0; i < MI; i++)
+#pragma unroll
+                for (int j = 0; j < NJ; j++) {
+                    if constexpr (BF) {
+                        bf16x8 av, bv;
+                        __builtin_memcpy(&av, &af[i], 16);
+                        __builtin_memcpy(&bv, &bfm[j], 16);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, acc[i][j], 0, 0, 0);
+                    } else {
+                        f16x8 av, bv;
+                        __builtin_memcpy(&av, &af[i], 16);
+                        __builtin_memcpy(&bv, &bfm[j], 16);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc[i][j], 0, 0, 0);
+                    }
+                }
+        }
+    };
+
+    // Prologue: step 0 in LDS buffer 0, step 1 in registers (s1), step 2 loading (s0).
+    ST s0, s1;
+    load(s0, 0);
+    if (BK < a.k) load(s1, BK);
+    store(s0, 0, 0);
+    if (2 * BK < a.k) load(s0, 2 * BK);
+    __syncthreads();
+    const uint32_t steps = (a.k + BK - 1) / BK;
+    for (uint32_t s = 0; s < steps; s += 2) {
+        // even step s: compute buffer 0, stage step s+1 (s1) into buffer 1, prefetch s+3 into s1
+        mfma_step(0);
+        if (s + 1 < steps) {
+            store(s1, (s + 1) * BK, 1);
+            if (s + 3 < steps) load(s1, (s + 3) * BK);
+        }
+        __syncthreads();
+        if (s + 1 >= steps) break;
+        // odd step s+1: compute buffer 1, stage step s+2 (s0) into buffer 0, prefetch s+4 into s0
+        mfma_step(1);
+        if (s + 2 < steps) {
+            store(s0, (s + 2) * BK, 0);
+            if (s + 4 < steps) load(s0, (s + 4) * BK);
+        }
+        __syncthreads();
     }
     // C fragment: lane l holds column l % 16, rows 4 (l / 16) .. + 4.
     const int cc = lane & 15, cr = (lane >> 4) * 4;
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < MI; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
+        for (int j = 0; j < NJ; j++) {
             const uint32_t col = n0 + tn + j * 16 + cc;
             if (col >= a.n) continue;
             const float b = a.bias ? round_bf16(a.bias[col]) : 0.f;
@@ -160,20 +366,36 @@ __global__ __launch_bounds__(256) void matmul_kernel(MatmulArgs a) {
 
 typedef void (*MatmulFn)(MatmulArgs);
 
-static MatmulFn matmul_pick(uint32_t fmt) {
+template <int BM, int BN>
+static MatmulFn matmul_pick_tile(uint32_t fmt) {
     switch (fmt) {
-    case OCO_MXFP4: return matmul_kernel<OCO_MXFP4, true>;
-    case OCO_BF16: return matmul_kernel<OCO_BF16, true>;
-    case OCO_Q8_0: return matmul_kernel<OCO_Q8_0, false>;
-    case OCO_Q4_K: return matmul_kernel<OCO_Q4_K, false>;
-    case OCO_Q5_K: return matmul_kernel<OCO_Q5_K, false>;
-    case OCO_Q6_K: return matmul_kernel<OCO_Q6_K, false>;
-    case OCO_Q4_0: return matmul_kernel<OCO_Q4_0, false>;
-    case OCO_Q4_1: return matmul_kernel<OCO_Q4_1, false>;
-    case OCO_F16: return matmul_kernel<OCO_F16, false>;
-    case OCO_F32: return matmul_kernel<OCO_F32, false>;
+    case OCO_MXFP4: return matmul_kernel<OCO_MXFP4, true, BM, BN>;
+    case OCO_BF16: return matmul_kernel<OCO_BF16, true, BM, BN>;
+    case OCO_Q8_0: return matmul_kernel<OCO_Q8_0, false, BM, BN>;
+    case OCO_Q4_K: return matmul_kernel<OCO_Q4_K, false, BM, BN>;
+    case OCO_Q5_K: return matmul_kernel<OCO_Q5_K, false, BM, BN>;
+    case OCO_Q6_K: return matmul_kernel<OCO_Q6_K, false, BM, BN>;
+    case OCO_Q4_0: return matmul_kernel<OCO_Q4_0, false, BM, BN>;
+    case OCO_Q4_1: return matmul_kernel<OCO_Q4_1, false, BM, BN>;
+    case OCO_F16: return matmul_kernel<OCO_F16, false, BM, BN>;
+    case OCO_F32: return matmul_kernel<OCO_F32, false, BM, BN>;
     }
     return nullptr;
+}
+
+// Tile choice (the prefill half of Builder::dense, pipelines.rs:267-355):
+// the largest tile that still gives every CU work.
+static MatmulFn matmul_pick(uint32_t fmt, uint32_t m, uint32_t n, int &bm, int &bn) {
+    int choice = -1;
+    if (const char *env = getenv("OCO_MATMUL_TILE")) choice = atoi(env);  // tuning runs only
+    auto tiles = [&](int tm, int tn) { return (uint64_t)((m + tm - 1) / tm) * ((n + tn - 1) / tn); };
+    if (choice < 0) choice = tiles(128, 128) >= 160 ? 3 : 1;  // measured: 128x128 once it fills the chip
+    switch (choice) {
+    case 3: bm = 128; bn = 128; return matmul_pick_tile<128, 128>(fmt);
+    case 2: bm = 128; bn = 64; return matmul_pick_tile<128, 64>(fmt);
+    case 1: bm = 64; bn = 64; return matmul_pick_tile<64, 64>(fmt);
+    default: bm = 64; bn = 128; return matmul_pick_tile<64, 128>(fmt);
+    }
 }
 
 }  // namespace oco
@@ -196,7 +418,8 @@ extern "C" int oco_matmul(uint32_t format, const void *w, const void *x, oco_dty
         return fail(OCO_ERR_UNSUPPORTED, "oco_matmul: MXFP4/BF16 weights take bf16 activations");
     if (y_dtype != OCO_DT_F32 && y_dtype != OCO_DT_BF16)
         return fail(OCO_ERR_UNSUPPORTED, "oco_matmul: output must be f32 or bf16");
-    MatmulFn fn = matmul_pick(format);
+    int bm = 128, bn = 64;
+    MatmulFn fn = matmul_pick(format, p->m, p->n, bm, bn);
     if (!fn) return fail(OCO_ERR_UNSUPPORTED, "oco_matmul: format %u", format);
     MatmulArgs a;
     a.w = (const uint8_t *)w;
@@ -209,7 +432,11 @@ extern "C" int oco_matmul(uint32_t format, const void *w, const void *x, oco_dty
     a.row_bytes = oco_row_bytes(format, p->k);
     a.x_f16 = x_dtype == OCO_DT_F16;
     a.y_bf16 = y_dtype == OCO_DT_BF16;
-    dim3 grid((p->n + 63) / 64, (p->m + 63) / 64);
-    hipLaunchKernelGGL(fn, grid, dim3(256), 0, (hipStream_t)stream, a);
+    dim3 grid((p->n + bn - 1) / bn, (p->m + bm - 1) / bm);
+    const size_t lds = (size_t)2 * (bm + bn) * (128 + 8) * 2;
+    if (lds > 64 * 1024)
+        OCO_TRY(hip_check(hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+                          "hipFuncSetAttribute"));
+    hipLaunchKernelGGL(fn, grid, dim3(256), lds, (hipStream_t)stream, a);
     return launch_check("oco_matmul");
 }
