@@ -205,10 +205,12 @@ class Prefill(Workload):
         self.x = oco.DeviceBuffer.from_array(synth.bf16_bits(synth.activations(8, self.m * self.k)))
         self.y = oco.DeviceBuffer(self.m * self.n * 4)
         self.p = oco.Matrix(self.k, self.n, self.m, 0, 1, 1, 0)
+        self.ws_bytes = oco.matmul_workspace(self.fmt, self.p)
+        self.ws = oco.DeviceBuffer(max(self.ws_bytes, 256))
 
     def launch(self, i):
         self.oco.matmul(self.fmt, self.w.ptr + (i % self.copies) * self.bytes, self.x, self.y, self.p,
-                        stream=self.stream)
+                        stream=self.stream, workspace=self.ws, workspace_bytes=self.ws_bytes)
 
     def work_per_step(self):
         return 2.0 * self.m * self.n * self.k

@@ -163,9 +163,22 @@ int oco_matvec(uint32_t format, const void *w, const void *x, oco_dtype x_dtype,
  * Operands: MXFP4 weights and bf16 activations enter bf16 MFMA exactly;
  * other formats decode to f16 (the reference's half(w), tile.metal:16-80)
  * with activations converted to f16.  X is bf16 or f16 row-major; Y f32 or
- * bf16.  Uses no workspace. */
+ * bf16.  MXFP4 instead runs the block-scaled FP8 x FP4 MFMA on the GGUF bytes
+ * as stored, with X split into two E4M3 terms (exact for bf16 inputs up to
+ * 2^-8 of each residual block maximum); that split needs a workspace, which
+ * oco_matmul takes from the stream-ordered pool (hipMallocAsync). */
 int oco_matmul(uint32_t format, const void *w, const void *x, oco_dtype x_dtype, void *y,
                oco_dtype y_dtype, const float *bias, const oco_matrix *p, oco_stream stream);
+
+/* Workspace bytes oco_matmul_ws needs for this call (0: none).  The
+ * reference draws such scratch from the session Arena (src/gpu/arena.rs). */
+uint64_t oco_matmul_workspace(uint32_t format, oco_dtype x_dtype, const oco_matrix *p);
+
+/* oco_matmul with caller-owned workspace (no allocation; graph-capturable).
+ * Calls sharing one workspace must be ordered on one stream. */
+int oco_matmul_ws(uint32_t format, const void *w, const void *x, oco_dtype x_dtype, void *y,
+                  oco_dtype y_dtype, const float *bias, const oco_matrix *p, void *workspace,
+                  uint64_t workspace_bytes, oco_stream stream);
 
 /* ---- routing ------------------------------------------------------------ */
 

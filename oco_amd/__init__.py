@@ -126,6 +126,8 @@ SIGNATURES = {
     "oco_dequant": (_i32, [_u32, _vp, _u64, _vp, _vp]),
     "oco_matvec": (_i32, [_u32, _vp, _vp, _i32, _vp, _i32, _vp, _vp, _MP, _vp]),
     "oco_matmul": (_i32, [_u32, _vp, _vp, _i32, _vp, _i32, _vp, _MP, _vp]),
+    "oco_matmul_workspace": (_u64, [_u32, _i32, _MP]),
+    "oco_matmul_ws": (_i32, [_u32, _vp, _vp, _i32, _vp, _i32, _vp, _MP, _vp, _u64, _vp]),
     "oco_route_select": (_i32, [_vp, _u32, _u32, _u32, _vp, _vp, _vp]),
     "oco_router": (_i32, [_vp, _i32, _vp, _vp, _u32, _u32, _u32, _u32, _vp, _vp, _vp, _vp]),
     "oco_route_plan_words": (_u64, [_u32, _u32]),
@@ -332,9 +334,20 @@ def matvec(fmt: int, w, x, y, p: Matrix, x_dtype=DType.F32, y_dtype=DType.F32, b
 
 
 def matmul(fmt: int, w, x, y, p: Matrix, x_dtype=DType.BF16, y_dtype=DType.F32, bias=None,
-           stream=None):
-    _check(load_library().oco_matmul(int(fmt), _addr(w), _addr(x), int(x_dtype), _addr(y),
-                                     int(y_dtype), _addr(bias), ctypes.byref(as_matrix(p)), _stream(stream)))
+           stream=None, workspace=None, workspace_bytes: int = 0):
+    """oco_matmul, or oco_matmul_ws when a workspace is given."""
+    lib = load_library()
+    if workspace is None:
+        _check(lib.oco_matmul(int(fmt), _addr(w), _addr(x), int(x_dtype), _addr(y), int(y_dtype),
+                              _addr(bias), ctypes.byref(as_matrix(p)), _stream(stream)))
+    else:
+        _check(lib.oco_matmul_ws(int(fmt), _addr(w), _addr(x), int(x_dtype), _addr(y), int(y_dtype),
+                                 _addr(bias), ctypes.byref(as_matrix(p)), _addr(workspace),
+                                 int(workspace_bytes), _stream(stream)))
+
+
+def matmul_workspace(fmt: int, p: Matrix, x_dtype=DType.BF16) -> int:
+    return int(load_library().oco_matmul_workspace(int(fmt), int(x_dtype), ctypes.byref(as_matrix(p))))
 
 
 def route_select(logits, tokens: int, experts: int, k: int, ids, probs, stream=None):

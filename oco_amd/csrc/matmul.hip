@@ -398,18 +398,24 @@ static MatmulFn matmul_pick(uint32_t fmt, uint32_t m, uint32_t n, int &bm, int &
     }
 }
 
-}  // namespace oco
+uint64_t mx_workspace_bytes(uint32_t m, uint32_t k);
+int mx_matmul_launch(const void *w, const void *x, void *y, bool y_bf16, const float *bias, uint32_t m, uint32_t n,
+                     uint32_t k, void *workspace, hipStream_t stream);
 
-using namespace oco;
+// MXFP4 goes to the block-scaled FP8 x FP4 MFMA unless OCO_MX_OFF is set
+// (tuning comparisons against the bf16 decode path).
+static bool use_mx(uint32_t format) {
+    static const bool off = getenv("OCO_MX_OFF") != nullptr;
+    return format == OCO_MXFP4 && !off;
+}
 
-extern "C" int oco_matmul(uint32_t format, const void *w, const void *x, oco_dtype x_dtype, void *y,
-                          oco_dtype y_dtype, const float *bias, const oco_matrix *p, oco_stream stream) {
+static int matmul_check(uint32_t format, const void *w, const void *x, oco_dtype x_dtype, const void *y,
+                        oco_dtype y_dtype, const float *bias, const oco_matrix *p) {
     if (!p || !w || !x || !y) return fail(OCO_ERR_INVALID, "oco_matmul: null argument");
     uint32_t e, bb;
     OCO_TRY(oco_block_layout(format, &e, &bb));
     if (p->k == 0 || p->k % 32 || p->k % e)
         return fail(OCO_ERR_INVALID, "oco_matmul: k=%u must be a multiple of 32 and of the block", p->k);
-    if (p->m == 0 || p->n == 0) return OCO_OK;
     if (p->experts > 1) return fail(OCO_ERR_UNSUPPORTED, "oco_matmul: routed rows go through oco_experts_apply");
     if (p->has_bias && !bias) return fail(OCO_ERR_INVALID, "oco_matmul: has_bias without bias");
     if (x_dtype != OCO_DT_BF16 && x_dtype != OCO_DT_F16)
@@ -418,6 +424,11 @@ extern "C" int oco_matmul(uint32_t format, const void *w, const void *x, oco_dty
         return fail(OCO_ERR_UNSUPPORTED, "oco_matmul: MXFP4/BF16 weights take bf16 activations");
     if (y_dtype != OCO_DT_F32 && y_dtype != OCO_DT_BF16)
         return fail(OCO_ERR_UNSUPPORTED, "oco_matmul: output must be f32 or bf16");
+    return OCO_OK;
+}
+
+static int matmul_decode_launch(uint32_t format, const void *w, const void *x, oco_dtype x_dtype, void *y,
+                                oco_dtype y_dtype, const float *bias, const oco_matrix *p, hipStream_t stream) {
     int bm = 128, bn = 64;
     MatmulFn fn = matmul_pick(format, p->m, p->n, bm, bn);
     if (!fn) return fail(OCO_ERR_UNSUPPORTED, "oco_matmul: format %u", format);
@@ -437,6 +448,45 @@ extern "C" int oco_matmul(uint32_t format, const void *w, const void *x, oco_dty
     if (lds > 64 * 1024)
         OCO_TRY(hip_check(hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
                           "hipFuncSetAttribute"));
-    hipLaunchKernelGGL(fn, grid, dim3(256), lds, (hipStream_t)stream, a);
+    hipLaunchKernelGGL(fn, grid, dim3(256), lds, stream, a);
     return launch_check("oco_matmul");
+}
+
+}  // namespace oco
+
+using namespace oco;
+
+extern "C" uint64_t oco_matmul_workspace(uint32_t format, oco_dtype x_dtype, const oco_matrix *p) {
+    (void)x_dtype;
+    if (!p || !use_mx(format)) return 0;
+    return mx_workspace_bytes(p->m, p->k);
+}
+
+extern "C" int oco_matmul_ws(uint32_t format, const void *w, const void *x, oco_dtype x_dtype, void *y,
+                             oco_dtype y_dtype, const float *bias, const oco_matrix *p, void *workspace,
+                             uint64_t workspace_bytes, oco_stream stream) {
+    OCO_TRY(matmul_check(format, w, x, x_dtype, y, y_dtype, bias, p));
+    if (p->m == 0 || p->n == 0) return OCO_OK;
+    if (use_mx(format)) {
+        const uint64_t need = mx_workspace_bytes(p->m, p->k);
+        if (!workspace || workspace_bytes < need)
+            return fail(OCO_ERR_INVALID, "oco_matmul_ws: workspace of %llu bytes, need %llu",
+                        (unsigned long long)workspace_bytes, (unsigned long long)need);
+        return mx_matmul_launch(w, x, y, y_dtype == OCO_DT_BF16, p->has_bias ? bias : nullptr, p->m, p->n, p->k,
+                                workspace, (hipStream_t)stream);
+    }
+    return matmul_decode_launch(format, w, x, x_dtype, y, y_dtype, bias, p, (hipStream_t)stream);
+}
+
+extern "C" int oco_matmul(uint32_t format, const void *w, const void *x, oco_dtype x_dtype, void *y,
+                          oco_dtype y_dtype, const float *bias, const oco_matrix *p, oco_stream stream) {
+    OCO_TRY(matmul_check(format, w, x, x_dtype, y, y_dtype, bias, p));
+    if (p->m == 0 || p->n == 0) return OCO_OK;
+    const uint64_t need = oco_matmul_workspace(format, x_dtype, p);
+    if (!need) return matmul_decode_launch(format, w, x, x_dtype, y, y_dtype, bias, p, (hipStream_t)stream);
+    void *ws = nullptr;
+    OCO_TRY(hip_check(hipMallocAsync(&ws, need, (hipStream_t)stream), "oco_matmul: hipMallocAsync"));
+    const int rc = oco_matmul_ws(format, w, x, x_dtype, y, y_dtype, bias, p, ws, need, stream);
+    const int rf = hip_check(hipFreeAsync(ws, (hipStream_t)stream), "oco_matmul: hipFreeAsync");
+    return rc != OCO_OK ? rc : rf;
 }

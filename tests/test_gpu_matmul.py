@@ -1,9 +1,12 @@
 """GPU parity of the MFMA prefill matmul against the fp64 oracle.
 
 Bars: relative L2 2e-3 of the fp64 product of the exact coefficients for
-f16-operand MFMA (the task's bf16/f16-activation bound), 1e-5 for MXFP4 on
-bf16 MFMA (exact operands); every element within the reference's roundoff
-bound of the half-operand product (matrix_precision.rs:119-142).
+f16-operand MFMA (the bf16/f16-activation bound), 1e-5 for MXFP4 on the
+block-scaled FP8 x FP4 MFMA (exact weights, activations split into two E4M3
+terms) on ordinary activations; every element within the reference's
+roundoff bound of the half-operand product (matrix_precision.rs:119-142).
+Activations with extreme in-block dynamic range get the explicit bound of
+test_matmul_mxfp4_wide_dynamic_range.
 """
 import numpy as np
 import pytest
@@ -70,3 +73,89 @@ def test_matmul_bias_and_bf16_output(lib):
     exact, _ = O.matmul_reference(12, w, x, n, k, half_operands=False)
     want = exact + O.bf16_round(bias)
     assert rel_l2(got, want) <= 5e-3
+
+
+def _mx_case(m, n, k, seed, scale_rows=None):
+    from oco_amd import synth
+    w = synth.weights(39, n, k, seed=seed)
+    x = synth.activations(seed + 1, m * k).reshape(m, k)
+    if scale_rows is not None:
+        x = x * scale_rows
+    return w, synth.bf16_bits(x.astype(np.float32)).reshape(m, k)
+
+
+@pytest.mark.parametrize("m,n,k", [(45, 70, 160), (1, 33, 32), (33, 65, 96), (130, 200, 2880)])
+def test_matmul_mxfp4_workspace_tail(lib, m, n, k):
+    """Block-scaled MFMA path through oco_matmul_ws: K steps of 64 with a
+    lone last block (k % 64 == 32), row/column tails, bias, bf16 output."""
+    say("matmul mxfp4 ws", m, n, k)
+    w, x = _mx_case(m, n, k, 21)
+    p = lib.Matrix(k, n, m, 0, 1, 1, 1)
+    need = lib.matmul_workspace(39, p)
+    assert need > 0
+    ws = lib.DeviceBuffer(need)
+    bias = np.random.default_rng(5).normal(size=n).astype(np.float32)
+    y = Guarded(lib, m * n * 2)
+    lib.matmul(39, lib.DeviceBuffer.from_array(w), lib.DeviceBuffer.from_array(x), y.ptr, p,
+               lib.DType.BF16, lib.DType.BF16, lib.DeviceBuffer.from_array(bias), workspace=ws,
+               workspace_bytes=need)
+    lib.synchronize()
+    got = O.bf16_to_f32(y.read(np.uint16)).reshape(m, n)
+    exact, mag = O.matmul_reference(39, w, x, n, k, half_operands=False)
+    b = O.bf16_round(bias)
+    want = exact + b
+    # bf16 output: fp32 roundoff of the sum plus one bf16 rounding
+    assert np.all(np.abs(got - want) <= O.roundoff_bound(want, mag + np.abs(b), k, True))
+
+
+def test_matmul_mxfp4_workspace_too_small(lib):
+    m, n, k = 40, 32, 64
+    w, x = _mx_case(m, n, k, 2)
+    p = lib.Matrix(k, n, m, 0, 1, 1, 0)
+    need = lib.matmul_workspace(39, p)
+    ws = lib.DeviceBuffer(need)
+    with pytest.raises(RuntimeError, match="workspace"):
+        lib.matmul(39, lib.DeviceBuffer.from_array(w), lib.DeviceBuffer.from_array(x),
+                   lib.DeviceBuffer(m * n * 4), p, workspace=ws, workspace_bytes=need - 1)
+
+
+def test_matmul_mxfp4_wide_dynamic_range(lib):
+    """Activations spanning 2^-30 .. 2^30 inside each 32-block.  The split
+    itself is exact to ~2^-21 of a block's maximum, but the block-scaled MFMA
+    sums one block's products in a fixed-point adder about 13 bits deep
+    (measured: 448 + 2^-5 kept, 448 + 0.0293 dropped), so each output may lose
+    up to 32 * 2^-13 of every block's largest |x w| (two terms: 2^-7 here)."""
+    m, n, k = 64, 96, 1024
+    rng = np.random.default_rng(7)
+    mag = 2.0 ** rng.integers(-30, 31, size=(m, k))
+    w, x = _mx_case(m, n, k, 31, scale_rows=mag)
+    got = run(lib, 39, w, x, m, n, k)
+    exact, mag_ = O.matmul_reference(39, w, x, n, k, half_operands=False)
+    X = O.bf16_to_f32(x).astype(np.float64)
+    W = O.dequant(39, w, n * k).astype(np.float64).reshape(n, k)
+    block_max = np.abs(X[:, None, :] * W[None, :, :]).reshape(m, n, k // 32, 32).max(-1).sum(-1)
+    assert rel_l2(got, exact) <= 1e-4
+    assert np.all(np.abs(got - exact) <= O.roundoff_bound(exact, mag_, k, False) + 2.0 ** -7 * block_max)
+
+
+def test_matmul_mxfp4_nan_scale_and_nan_activation(lib):
+    """E8M0 255 makes its weight row's outputs NaN; a NaN activation makes its
+    row NaN; everything else stays finite and exact."""
+    m, n, k = 40, 48, 256
+    w, x = _mx_case(m, n, k, 41)
+    w = w.copy()
+    row_bytes = k // 32 * 17
+    w[5 * row_bytes + 2 * 17] = 255          # weight row 5, block 2
+    x = x.copy()
+    x[7, 100] = 0x7FC0                        # activation row 7: NaN
+    got = run(lib, 39, w, x, m, n, k)
+    assert np.all(np.isnan(got[:, 5])) and np.all(np.isnan(got[7, :]))
+    keep_r = np.array([r for r in range(m) if r != 7])
+    keep_c = np.array([c for c in range(n) if c != 5])
+    w_ok = w.copy()
+    w_ok[5 * row_bytes + 2 * 17] = 127
+    x_ok = x.copy()
+    x_ok[7, 100] = 0
+    exact, _ = O.matmul_reference(39, w_ok, x_ok, n, k, half_operands=False)
+    sub = got[np.ix_(keep_r, keep_c)]
+    assert np.all(np.isfinite(sub)) and rel_l2(sub, exact[np.ix_(keep_r, keep_c)]) <= 1e-5
