@@ -173,6 +173,56 @@ class MoeDecode(Workload):
         return self.distinct * self.expert_bytes
 
 
+class MoePrefill(MoeDecode):
+    """Qwen3-30B-A3B expert layer at prefill: 128 experts, gate/up [768 x 2048]
+    and down [2048 x 768] Q4_K, top-8 of softmax(N(0,1) logits) over 512
+    tokens (4096 routes: every expert is hit), SwiGLU, weighted combine.  Two
+    bank copies (2 x 340 MB) rotate past the Infinity Cache.  Work = bytes of
+    the experts hit (HBM-bound: 38.65 GFLOP over 339,738,624 bytes)."""
+
+    def __init__(self, tokens=512):
+        self.tokens = tokens
+        self.name = "moe_prefill_qwen3_30b_a3b"
+
+    def setup(self, oco, stream):
+        import numpy as np
+        from oco_amd import synth
+        self.oco, self.stream = oco, stream
+        E, h, f, k = 128, 2048, 768, 8
+        self.k = k
+        banks = _BANKS.get("qwen3_30b")
+        if banks is None:
+            banks = _BANKS["qwen3_30b"] = []
+            for c in range(2):
+                g = synth.weights(12, E * f, h, 300 + 3 * c)
+                u = synth.weights(12, E * f, h, 301 + 3 * c)
+                d = synth.weights(12, E * h, f, 302 + 3 * c)
+                bufs = [oco.DeviceBuffer.from_array(a) for a in (g, u, d)]
+                banks.append(oco.ExpertBank(12, h, f, E, k, *bufs, activation=oco.Activation.SWIGLU,
+                                            up_bias_one=False))
+                del g, u, d
+        self.banks = banks
+        self.tables = []
+        distinct = []
+        rng = np.random.default_rng(4321)
+        for t in range(8):
+            logits = rng.normal(size=(self.tokens, E)).astype(np.float32)
+            ids, probs = _select(logits, k)
+            distinct.append(len(set(ids.ravel().tolist())))
+            self.tables.append((oco.DeviceBuffer.from_array(ids), oco.DeviceBuffer.from_array(probs)))
+        self.distinct = float(np.mean(distinct))
+        self.x = [oco.DeviceBuffer.from_array(synth.bf16_bits(synth.activations(400 + i, self.tokens * h)))
+                  for i in range(2)]
+        self.out = oco.DeviceBuffer.from_array(np.zeros(self.tokens * h, np.uint16))
+        self.ws = oco.DeviceBuffer(banks[0].workspace_bytes(self.tokens))
+        self.expert_bytes = 3 * f * (h // 256) * 144
+
+    def launch(self, i):
+        ids, probs = self.tables[i % 8]
+        self.banks[i % 2].apply(self.x[i % 2], self.oco.DType.BF16, ids, probs, self.tokens, self.out,
+                                workspace=self.ws, stream=self.stream)
+
+
 _BANKS = {}
 
 
@@ -227,6 +277,7 @@ WORKLOADS = {
     "moe_decode_gpt_oss_b4": lambda: MoeDecode(4),
     "moe_decode_gpt_oss_b16": lambda: MoeDecode(16),
     "prefill_mxfp4_5760x2880_m512": lambda: Prefill("prefill_mxfp4_5760x2880_m512", 39, 5760, 2880, 512),
+    "moe_prefill_qwen3_30b_a3b": MoePrefill,
 }
 PEAK_TFLOPS = {"bf16": 2500.0, "fp4": 10100.0}
 HEADLINE = "mxfp4_decode_matvec_5760x2880"
@@ -352,7 +403,8 @@ def main():
         extra = []
         for name in ["q8_0_matvec_4096x4096", "q4_k_matvec_12288x4096", "q6_k_matvec_4096x12288",
                      "q6_k_lm_head_151936x4096", "qwen3_8b_q4km_decode_stack", "moe_decode_gpt_oss_b1",
-                     "moe_decode_gpt_oss_b4", "moe_decode_gpt_oss_b16", "prefill_mxfp4_5760x2880_m512"]:
+                     "moe_decode_gpt_oss_b4", "moe_decode_gpt_oss_b16", "prefill_mxfp4_5760x2880_m512",
+                     "moe_prefill_qwen3_30b_a3b"]:
             if name == wl.name:
                 continue
             w2 = WORKLOADS[name]()

@@ -245,7 +245,13 @@ uint64_t oco_experts_workspace(const oco_experts *w, uint32_t tokens);
  * once per call however many tokens chose it.  x: [tokens, hidden] of
  * x_dtype; out: [tokens, hidden] bf16 residual (read and written);
  * `routed` (may be NULL) receives the per-route f32 down outputs
- * [tokens*k, hidden] before the combine.  workspace: oco_experts_workspace bytes. */
+ * [tokens*k, hidden] before the combine.  workspace: oco_experts_workspace bytes.
+ * From 32 tokens on (prefill) the layer runs as grouped MFMA tiles over the
+ * route plan -- expert_up_tensor / moe_activate / expert_down_tensor
+ * (projections.metal:192-376, routing.metal:44-64) -- on f16 operands as the
+ * reference's half tiles do; activation rows enter the down tiles with a
+ * power-of-two gain into f16 range (the reference's q4_input_scales idea),
+ * so large activations do not overflow. */
 int oco_experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype,
                       const uint32_t *ids, const float *probs, uint32_t tokens, uint16_t *out,
                       float *routed, void *workspace, uint64_t workspace_bytes, oco_stream stream);

@@ -15,6 +15,7 @@
 
 #include <algorithm>
 
+#include "matmul.h"
 #include "route.h"
 #include "stream.h"
 
@@ -335,6 +336,20 @@ static int check_bank(const oco_experts *w) {
 
 static uint64_t align256(uint64_t v) { return (v + 255) & ~255ull; }
 
+// Prefill: from this many tokens on, the routed layer runs as grouped MFMA
+// GEMMs over the route plan's expert tiles.
+constexpr uint32_t MOE_MFMA_TOKENS = 32;
+
+__global__ __launch_bounds__(256) void f32_to_f16_kernel(const float *x, uint16_t *y, uint64_t n) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) {
+        const _Float16 h = (_Float16)x[i];
+        uint16_t b;
+        __builtin_memcpy(&b, &h, 2);
+        y[i] = b;
+    }
+}
+
 }  // namespace oco
 
 using namespace oco;
@@ -344,8 +359,10 @@ extern "C" {
 uint64_t oco_experts_workspace(const oco_experts *w, uint32_t tokens) {
     if (!w) return 0;
     const uint64_t routes = (uint64_t)tokens * w->k;
+    // plan, f32 activations, f16 copy of f32 inputs and activation row maxima
+    // (prefill), route outputs
     return align256(oco_route_plan_words((uint32_t)routes, w->experts) * 4) + align256(routes * w->ffn * 4) +
-           align256(routes * w->hidden * 4);
+           align256((uint64_t)tokens * w->hidden * 2) + align256(routes * 4) + align256(routes * w->hidden * 4);
 }
 
 int oco_experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype, const uint32_t *ids,
@@ -364,7 +381,61 @@ int oco_experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype, co
     uint8_t *ws = (uint8_t *)workspace;
     uint32_t *plan = (uint32_t *)ws;
     float *act = (float *)(ws + align256(oco_route_plan_words(routes, w->experts) * 4));
-    float *down = routed ? routed : (float *)((uint8_t *)act + align256((uint64_t)routes * w->ffn * 4));
+    uint16_t *x16 = (uint16_t *)((uint8_t *)act + align256((uint64_t)routes * w->ffn * 4));
+    uint32_t *rowmax = (uint32_t *)((uint8_t *)x16 + align256((uint64_t)tokens * w->hidden * 2));
+    float *down = routed ? routed : (float *)((uint8_t *)rowmax + align256((uint64_t)routes * 4));
+
+    if (tokens >= MOE_MFMA_TOKENS) {
+        // Prefill: grouped MFMA GEMMs (expert_up_tensor / moe_activate /
+        // expert_down_tensor, projections.metal:192-376, routing.metal:44-64).
+        const uint32_t bm = routes / w->experts <= 40 ? 32 : 64;
+        OCO_TRY(oco_route_plan(ids, routes, w->experts, bm, 0, 0, plan, stream));
+        const void *xin = x;
+        if (x_dtype == OCO_DT_F32) {  // the tiles take f16 (or bf16) rows
+            const uint64_t n = (uint64_t)tokens * w->hidden;
+            hipLaunchKernelGGL(f32_to_f16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+                               (const float *)x, x16, n);
+            OCO_TRY(launch_check("experts f16 inputs"));
+            xin = x16;
+        }
+        OCO_TRY(oco_buffer_fill32(rowmax, 0, routes, stream));
+        MatmulArgs g = {};
+        g.w = (const uint8_t *)w->gate;
+        g.w2 = (const uint8_t *)w->up;
+        g.bias = w->gate_bias;
+        g.bias2 = w->up_bias;
+        g.x = xin;
+        g.x_f16 = x_dtype == OCO_DT_F32;
+        g.y = act;  // f32 [routes][ffn], expert-sorted rows
+        g.rowmax = rowmax;
+        g.m = routes;
+        g.n = w->ffn;
+        g.k = w->hidden;
+        g.row_bytes = oco_row_bytes(w->format, w->hidden);
+        g.expert_bytes = g.row_bytes * w->ffn;
+        g.plan = plan;
+        g.routes = routes;
+        g.experts = w->experts;
+        g.topk = w->k;
+        g.act = w->activation;
+        g.up_one = w->up_bias_one;
+        OCO_TRY(grouped_matmul_launch(MM_GATE_UP, w->format, g, bm, s));
+        MatmulArgs d = g;
+        d.w = (const uint8_t *)w->down;
+        d.w2 = nullptr;
+        d.bias = w->down_bias;
+        d.bias2 = nullptr;
+        d.x = act;
+        d.x_f16 = 1;
+        d.y = down;  // f32 [routes][hidden]
+        d.y_bf16 = 0;
+        d.n = w->hidden;
+        d.k = w->ffn;
+        d.row_bytes = oco_row_bytes(w->format, w->ffn);
+        d.expert_bytes = d.row_bytes * w->hidden;
+        OCO_TRY(grouped_matmul_launch(MM_DOWN, w->format, d, bm, s));
+        return oco_moe_sum(down, OCO_DT_F32, probs, out, w->hidden, tokens, w->k, stream);
+    }
 
     uint32_t tiles = routes, parallel = routes;
     const uint32_t *use_plan = nullptr;

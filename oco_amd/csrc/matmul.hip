@@ -15,6 +15,7 @@
 #include <stdlib.h>
 
 #include "formats.h"
+#include "matmul.h"
 
 namespace oco {
 
@@ -22,15 +23,6 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-struct MatmulArgs {
-    const uint8_t *w;
-    const void *x;
-    void *y;
-    const float *bias;
-    uint32_t m, n, k;
-    uint64_t row_bytes;
-    uint32_t x_f16, y_bf16;
-};
 
 // 16-bit operand bits of a float: bf16 (round to nearest even) or f16.
 template <bool BF>
@@ -55,6 +47,31 @@ struct BlockShape {
 };
 
 __device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) { return (uint32_t)lo | ((uint32_t)hi << 16); }
+
+// Power of two that brings a row with max |value| `bits` (f32 bits) into
+// [2^14, 2^15) -- f16 range with its full precision; 1 for zero or
+// non-finite rows.
+__device__ __forceinline__ float row_gain(uint32_t bits) {
+    if (bits == 0 || bits >= 0x7f800000u) return 1.0f;
+    const int e = (int)(bits >> 23) - 127;  // floor(log2(max)), subnormals count as 2^-127
+    return __builtin_ldexpf(1.0f, max(-100, min(100, 14 - e)));
+}
+
+// Expert activations (projections.metal:4-13 clipped SwiGLU; elementwise.metal:
+// 70-88 SwiGLU), in f32; non-finite inputs give NaN.
+__device__ __forceinline__ float expert_activation(uint32_t act, float g, float u) {
+    if ((__float_as_uint(g) & 0x7f800000u) == 0x7f800000u || (__float_as_uint(u) & 0x7f800000u) == 0x7f800000u)
+        return __uint_as_float(0x7fc00000u);
+    float scale = 1.0f;
+    if (act == OCO_ACT_SWIGLU_CLIPPED) {
+        g = fminf(g, 7.0f);
+        u = fminf(fmaxf(u, -6.0f), 8.0f);
+        scale = 1.702f;
+    }
+    const float e = expf(-fabsf(g) * scale);
+    const float sig = (g < 0 ? e : 1.0f) / (1.0f + e);
+    return sig * g * u;
+}
 
 // One thread's share of a weight tile step: a 32-coefficient piece of one
 // row, decoded to MFMA operand bits as four runs of eight consecutive
@@ -210,7 +227,15 @@ struct Stage {
     typename PrefillPiece<FMT, BF>::Raw w[WPT];
 };
 
-template <int FMT, bool BF, int BM, int BN>
+//
+// Grouped modes (MM_GATE_UP, MM_DOWN) serve routed experts at prefill
+// (expert_up_tensor / expert_down_tensor, projections.metal:192-376): tile y
+// is the route plan's tile (expert e, first list row b), its rows the routes
+// list[e][b ..] (gate/up: their tokens' activation rows; down: the
+// expert-sorted activation rows).  In gate/up mode the BN weight rows are
+// BN/2 gate and the same BN/2 up rows, placed so each wavefront holds a gate
+// column and its up column in the same lane: the activation is fused.
+template <int FMT, bool BF, int BM, int BN, int G = MM_DENSE>
 __global__ __launch_bounds__(256) void matmul_kernel(MatmulArgs a) {
     using PP = PrefillPiece<FMT, BF>;
     using ST = Stage<FMT, BF, BM, BN>;
@@ -219,8 +244,28 @@ __global__ __launch_bounds__(256) void matmul_kernel(MatmulArgs a) {
     constexpr int XS = BM * LD, WS = BN * LD;
     extern __shared__ __attribute__((aligned(16))) uint16_t lds[];  // [2][XS] then [2][WS]
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const uint32_t m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    uint32_t m0 = blockIdx.y * BM;
+    const uint32_t n0 = blockIdx.x * (G == MM_GATE_UP ? BN / 2 : BN);
     const int tm = (wave >> 1) * (BM / 2), tn = (wave & 1) * (BN / 2);
+
+    // Grouped tile: expert, rows, and each row's route (gate/up and down) or
+    // expert-sorted row.
+    __shared__ uint32_t tile_route[G == MM_DENSE ? 1 : BM];
+    uint32_t expert = 0, rows = a.m, sorted0 = 0;
+    if constexpr (G != MM_DENSE) {
+        const uint32_t y = blockIdx.y;
+        if (y >= a.plan[1]) return;  // uniform: past the plan's tile count
+        expert = a.plan[6 + 2 * y];
+        const uint32_t first = a.plan[7 + 2 * y];
+        const uint64_t grouped = 6 + 2 * ((uint64_t)(a.routes + 15) / 16 + a.experts);
+        const uint64_t list = grouped + (uint64_t)expert * (a.routes + 1);
+        const uint64_t sorted = grouped + (uint64_t)a.experts * (a.routes + 1);
+        rows = min((uint32_t)BM, a.plan[list] - first);
+        sorted0 = a.plan[sorted + expert] + first;
+        for (uint32_t r = tid; r < rows; r += 256) tile_route[r] = a.plan[list + 1 + first + r];
+        __syncthreads();
+        m0 = 0;
+    }
 
     f32x4 acc[MI][NJ];
 #pragma unroll
@@ -236,17 +281,58 @@ __global__ __launch_bounds__(256) void matmul_kernel(MatmulArgs a) {
         const int p = tid + 256 * u;
         wrow[u] = p % BN;
         wpc[u] = p / BN;
-        wr[u] = a.w + (uint64_t)min(n0 + wrow[u], a.n - 1) * a.row_bytes;
+        if constexpr (G == MM_GATE_UP) {
+            // LDS row q: column half h = q / (BN/2); its first BN/4 rows gate, the next BN/4 up
+            const int q = wrow[u], h = q / (BN / 2), rr = q % (BN / 2);
+            const uint32_t col = n0 + h * (BN / 4) + rr % (BN / 4);
+            const uint8_t *base = (rr < BN / 4 ? a.w : a.w2) + expert * a.expert_bytes;
+            wr[u] = base + (uint64_t)min(col, a.n - 1) * a.row_bytes;
+        } else {
+            wr[u] = a.w + expert * a.expert_bytes + (uint64_t)min(n0 + wrow[u], a.n - 1) * a.row_bytes;
+        }
+    }
+    // Activation row of each X chunk this thread stages (fixed over K).  In
+    // down mode the rows are f32 activations, scaled by a power of two
+    // (row_gain) into f16 range; the epilogue divides it back out exactly.
+    const uint16_t *xrow[XPT];
+    bool xlive[XPT];
+    float xgain[G == MM_DOWN ? XPT : 1];
+#pragma unroll
+    for (int i = 0; i < XPT; i++) {
+        const int r = (tid + 256 * i) >> 4;
+        uint32_t src = m0 + r;
+        if constexpr (G == MM_GATE_UP) src = r < (int)rows ? tile_route[r] / a.topk : 0;
+        if constexpr (G == MM_DOWN) src = sorted0 + r;
+        xlive[i] = (uint32_t)r < rows && (G != MM_DENSE || m0 + r < a.m);
+        const uint32_t row = xlive[i] ? src : 0;
+        if constexpr (G == MM_DOWN) {
+            xrow[i] = reinterpret_cast<const uint16_t *>(reinterpret_cast<const float *>(a.x) + (uint64_t)row * a.k);
+            xgain[i] = row_gain(a.rowmax[row]);
+        } else {
+            xrow[i] = xg + (uint64_t)row * a.k;
+        }
     }
 
     auto load = [&](ST &st, uint32_t k0) {
 #pragma unroll
         for (int i = 0; i < XPT; i++) {
-            const int chunk = tid + 256 * i, r = chunk >> 4, cc = (chunk & 15) * 8;
-            const uint32_t row = m0 + r;
-            st.x[i] = row < a.m && k0 + cc < a.k
-                          ? *reinterpret_cast<const uint4 *>(xg + (uint64_t)row * a.k + k0 + cc)
-                          : make_uint4(0, 0, 0, 0);
+            const int chunk = tid + 256 * i, cc = (chunk & 15) * 8;
+            if constexpr (G == MM_DOWN) {
+                uint4 v = make_uint4(0, 0, 0, 0);
+                if (xlive[i] && k0 + cc < a.k) {
+                    const float4 *src = reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(xrow[i]) + k0 + cc);
+                    const float4 p = src[0], q = src[1];
+                    const float g = xgain[i];
+                    v = make_uint4(pack2(operand_bits<false>(p.x * g), operand_bits<false>(p.y * g)),
+                                   pack2(operand_bits<false>(p.z * g), operand_bits<false>(p.w * g)),
+                                   pack2(operand_bits<false>(q.x * g), operand_bits<false>(q.y * g)),
+                                   pack2(operand_bits<false>(q.z * g), operand_bits<false>(q.w * g)));
+                }
+                st.x[i] = v;
+            } else {
+                st.x[i] = xlive[i] && k0 + cc < a.k ? *reinterpret_cast<const uint4 *>(xrow[i] + k0 + cc)
+                                                    : make_uint4(0, 0, 0, 0);
+            }
         }
 #pragma unroll
         for (int u = 0; u < WPT; u++)  // 32-block formats: the last step may cover a partial 128
@@ -343,19 +429,59 @@ __global__ __launch_bounds__(256) void matmul_kernel(MatmulArgs a) {
     }
     // C fragment: lane l holds column l % 16, rows 4 (l / 16) .. + 4.
     const int cc = lane & 15, cr = (lane >> 4) * 4;
+    if constexpr (G == MM_GATE_UP) {
+        // tiles j < NJ/2: gate columns, j + NJ/2: the same up columns
+#pragma unroll
+        for (int j = 0; j < NJ / 2; j++) {
+            const uint32_t col = n0 + (wave & 1) * (BN / 4) + j * 16 + cc;
+            if (col >= a.n) continue;
+            const uint64_t bi = (uint64_t)expert * a.n + col;
+            const float bg = a.bias ? round_bf16(a.bias[bi]) : 0.f;
+            const float bu = a.bias2 ? round_bf16(a.bias2[bi] + (a.up_one ? 1.0f : 0.0f)) : (a.up_one ? 1.0f : 0.0f);
+#pragma unroll
+            for (int i = 0; i < MI; i++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const uint32_t r = tm + i * 16 + cr + v;
+                    const float act = expert_activation(a.act, acc[i][j][v] + bg, acc[i][j + NJ / 2][v] + bu);
+                    acc[i][j][v] = act;  // kept for the row maxima
+                    if (r < rows) reinterpret_cast<float *>(a.y)[(uint64_t)(sorted0 + r) * a.n + col] = act;
+                }
+        }
+        // Row maxima of |act| over this wavefront's columns (16 lanes share a
+        // row), one atomic per row; NaN/Inf rows record 0x7f800000 or more.
+#pragma unroll
+        for (int i = 0; i < MI; i++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                uint32_t m = 0;
+#pragma unroll
+                for (int j = 0; j < NJ / 2; j++) {
+                    const uint32_t col = n0 + (wave & 1) * (BN / 4) + j * 16 + cc;
+                    if (col < a.n) m = max(m, __float_as_uint(acc[i][j][v]) & 0x7fffffffu);
+                }
+#pragma unroll
+                for (int o = 1; o < 16; o <<= 1) m = max(m, (uint32_t)__shfl_xor((int)m, o));
+                const uint32_t r = tm + i * 16 + cr + v;
+                if (cc == 0 && r < rows) atomicMax(&a.rowmax[sorted0 + r], m);
+            }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < MI; i++)
 #pragma unroll
         for (int j = 0; j < NJ; j++) {
             const uint32_t col = n0 + tn + j * 16 + cc;
             if (col >= a.n) continue;
-            const float b = a.bias ? round_bf16(a.bias[col]) : 0.f;
+            const float b = a.bias ? round_bf16(a.bias[(uint64_t)expert * a.n + col]) : 0.f;
 #pragma unroll
             for (int v = 0; v < 4; v++) {
                 const uint32_t row = m0 + tm + i * 16 + cr + v;
-                if (row >= a.m) continue;
-                const float r = acc[i][j][v] + b;
-                const uint64_t o = (uint64_t)row * a.n + col;
+                if (row >= (G == MM_DENSE ? a.m : rows)) continue;
+                float r = acc[i][j][v];
+                if constexpr (G == MM_DOWN) r /= row_gain(a.rowmax[sorted0 + row]);  // exact: a power of two
+                r += b;
+                const uint64_t o = (uint64_t)(G == MM_DOWN ? tile_route[row] : row) * a.n + col;
                 if (a.y_bf16)
                     reinterpret_cast<uint16_t *>(a.y)[o] = f32_to_bf16_bits(r);
                 else
@@ -396,6 +522,37 @@ static MatmulFn matmul_pick(uint32_t fmt, uint32_t m, uint32_t n, int &bm, int &
     case 1: bm = 64; bn = 64; return matmul_pick_tile<64, 64>(fmt);
     default: bm = 64; bn = 128; return matmul_pick_tile<64, 128>(fmt);
     }
+}
+
+// Grouped (routed-expert) prefill GEMMs on f16 operands -- the reference's
+// half(w) x half(x) expert tiles (projections.metal:192-376).  Rows per tile
+// BM = 32 or 64 (the route plan must use tile_rows = BM), 128 weight rows.
+template <int BM, int G>
+static MatmulFn grouped_pick(uint32_t fmt) {
+    switch (fmt) {
+    case OCO_Q4_K: return matmul_kernel<OCO_Q4_K, false, BM, 128, G>;
+    case OCO_Q6_K: return matmul_kernel<OCO_Q6_K, false, BM, 128, G>;
+    case OCO_Q8_0: return matmul_kernel<OCO_Q8_0, false, BM, 128, G>;
+    case OCO_MXFP4: return matmul_kernel<OCO_MXFP4, false, BM, 128, G>;
+    }
+    return nullptr;
+}
+
+int grouped_matmul_launch(int mode, uint32_t fmt, const MatmulArgs &a, uint32_t bm, hipStream_t stream) {
+    MatmulFn fn = nullptr;
+    if (mode == MM_GATE_UP) fn = bm == 32 ? grouped_pick<32, MM_GATE_UP>(fmt) : grouped_pick<64, MM_GATE_UP>(fmt);
+    if (mode == MM_DOWN) fn = bm == 32 ? grouped_pick<32, MM_DOWN>(fmt) : grouped_pick<64, MM_DOWN>(fmt);
+    if (!fn) return fail(OCO_ERR_UNSUPPORTED, "experts: format %u has no grouped MFMA kernel", fmt);
+    if (a.k % 32) return fail(OCO_ERR_INVALID, "experts: k=%u is not a multiple of 32", a.k);
+    constexpr uint32_t BN = 128;
+    const uint32_t cols = mode == MM_GATE_UP ? BN / 2 : BN;
+    const dim3 grid((a.n + cols - 1) / cols, (a.routes + bm - 1) / bm + a.experts);
+    const size_t lds = (size_t)2 * (bm + BN) * (128 + 8) * 2;
+    if (lds > 64 * 1024)
+        OCO_TRY(hip_check(hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+                          "hipFuncSetAttribute"));
+    hipLaunchKernelGGL(fn, grid, dim3(256), lds, stream, a);
+    return launch_check("experts grouped matmul");
 }
 
 uint64_t mx_workspace_bytes(uint32_t m, uint32_t k);

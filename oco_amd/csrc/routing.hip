@@ -41,35 +41,57 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const XT *x, const f
 // Route plan (routing.metal:4-39, nemotron.metal:238-273) by one workgroup:
 // per-expert route lists in route order, expert-sorted first rows, each
 // route's sorted row, (expert, first list row) tiles of `tile_rows`, and the
-// two dispatch grids at words 0-5.  Counts go through LDS; lists are
-// written by one thread per expert.
-__global__ __launch_bounds__(256) void route_plan_kernel(const uint32_t *ids, uint32_t routes,
-                                                         uint32_t experts, uint32_t tile_rows,
-                                                         uint32_t up_tiles, uint32_t down_tiles,
-                                                         uint32_t *plan) {
-    extern __shared__ uint32_t counts[];  // [experts] counts, [experts] offsets
+// two dispatch grids at words 0-5.  Routes are taken 1024 at a time; a
+// route's place in its expert's list is the expert's running count plus the
+// number of earlier routes of the chunk with the same expert (broadcast LDS
+// reads), so lists keep route order.  Ids >= experts are left out.
+constexpr uint32_t PLAN_THREADS = 1024;
+
+__global__ __launch_bounds__(PLAN_THREADS) void route_plan_kernel(const uint32_t *ids, uint32_t routes,
+                                                                  uint32_t experts, uint32_t tile_rows,
+                                                                  uint32_t up_tiles, uint32_t down_tiles,
+                                                                  uint32_t *plan) {
+    extern __shared__ __attribute__((aligned(16))) uint32_t sh[];  // chunk ids [1024]; run, tile base, offset [experts]
+    uint32_t *chunk = sh, *run = sh + PLAN_THREADS, *tbase = run + experts, *offs = tbase + experts;
+    const uint32_t tid = threadIdx.x;
     const uint64_t grouped = 6 + 2 * ((uint64_t)(routes + 15) / 16 + experts);
     const uint64_t sorted = grouped + (uint64_t)experts * (routes + 1);
-    for (uint32_t e = threadIdx.x; e < experts; e += blockDim.x) {
-        uint32_t count = 0;
-        const uint64_t base = grouped + (uint64_t)e * (routes + 1);
-        for (uint32_t i = 0; i < routes; i++)
-            if (ids[i] == e) plan[base + 1 + count++] = i;
-        plan[base] = count;
-        counts[e] = count;
-    }
+    for (uint32_t e = tid; e < experts; e += PLAN_THREADS) run[e] = 0;
     __syncthreads();
-    if (threadIdx.x == 0) {
-        uint32_t tiles = 0, offset = 0;
-        for (uint32_t e = 0; e < experts; e++) {
-            counts[experts + e] = offset;
-            plan[sorted + e] = offset;
-            offset += counts[e];
-            for (uint32_t b = 0; b < counts[e]; b += tile_rows) {
-                plan[6 + 2 * (uint64_t)tiles] = e;
-                plan[6 + 2 * (uint64_t)tiles + 1] = b;
-                tiles++;
+    for (uint32_t base = 0; base < routes; base += PLAN_THREADS) {
+        const uint32_t i = base + tid;
+        const uint32_t e = i < routes ? ids[i] : 0xffffffffu;
+        chunk[tid] = e;
+        __syncthreads();
+        uint32_t rank = 0;
+        if (e < experts) {
+            const uint4 *c4 = reinterpret_cast<const uint4 *>(chunk);
+            uint32_t j = 0;
+            for (; j + 4 <= tid; j += 4) {
+                const uint4 v = c4[j / 4];
+                rank += (v.x == e) + (v.y == e) + (v.z == e) + (v.w == e);
             }
+            for (; j < tid; j++) rank += chunk[j] == e;
+        }
+        const uint32_t pos = e < experts ? run[e] + rank : 0;
+        __syncthreads();  // every read of run[] and chunk[] is done
+        if (e < experts) {
+            plan[grouped + (uint64_t)e * (routes + 1) + 1 + pos] = i;
+            plan[sorted + experts + i] = pos;  // the expert's offset is added below
+            atomicAdd(&run[e], 1u);
+        }
+        __syncthreads();
+    }
+    if (tid == 0) {  // offsets and tile bases (a scan over experts)
+        uint32_t offset = 0, tiles = 0;
+        for (uint32_t e = 0; e < experts; e++) {
+            const uint32_t count = run[e];
+            plan[grouped + (uint64_t)e * (routes + 1)] = count;
+            plan[sorted + e] = offset;
+            offs[e] = offset;
+            tbase[e] = tiles;
+            offset += count;
+            tiles += (count + tile_rows - 1) / tile_rows;
         }
         plan[0] = up_tiles;
         plan[1] = tiles;
@@ -79,10 +101,17 @@ __global__ __launch_bounds__(256) void route_plan_kernel(const uint32_t *ids, ui
         plan[5] = 1;
     }
     __syncthreads();
-    for (uint32_t e = threadIdx.x; e < experts; e += blockDim.x) {
-        const uint64_t base = grouped + (uint64_t)e * (routes + 1);
-        const uint32_t count = counts[e], offset = counts[experts + e];
-        for (uint32_t i = 0; i < count; i++) plan[sorted + experts + plan[base + 1 + i]] = offset + i;
+    for (uint32_t e = tid; e < experts; e += PLAN_THREADS) {
+        uint32_t t = tbase[e];
+        for (uint32_t b = 0; b < run[e]; b += tile_rows, t++) {
+            plan[6 + 2 * (uint64_t)t] = e;
+            plan[6 + 2 * (uint64_t)t + 1] = b;
+        }
+    }
+    // sorted row of each route = its expert's offset + its place in the list
+    for (uint32_t i = tid; i < routes; i += PLAN_THREADS) {
+        const uint32_t e = ids[i];
+        if (e < experts) plan[sorted + experts + i] += offs[e];
     }
 }
 
@@ -169,8 +198,8 @@ int oco_route_plan(const uint32_t *ids, uint32_t routes, uint32_t experts, uint3
         return fail(OCO_ERR_INVALID,
                     "oco_route_plan: need 0 < experts <= 4096 and tile_rows >= 16 (the plan holds ceil(routes/16) + "
                     "experts tiles)");
-    hipLaunchKernelGGL(route_plan_kernel, dim3(1), dim3(256), (size_t)experts * 8, (hipStream_t)stream, ids,
-                       routes, experts, tile_rows, up_tiles, down_tiles, plan);
+    hipLaunchKernelGGL(route_plan_kernel, dim3(1), dim3(PLAN_THREADS), (size_t)(PLAN_THREADS + 3 * experts) * 4,
+                       (hipStream_t)stream, ids, routes, experts, tile_rows, up_tiles, down_tiles, plan);
     return launch_check("oco_route_plan");
 }
 

@@ -239,25 +239,23 @@ def experts_reference(fmt, hidden, ffn, gate, up, down, x, ids, probs, residual_
     mag_up = np.zeros((routes, ffn))
     y = np.zeros((routes, hidden))
     mag_y = np.zeros((routes, hidden))
-    cache = {}
-    for r in range(routes):
-        e = int(ids[r])
-        if e not in cache:
-            cache[e] = (expert_rows(fmt, gate, e, ffn, hidden), expert_rows(fmt, up, e, ffn, hidden),
-                        expert_rows(fmt, down, e, hidden, ffn))
-        G, U, D = cache[e]
-        xt = xf[r // k]
+    for e in np.unique(ids):  # the routes of one expert as matrix products
+        e = int(e)
+        rs = np.nonzero(ids == e)[0]
+        G, U, D = (expert_rows(fmt, gate, e, ffn, hidden), expert_rows(fmt, up, e, ffn, hidden),
+                   expert_rows(fmt, down, e, hidden, ffn))
+        X = xf[rs // k]
         gb = bf16_round(gate_bias[e * ffn:(e + 1) * ffn]) if gate_bias is not None else 0.0
         ub = (bf16_round(up_bias[e * ffn:(e + 1) * ffn] + (1.0 if up_one else 0.0)) if up_bias is not None
               else (1.0 if up_one else 0.0))
-        gat[r] = G @ xt + gb
-        upv[r] = U @ xt + ub
-        mag_up[r] = np.abs(U) @ np.abs(xt) + np.abs(ub)
-        act[r] = (swiglu_clipped_f64 if activation == 0 else swiglu_f64)(gat[r], upv[r])
-        a_in = act[r] if act_override is None else np.asarray(act_override[r], np.float64)
+        gat[rs] = X @ G.T + gb
+        upv[rs] = X @ U.T + ub
+        mag_up[rs] = np.abs(X) @ np.abs(U).T + np.abs(ub)
+        act[rs] = (swiglu_clipped_f64 if activation == 0 else swiglu_f64)(gat[rs], upv[rs])
+        a_in = act[rs] if act_override is None else np.asarray(act_override, np.float64)[rs]
         db = bf16_round(down_bias[e * hidden:(e + 1) * hidden]) if down_bias is not None else 0.0
-        y[r] = D @ a_in + db
-        mag_y[r] = np.abs(D) @ np.abs(a_in) + np.abs(db)
+        y[rs] = a_in @ D.T + db
+        mag_y[rs] = np.abs(a_in) @ np.abs(D).T + np.abs(db)
     p = np.asarray(probs, np.float64).reshape(tokens, k)
     yb = bf16_round(y).reshape(tokens, k, hidden)
     s = np.einsum("tkh,tk->th", yb, p)

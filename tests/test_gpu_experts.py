@@ -66,7 +66,8 @@ def test_router_logits(lib):
     np.testing.assert_array_equal(ib.download(np.uint32).reshape(tokens, k), want_ids)
 
 
-@pytest.mark.parametrize("batch,experts,tile", [(1, 32, 16), (17, 32, 64), (257, 32, 64), (512, 128, 16)])
+@pytest.mark.parametrize("batch,experts,tile", [(1, 32, 16), (17, 32, 64), (257, 32, 64), (512, 128, 16),
+                                                (600, 128, 32), (2048, 128, 64), (300, 256, 16)])
 def test_route_plan_bit_exact(lib, batch, experts, tile):
     say("route_plan", batch, experts, tile)
     if experts == 32 and batch > 1:
@@ -195,7 +196,8 @@ def test_experts_apply_matches_oracle(lib, fmt, tokens):
 
 def test_experts_overfull_tiles(lib):
     """Batch 257 with ids [31, t%15, 15+t%8, 30]: experts 30/31 own 257 routes each,
-    spanning many tiles (mxfp4.rs:309-482)."""
+    spanning many tiles (mxfp4.rs:309-482).  At 257 tokens the layer runs as
+    grouped f16 MFMA tiles (the reference's half tiles): bar 2e-3."""
     E, hidden, ffn, k, tokens = 32, 96, 96, 4, 257
     say("experts overfull")
     host, devs = bank(lib, 39, E, hidden, ffn, seed=77)
@@ -211,7 +213,7 @@ def test_experts_overfull_tiles(lib):
     bk.apply(dev(lib, x), lib.DType.F32, dev(lib, ids), dev(lib, probs), tokens, outb, routed=routed.ptr)
     lib.synchronize()
     ref = O.experts_reference(39, hidden, ffn, g, u, d, x, ids, probs, resid, gb, ub, db)
-    assert rel_l2(routed.read(np.float32).reshape(-1, hidden), ref["down"]) < 1e-4
+    assert rel_l2(routed.read(np.float32).reshape(-1, hidden), ref["down"]) < 2e-3
 
 
 def test_experts_full_shape_batch4(lib):
@@ -231,3 +233,59 @@ def test_experts_full_shape_batch4(lib):
     lib.synchronize()
     ref = O.experts_reference(39, hidden, ffn, g, u, d, x, ids, probs, resid, gb, ub, db)
     assert rel_l2(routed.read(np.float32).reshape(-1, hidden), ref["down"]) < 1e-4
+
+
+# ---- prefill: grouped MFMA tiles -----------------------------------------------
+
+def _prefill_case(lib, fmt, E, hidden, ffn, k, tokens, x_dtype, seed, clipped):
+    host, devs = bank(lib, fmt, E, hidden, ffn, seed=seed)
+    g, u, d, gb, ub, db = host
+    rng = np.random.default_rng(seed)
+    x = rng.normal(size=(tokens, hidden)).astype(np.float32)
+    ids, probs = O.select_experts(rng.normal(size=(tokens, E)).astype(np.float32), k)
+    resid = O.f32_to_bf16(rng.normal(size=(tokens, hidden)).astype(np.float32))
+    act = 0 if clipped else 1
+    if clipped:
+        bk = lib.ExpertBank(fmt, hidden, ffn, E, k, *devs, activation=act, up_bias_one=True)
+    else:  # Qwen3 MoE: no biases, plain SwiGLU
+        bk = lib.ExpertBank(fmt, hidden, ffn, E, k, devs[0], devs[1], devs[2], activation=act, up_bias_one=False)
+        gb = ub = db = None
+    if x_dtype == "bf16":
+        xin, xdt = O.f32_to_bf16(x), lib.DType.BF16
+        x = O.bf16_to_f32(xin)
+    else:
+        xin, xdt = x, lib.DType.F32
+    outb = dev(lib, resid)
+    routed = Guarded(lib, tokens * k * hidden * 4)
+    bk.apply(dev(lib, xin), xdt, dev(lib, ids), dev(lib, probs), tokens, outb, routed=routed.ptr)
+    lib.synchronize()
+    ref = O.experts_reference(fmt, hidden, ffn, g, u, d, x, ids, probs, resid, gb, ub, db,
+                              activation=act, up_one=clipped)
+    return routed.read(np.float32).reshape(tokens * k, hidden), outb.download(np.uint16).reshape(tokens, hidden), ref
+
+
+@pytest.mark.parametrize("fmt,clipped", [(12, False), (14, False), (8, False), (39, True)])
+@pytest.mark.parametrize("tokens,x_dtype", [(32, "f32"), (130, "bf16")])
+def test_experts_prefill_matches_oracle(lib, fmt, clipped, tokens, x_dtype):
+    """Grouped MFMA prefill (expert_up_tensor / moe_activate / expert_down_tensor,
+    projections.metal:192-376): f16 operands and f16 activations as in the
+    reference's tiles; bar relL2 2e-3 on the route outputs, the combine within
+    bf16 roundings of the reference's."""
+    E, hidden, ffn, k = 16, 512, 256, 4
+    say("experts prefill", fmt, tokens, x_dtype)
+    got, out, ref = _prefill_case(lib, fmt, E, hidden, ffn, k, tokens, x_dtype, 60 + fmt + tokens, clipped)
+    assert rel_l2(got, ref["down"]) < 2e-3
+    want = O.bf16_to_f32(ref["out"])
+    diff = np.abs(O.bf16_to_f32(out).astype(np.float64) - want)
+    # bf16 roundings of the output plus the route error carried by sum |y_r| p_r
+    mag = np.abs(ref["down"]).reshape(tokens, k, hidden).sum(axis=1)
+    assert np.all(diff <= 2 ** -6 * np.abs(want) + 4e-3 * mag + 2e-2)
+
+
+def test_experts_prefill_qwen3_shape(lib):
+    """Qwen3-30B-A3B layer geometry (hidden 2048, ffn 768, Q4_K, top-8, SwiGLU)
+    at 512 tokens over 8 experts: ~512 routes per expert, many 64-row tiles."""
+    E, hidden, ffn, k, tokens = 8, 2048, 768, 8, 512
+    say("experts prefill qwen3 shape")
+    got, _, ref = _prefill_case(lib, 12, E, hidden, ffn, k, tokens, "bf16", 91, False)
+    assert rel_l2(got, ref["down"]) < 2e-3
