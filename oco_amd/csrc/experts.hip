@@ -340,10 +340,17 @@ static uint64_t align256(uint64_t v) { return (v + 255) & ~255ull; }
 // GEMMs over the route plan's expert tiles.
 constexpr uint32_t MOE_MFMA_TOKENS = 32;
 
-__global__ __launch_bounds__(256) void f32_to_f16_kernel(const float *x, uint16_t *y, uint64_t n) {
+// Activation rows to f16 (the reference's half(x)) from f32 or bf16.
+template <typename XT>
+__global__ __launch_bounds__(256) void to_f16_kernel(const XT *x, uint16_t *y, uint64_t n) {
     const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
     if (i < n) {
-        const _Float16 h = (_Float16)x[i];
+        float v;
+        if constexpr (sizeof(XT) == 4)
+            v = x[i];
+        else
+            v = __uint_as_float((uint32_t)x[i] << 16);
+        const _Float16 h = (_Float16)v;
         uint16_t b;
         __builtin_memcpy(&b, &h, 2);
         y[i] = b;
@@ -388,16 +395,21 @@ int oco_experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype, co
     if (tokens >= MOE_MFMA_TOKENS) {
         // Prefill: grouped MFMA GEMMs (expert_up_tensor / moe_activate /
         // expert_down_tensor, projections.metal:192-376, routing.metal:44-64).
-        const uint32_t bm = routes / w->experts <= 40 ? 32 : 64;
+        const bool q4 = w->format == OCO_Q4_K && !getenv("OCO_MOE_LDS");  // OCO_MOE_LDS: tuning comparisons
+        // Rows per tile: most experts in one tile (mean routes per expert,
+        // plus room for the spread).
+        const uint32_t mean = routes / w->experts;
+        const uint32_t bm = q4 ? (mean <= 20 ? 32 : mean <= 36 ? 48 : 64) : (mean <= 40 ? 32 : 64);
         OCO_TRY(oco_route_plan(ids, routes, w->experts, bm, 0, 0, plan, stream));
-        const void *xin = x;
-        if (x_dtype == OCO_DT_F32) {  // the tiles take f16 (or bf16) rows
-            const uint64_t n = (uint64_t)tokens * w->hidden;
-            hipLaunchKernelGGL(f32_to_f16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
-                               (const float *)x, x16, n);
-            OCO_TRY(launch_check("experts f16 inputs"));
-            xin = x16;
-        }
+        // The tiles take f16 rows (the reference's half(x)).
+        const uint64_t nx = (uint64_t)tokens * w->hidden;
+        const dim3 gx((unsigned)((nx + 255) / 256));
+        if (x_dtype == OCO_DT_F32)
+            hipLaunchKernelGGL(to_f16_kernel<float>, gx, dim3(256), 0, s, (const float *)x, x16, nx);
+        else
+            hipLaunchKernelGGL(to_f16_kernel<uint16_t>, gx, dim3(256), 0, s, (const uint16_t *)x, x16, nx);
+        OCO_TRY(launch_check("experts f16 inputs"));
+        const void *xin = x16;
         OCO_TRY(oco_buffer_fill32(rowmax, 0, routes, stream));
         MatmulArgs g = {};
         g.w = (const uint8_t *)w->gate;
@@ -405,7 +417,7 @@ int oco_experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype, co
         g.bias = w->gate_bias;
         g.bias2 = w->up_bias;
         g.x = xin;
-        g.x_f16 = x_dtype == OCO_DT_F32;
+        g.x_f16 = 1;
         g.y = act;  // f32 [routes][ffn], expert-sorted rows
         g.rowmax = rowmax;
         g.m = routes;
@@ -419,7 +431,7 @@ int oco_experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype, co
         g.topk = w->k;
         g.act = w->activation;
         g.up_one = w->up_bias_one;
-        OCO_TRY(grouped_matmul_launch(MM_GATE_UP, w->format, g, bm, s));
+        OCO_TRY(q4 ? moe_q4k_launch(MM_GATE_UP, g, bm, s) : grouped_matmul_launch(MM_GATE_UP, w->format, g, bm, s));
         MatmulArgs d = g;
         d.w = (const uint8_t *)w->down;
         d.w2 = nullptr;
@@ -433,7 +445,7 @@ int oco_experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype, co
         d.k = w->ffn;
         d.row_bytes = oco_row_bytes(w->format, w->ffn);
         d.expert_bytes = d.row_bytes * w->hidden;
-        OCO_TRY(grouped_matmul_launch(MM_DOWN, w->format, d, bm, s));
+        OCO_TRY(q4 ? moe_q4k_launch(MM_DOWN, d, bm, s) : grouped_matmul_launch(MM_DOWN, w->format, d, bm, s));
         return oco_moe_sum(down, OCO_DT_F32, probs, out, w->hidden, tokens, w->k, stream);
     }
 

@@ -33,4 +33,8 @@ constexpr int MM_DOWN = 2;     // per expert tile: routed[route] = act W_down^T 
 // a per-row power-of-two gain into f16 and writes f32 (or bf16) route rows.
 int grouped_matmul_launch(int mode, uint32_t fmt, const MatmulArgs &a, uint32_t bm, hipStream_t stream);
 
+// The same for Q4_K banks with weights decoded in registers (route plan with
+// tile_rows = bm: 32, 48 or 64).
+int moe_q4k_launch(int mode, const MatmulArgs &a, uint32_t bm, hipStream_t stream);
+
 }  // namespace oco

@@ -43,46 +43,36 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const XT *x, const f
 // route's sorted row, (expert, first list row) tiles of `tile_rows`, and the
 // two dispatch grids at words 0-5.  Routes are taken 1024 at a time; a
 // route's place in its expert's list is the expert's running count plus the
-// number of earlier routes of the chunk with the same expert (broadcast LDS
-// reads), so lists keep route order.  Ids >= experts are left out.
+// number of earlier routes of the chunk with the same expert, so lists keep
+// route order: up to 256 experts from lane comparisons inside each
+// wavefront and per-wavefront histograms in LDS, beyond that by broadcast
+// LDS reads of the whole chunk.  Ids >= experts are left out.
 constexpr uint32_t PLAN_THREADS = 1024;
+constexpr uint32_t PLAN_HIST_EXPERTS = 256;  // per-wavefront histograms in LDS up to this many experts
 
 __global__ __launch_bounds__(PLAN_THREADS) void route_plan_kernel(const uint32_t *ids, uint32_t routes,
                                                                   uint32_t experts, uint32_t tile_rows,
                                                                   uint32_t up_tiles, uint32_t down_tiles,
                                                                   uint32_t *plan) {
-    extern __shared__ __attribute__((aligned(16))) uint32_t sh[];  // chunk ids [1024]; run, tile base, offset [experts]
+    // LDS: chunk ids [1024]; run, tile base, offset [experts]; per-wavefront
+    // histograms [16][experts] (experts <= PLAN_HIST_EXPERTS)
+    extern __shared__ __attribute__((aligned(16))) uint32_t sh[];
     uint32_t *chunk = sh, *run = sh + PLAN_THREADS, *tbase = run + experts, *offs = tbase + experts;
-    const uint32_t tid = threadIdx.x;
+    uint32_t *hist = offs + experts;
+    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const uint64_t grouped = 6 + 2 * ((uint64_t)(routes + 15) / 16 + experts);
     const uint64_t sorted = grouped + (uint64_t)experts * (routes + 1);
+
+    // 1. counts per expert
     for (uint32_t e = tid; e < experts; e += PLAN_THREADS) run[e] = 0;
     __syncthreads();
-    for (uint32_t base = 0; base < routes; base += PLAN_THREADS) {
-        const uint32_t i = base + tid;
-        const uint32_t e = i < routes ? ids[i] : 0xffffffffu;
-        chunk[tid] = e;
-        __syncthreads();
-        uint32_t rank = 0;
-        if (e < experts) {
-            const uint4 *c4 = reinterpret_cast<const uint4 *>(chunk);
-            uint32_t j = 0;
-            for (; j + 4 <= tid; j += 4) {
-                const uint4 v = c4[j / 4];
-                rank += (v.x == e) + (v.y == e) + (v.z == e) + (v.w == e);
-            }
-            for (; j < tid; j++) rank += chunk[j] == e;
-        }
-        const uint32_t pos = e < experts ? run[e] + rank : 0;
-        __syncthreads();  // every read of run[] and chunk[] is done
-        if (e < experts) {
-            plan[grouped + (uint64_t)e * (routes + 1) + 1 + pos] = i;
-            plan[sorted + experts + i] = pos;  // the expert's offset is added below
-            atomicAdd(&run[e], 1u);
-        }
-        __syncthreads();
+    for (uint32_t i = tid; i < routes; i += PLAN_THREADS) {
+        const uint32_t e = ids[i];
+        if (e < experts) atomicAdd(&run[e], 1u);
     }
-    if (tid == 0) {  // offsets and tile bases (a scan over experts)
+    __syncthreads();
+    // 2. offsets, tile bases, counts (a scan over experts)
+    if (tid == 0) {
         uint32_t offset = 0, tiles = 0;
         for (uint32_t e = 0; e < experts; e++) {
             const uint32_t count = run[e];
@@ -107,11 +97,55 @@ __global__ __launch_bounds__(PLAN_THREADS) void route_plan_kernel(const uint32_t
             plan[6 + 2 * (uint64_t)t] = e;
             plan[6 + 2 * (uint64_t)t + 1] = b;
         }
+        run[e] = 0;  // reused as the running count of step 3
     }
-    // sorted row of each route = its expert's offset + its place in the list
-    for (uint32_t i = tid; i < routes; i += PLAN_THREADS) {
-        const uint32_t e = ids[i];
-        if (e < experts) plan[sorted + experts + i] += offs[e];
+    __syncthreads();
+    // 3. stable placement, 1024 routes at a time: a route's place in its
+    // expert's list is the running count plus its rank among the chunk's
+    // earlier routes of the same expert
+    uint32_t e_next = tid < routes ? ids[tid] : 0xffffffffu;
+    for (uint32_t base = 0; base < routes; base += PLAN_THREADS) {
+        const uint32_t i = base + tid, e = e_next;
+        e_next = i + PLAN_THREADS < routes ? ids[i + PLAN_THREADS] : 0xffffffffu;  // next chunk, in flight
+        uint32_t rank = 0;
+        if (experts <= PLAN_HIST_EXPERTS) {
+            // rank among earlier lanes of the wavefront; whether this is the
+            // expert's last lane in it
+            bool last = true;
+            for (int b = 0; b < 64; b++) {
+                const uint32_t eb = (uint32_t)__builtin_amdgcn_readlane((int)e, b);
+                if (eb == e) {
+                    if ((uint32_t)b < lane) rank++;
+                    if ((uint32_t)b > lane) last = false;
+                }
+            }
+            for (uint32_t t = tid; t < 16 * experts; t += PLAN_THREADS) hist[t] = 0;
+            __syncthreads();
+            if (e < experts && last) hist[wave * experts + e] = rank + 1;
+            __syncthreads();
+            if (e < experts)
+                for (uint32_t w = 0; w < wave; w++) rank += hist[w * experts + e];
+        } else {
+            chunk[tid] = e;
+            __syncthreads();
+            if (e < experts) {
+                const uint4 *c4 = reinterpret_cast<const uint4 *>(chunk);
+                uint32_t j = 0;
+                for (; j + 4 <= tid; j += 4) {
+                    const uint4 v = c4[j / 4];
+                    rank += (v.x == e) + (v.y == e) + (v.z == e) + (v.w == e);
+                }
+                for (; j < tid; j++) rank += chunk[j] == e;
+            }
+        }
+        const uint32_t pos = e < experts ? run[e] + rank : 0;
+        __syncthreads();  // every read of run[], chunk[] and hist[] is done
+        if (e < experts) {
+            plan[grouped + (uint64_t)e * (routes + 1) + 1 + pos] = i;
+            plan[sorted + experts + i] = offs[e] + pos;
+            atomicAdd(&run[e], 1u);
+        }
+        __syncthreads();
     }
 }
 
@@ -198,7 +232,8 @@ int oco_route_plan(const uint32_t *ids, uint32_t routes, uint32_t experts, uint3
         return fail(OCO_ERR_INVALID,
                     "oco_route_plan: need 0 < experts <= 4096 and tile_rows >= 16 (the plan holds ceil(routes/16) + "
                     "experts tiles)");
-    hipLaunchKernelGGL(route_plan_kernel, dim3(1), dim3(PLAN_THREADS), (size_t)(PLAN_THREADS + 3 * experts) * 4,
+    hipLaunchKernelGGL(route_plan_kernel, dim3(1), dim3(PLAN_THREADS),
+                       (size_t)(PLAN_THREADS + 3 * experts + (experts <= PLAN_HIST_EXPERTS ? 16 * experts : 0)) * 4,
                        (hipStream_t)stream, ids, routes, experts, tile_rows, up_tiles, down_tiles, plan);
     return launch_check("oco_route_plan");
 }
