@@ -439,14 +439,16 @@ int oco_experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype, co
         d.bias2 = nullptr;
         d.x = act;
         d.x_f16 = 1;
-        d.y = down;  // f32 [routes][hidden]
-        d.y_bf16 = 0;
+        // Route outputs: f32 when the caller asks for them, else bf16 as the
+        // reference stores them (moe_sum rounds f32 routes to bf16 anyway).
+        d.y = down;
+        d.y_bf16 = routed ? 0 : 1;
         d.n = w->hidden;
         d.k = w->ffn;
         d.row_bytes = oco_row_bytes(w->format, w->ffn);
         d.expert_bytes = d.row_bytes * w->hidden;
         OCO_TRY(q4 ? moe_q4k_launch(MM_DOWN, d, bm, s) : grouped_matmul_launch(MM_DOWN, w->format, d, bm, s));
-        return oco_moe_sum(down, OCO_DT_F32, probs, out, w->hidden, tokens, w->k, stream);
+        return oco_moe_sum(down, routed ? OCO_DT_F32 : OCO_DT_BF16, probs, out, w->hidden, tokens, w->k, stream);
     }
 
     uint32_t tiles = routes, parallel = routes;

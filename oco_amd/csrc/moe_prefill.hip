@@ -312,8 +312,8 @@ __global__ __launch_bounds__(64 * NW) void moe_q4k_kernel(MatmulArgs a) {
     }
 }
 
-// Four wavefronts; rows per tile bm = 16 MI routes (32, 48 or 64).
-constexpr int Q4_NW = 4;
+// Eight wavefronts (two per SIMD); rows per tile bm = 16 MI routes (32, 48 or 64).
+constexpr int Q4_NW = 8;
 
 template <int MI>
 static void q4_launch(int mode, const MatmulArgs &a, dim3 grid, hipStream_t stream) {

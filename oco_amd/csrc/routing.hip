@@ -63,31 +63,63 @@ __global__ __launch_bounds__(PLAN_THREADS) void route_plan_kernel(const uint32_t
     const uint64_t grouped = 6 + 2 * ((uint64_t)(routes + 15) / 16 + experts);
     const uint64_t sorted = grouped + (uint64_t)experts * (routes + 1);
 
-    // 1. counts per expert
+    // 1. counts per expert (four ids in flight per thread)
     for (uint32_t e = tid; e < experts; e += PLAN_THREADS) run[e] = 0;
     __syncthreads();
-    for (uint32_t i = tid; i < routes; i += PLAN_THREADS) {
-        const uint32_t e = ids[i];
-        if (e < experts) atomicAdd(&run[e], 1u);
+    for (uint32_t base = tid; base < routes; base += 4 * PLAN_THREADS) {
+        uint32_t ev[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const uint32_t i = base + u * PLAN_THREADS;
+            ev[u] = i < routes ? ids[i] : 0xffffffffu;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+            if (ev[u] < experts) atomicAdd(&run[ev[u]], 1u);
     }
     __syncthreads();
-    // 2. offsets, tile bases, counts (a scan over experts)
-    if (tid == 0) {
-        uint32_t offset = 0, tiles = 0;
-        for (uint32_t e = 0; e < experts; e++) {
-            const uint32_t count = run[e];
-            plan[grouped + (uint64_t)e * (routes + 1)] = count;
-            plan[sorted + e] = offset;
-            offs[e] = offset;
-            tbase[e] = tiles;
-            offset += count;
-            tiles += (count + tile_rows - 1) / tile_rows;
+    // 2. offsets and tile bases: a block-wide exclusive scan over experts
+    // (thread t owns experts [t P, t P + P)), then counts, offsets, tiles
+    const uint32_t P = (experts + PLAN_THREADS - 1) / PLAN_THREADS, e0 = tid * P;
+    uint32_t my_c = 0, my_t = 0;
+    for (uint32_t e = e0; e < min(e0 + P, experts); e++) {
+        my_c += run[e];
+        my_t += (run[e] + tile_rows - 1) / tile_rows;
+    }
+    uint32_t inc_c = my_c, inc_t = my_t;  // inclusive scans within the wavefront
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t c2 = (uint32_t)__shfl_up((int)inc_c, o), t2 = (uint32_t)__shfl_up((int)inc_t, o);
+        if ((int)lane >= o) {
+            inc_c += c2;
+            inc_t += t2;
         }
+    }
+    uint32_t *wsum = chunk;  // [16] counts, [16] tiles (chunk is free until step 3)
+    if (lane == 63) {
+        wsum[wave] = inc_c;
+        wsum[16 + wave] = inc_t;
+    }
+    __syncthreads();
+    uint32_t off_c = inc_c - my_c, off_t = inc_t - my_t;
+    for (uint32_t w = 0; w < wave; w++) {
+        off_c += wsum[w];
+        off_t += wsum[16 + w];
+    }
+    for (uint32_t e = e0; e < min(e0 + P, experts); e++) {
+        const uint32_t count = run[e];
+        plan[grouped + (uint64_t)e * (routes + 1)] = count;
+        plan[sorted + e] = off_c;
+        offs[e] = off_c;
+        tbase[e] = off_t;
+        off_c += count;
+        off_t += (count + tile_rows - 1) / tile_rows;
+    }
+    if (tid == PLAN_THREADS - 1) {  // the last thread ends with the totals
         plan[0] = up_tiles;
-        plan[1] = tiles;
+        plan[1] = off_t;
         plan[2] = 1;
         plan[3] = down_tiles;
-        plan[4] = tiles;
+        plan[4] = off_t;
         plan[5] = 1;
     }
     __syncthreads();
@@ -97,8 +129,9 @@ __global__ __launch_bounds__(PLAN_THREADS) void route_plan_kernel(const uint32_t
             plan[6 + 2 * (uint64_t)t] = e;
             plan[6 + 2 * (uint64_t)t + 1] = b;
         }
-        run[e] = 0;  // reused as the running count of step 3
     }
+    __syncthreads();
+    for (uint32_t e = tid; e < experts; e += PLAN_THREADS) run[e] = 0;  // reused as the running count of step 3
     __syncthreads();
     // 3. stable placement, 1024 routes at a time: a route's place in its
     // expert's list is the running count plus its rank among the chunk's

@@ -289,3 +289,25 @@ def test_experts_prefill_qwen3_shape(lib):
     say("experts prefill qwen3 shape")
     got, _, ref = _prefill_case(lib, 12, E, hidden, ffn, k, tokens, "bf16", 91, False)
     assert rel_l2(got, ref["down"]) < 2e-3
+
+
+@pytest.mark.parametrize("fmt", [12, 39])
+def test_experts_prefill_bf16_routes_bit_identical(lib, fmt):
+    """Without `routed` the down tiles store bf16 routes (as the reference
+    does); moe_sum rounds f32 routes to bf16 first, so both runs agree bit
+    for bit."""
+    E, hidden, ffn, k, tokens = 16, 512, 256, 4, 64
+    host, devs = bank(lib, fmt, E, hidden, ffn, seed=17)
+    rng = np.random.default_rng(17)
+    x = rng.normal(size=(tokens, hidden)).astype(np.float32)
+    ids, probs = O.select_experts(rng.normal(size=(tokens, E)).astype(np.float32), k)
+    resid = O.f32_to_bf16(rng.normal(size=(tokens, hidden)).astype(np.float32))
+    bk = lib.ExpertBank(fmt, hidden, ffn, E, k, *devs, activation=0 if fmt == 39 else 1, up_bias_one=fmt == 39)
+    outs = []
+    for with_routed in (True, False):
+        outb = dev(lib, resid)
+        routed = lib.DeviceBuffer(tokens * k * hidden * 4) if with_routed else None
+        bk.apply(dev(lib, x), lib.DType.F32, dev(lib, ids), dev(lib, probs), tokens, outb, routed=routed)
+        lib.synchronize()
+        outs.append(outb.download(np.uint16))
+    np.testing.assert_array_equal(outs[0], outs[1])
