@@ -173,4 +173,16 @@ struct XLoad<bf16_t> {
     }
 };
 
+// XCD-aware workgroup order.  MI355X dispatches workgroup p (linear id) to
+// XCD p % 8, and each XCD has its own L2.  xcd_order(p, used) renumbers the
+// first `used` logical ids so that XCD x runs one contiguous range of them,
+// evenly split: workgroups that share operands, when numbered consecutively,
+// then share one L2.  Surplus workgroups (grids sized for a bound known only
+// on the device) get `used` and exit.
+constexpr uint32_t XCDS = 8;
+__device__ __forceinline__ uint32_t xcd_order(uint32_t p, uint32_t used) {
+    const uint32_t q = used / XCDS, r = used % XCDS, x = p % XCDS, slot = p / XCDS;
+    return slot < q + (x < r ? 1u : 0u) ? x * q + min(x, r) + slot : used;
+}
+
 }  // namespace oco

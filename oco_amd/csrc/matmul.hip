@@ -244,8 +244,17 @@ __global__ __launch_bounds__(256) void matmul_kernel(MatmulArgs a) {
     constexpr int XS = BM * LD, WS = BN * LD;
     extern __shared__ __attribute__((aligned(16))) uint16_t lds[];  // [2][XS] then [2][WS]
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    uint32_t m0 = blockIdx.y * BM;
-    const uint32_t n0 = blockIdx.x * (G == MM_GATE_UP ? BN / 2 : BN);
+    // Logical (column tile bx, row tile / plan tile by) in XCD order: dense
+    // tiles column-major (the row tiles of a weight column tile share one
+    // L2), grouped tiles tile-major (the column tiles of a route tile share
+    // its activation rows).
+    const uint32_t used = G == MM_DENSE ? gridDim.x * gridDim.y : gridDim.x * min(a.plan[1], gridDim.y);
+    const uint32_t lin = xcd_order(blockIdx.x + gridDim.x * blockIdx.y, used);
+    if (lin >= used) return;  // uniform: a surplus workgroup (grouped grids are sized for the tile bound)
+    const uint32_t bx = G == MM_DENSE ? lin / gridDim.y : lin % gridDim.x;
+    const uint32_t by = G == MM_DENSE ? lin % gridDim.y : lin / gridDim.x;
+    uint32_t m0 = by * BM;
+    const uint32_t n0 = bx * (G == MM_GATE_UP ? BN / 2 : BN);
     const int tm = (wave >> 1) * (BM / 2), tn = (wave & 1) * (BN / 2);
 
     // Grouped tile: expert, rows, and each row's route (gate/up and down) or
@@ -253,7 +262,7 @@ __global__ __launch_bounds__(256) void matmul_kernel(MatmulArgs a) {
     __shared__ uint32_t tile_route[G == MM_DENSE ? 1 : BM];
     uint32_t expert = 0, rows = a.m, sorted0 = 0;
     if constexpr (G != MM_DENSE) {
-        const uint32_t y = blockIdx.y;
+        const uint32_t y = by;
         if (y >= a.plan[1]) return;  // uniform: past the plan's tile count
         expert = a.plan[6 + 2 * y];
         const uint32_t first = a.plan[7 + 2 * y];

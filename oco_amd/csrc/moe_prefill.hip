@@ -132,8 +132,12 @@ __global__ __launch_bounds__(64 * NW) void moe_q4k_kernel(MatmulArgs a) {
     __shared__ uint32_t tile_route[ROWS];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c16 = lane & 15, q = lane >> 4;
-    const uint32_t y = blockIdx.y;
-    if (y >= a.plan[1]) return;  // uniform: past the plan's tile count
+    // Logical (column group, tile), tile-major per XCD: the column groups of
+    // one tile share its activation rows in one L2.
+    const uint32_t used = gridDim.x * min(a.plan[1], gridDim.y);  // the plan's real tiles
+    const uint32_t lin = xcd_order(blockIdx.x + gridDim.x * blockIdx.y, used);
+    if (lin >= used) return;  // uniform: a surplus workgroup
+    const uint32_t bx = lin % gridDim.x, y = lin / gridDim.x;
     const uint32_t expert = a.plan[6 + 2 * y], first = a.plan[7 + 2 * y];
     const uint64_t grouped = 6 + 2 * ((uint64_t)(a.routes + 15) / 16 + a.experts);
     const uint64_t list = grouped + (uint64_t)expert * (a.routes + 1);
@@ -144,7 +148,7 @@ __global__ __launch_bounds__(64 * NW) void moe_q4k_kernel(MatmulArgs a) {
     __syncthreads();
 
     // This wavefront's two 16-row weight fragments.
-    const uint32_t col0 = (blockIdx.x * NW + wave) * (G == MM_GATE_UP ? 16 : 32);
+    const uint32_t col0 = (bx * NW + wave) * (G == MM_GATE_UP ? 16 : 32);
     const uint8_t *wrow[2];
 #pragma unroll
     for (int j = 0; j < 2; j++) {

@@ -239,7 +239,12 @@ __global__ __launch_bounds__(256 * NW) void mx_matmul_kernel(MxArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];  // [3][STAGE]
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane & 31, part = lane >> 5;
     const int wm = wave & 3, wn = wave >> 2;
-    const uint32_t tile0 = blockIdx.y * (4 * MI) + wm * MI, col0 = blockIdx.x * P::BN;
+    // Logical (column tile, row tile), column-major per XCD: the row tiles of
+    // one weight column tile share its GGUF bytes in one L2, and each XCD's
+    // share of the split activations stays resident.
+    const uint32_t lin = xcd_order(blockIdx.x + gridDim.x * blockIdx.y, gridDim.x * gridDim.y);
+    const uint32_t bx = lin / gridDim.y, by = lin % gridDim.y;
+    const uint32_t tile0 = by * (4 * MI) + wm * MI, col0 = bx * P::BN;
     const uint32_t nblk = a.k / 32;
 
     MxRing<MI, CT, NW, D> ring;
