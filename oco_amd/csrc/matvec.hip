@@ -211,19 +211,33 @@ __global__ __launch_bounds__(256) void stream_kernel(StreamArgs a) {
     // Stage x (f32) in piece-major order, then the per-piece sums.
     {
         const XT *xr = reinterpret_cast<const XT *>(a.x) + (uint64_t)input * p.k;
-        for (uint32_t f = threadIdx.x; f < p.k / 4; f += 256) {
-            float v[4];
-            if constexpr (sizeof(XT) == 4) {
-                float4 t = reinterpret_cast<const float4 *>(xr)[f];
-                v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
-            } else {
-                uint2 t = reinterpret_cast<const uint2 *>(xr)[f];
-                v[0] = __uint_as_float(t.x << 16); v[1] = __uint_as_float(t.x & 0xffff0000u);
-                v[2] = __uint_as_float(t.y << 16); v[3] = __uint_as_float(t.y & 0xffff0000u);
+        // Four loads in flight per thread before any store: x arrives in one
+        // memory round trip, not one per loop iteration.
+        for (uint32_t f0 = threadIdx.x; f0 < p.k / 4; f0 += 4 * 256) {
+            float v[4][4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const uint32_t f = f0 + 256 * u;
+                if (f < p.k / 4) {
+                    if constexpr (sizeof(XT) == 4) {
+                        const float4 t = reinterpret_cast<const float4 *>(xr)[f];
+                        v[u][0] = t.x; v[u][1] = t.y; v[u][2] = t.z; v[u][3] = t.w;
+                    } else {
+                        const uint2 t = reinterpret_cast<const uint2 *>(xr)[f];
+                        v[u][0] = __uint_as_float(t.x << 16); v[u][1] = __uint_as_float(t.x & 0xffff0000u);
+                        v[u][2] = __uint_as_float(t.y << 16); v[u][3] = __uint_as_float(t.y & 0xffff0000u);
+                    }
+                }
             }
-            uint32_t pp, tt;
-            T::map(f, pp, tt);
-            xs4[tt * PT + pp] = make_float4(v[0], v[1], v[2], v[3]);
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const uint32_t f = f0 + 256 * u;
+                if (f < p.k / 4) {
+                    uint32_t pp, tt;
+                    T::map(f, pp, tt);
+                    xs4[tt * PT + pp] = make_float4(v[u][0], v[u][1], v[u][2], v[u][3]);
+                }
+            }
         }
         if constexpr (T::NSUM > 0) {
             __syncthreads();
@@ -373,9 +387,11 @@ static StreamPlan stream_plan(uint32_t fmt, uint32_t k, uint32_t n, uint32_t m) 
     }
     uint64_t row_bytes = oco_row_bytes(fmt, k);
     int ks = row_bytes > 6144 ? 4 : row_bytes > 3072 ? 2 : 1;
-    (void)n;
     (void)m;
-    return {1, ks, 2};
+    // Three workgroups per CU only pay off on long streams (measured: the
+    // 510 MB Q6_K lm_head 3.6 -> 4.2 TB/s; 8-41 MB matrices lose with it).
+    const int wg = (uint64_t)n * row_bytes > (128ull << 20) ? 3 : 2;
+    return {1, ks, wg};
 }
 
 typedef void (*MatvecFn)(MatvecArgs);
