@@ -339,6 +339,8 @@ static uint64_t align256(uint64_t v) { return (v + 255) & ~255ull; }
 // Prefill: from this many tokens on, the routed layer runs as grouped MFMA
 // GEMMs over the route plan's expert tiles.
 constexpr uint32_t MOE_MFMA_TOKENS = 32;
+// MXFP4 banks take the block-scaled MFMA path from this many tokens on.
+constexpr uint32_t MOE_MX_TOKENS = 8;  // measured: B=16 331 -> 237 us; B=4 is faster on the routed kernel
 
 // Activation rows to f16 (the reference's half(x)) from f32 or bf16.
 template <typename XT>
@@ -367,9 +369,13 @@ uint64_t oco_experts_workspace(const oco_experts *w, uint32_t tokens) {
     if (!w) return 0;
     const uint64_t routes = (uint64_t)tokens * w->k;
     // plan, f32 activations, f16 copy of f32 inputs and activation row maxima
-    // (prefill), route outputs
-    return align256(oco_route_plan_words((uint32_t)routes, w->experts) * 4) + align256(routes * w->ffn * 4) +
-           align256((uint64_t)tokens * w->hidden * 2) + align256(routes * 4) + align256(routes * w->hidden * 4);
+    // (prefill), route outputs; MXFP4 banks also the E4M3 splits of the
+    // inputs and of the activations
+    uint64_t bytes = align256(oco_route_plan_words((uint32_t)routes, w->experts) * 4) + align256(routes * w->ffn * 4) +
+                     align256((uint64_t)tokens * w->hidden * 2) + align256(routes * 4) + align256(routes * w->hidden * 4);
+    if (w->format == OCO_MXFP4)
+        bytes += align256(mx_rows_bytes(tokens, w->hidden, 3)) + align256(mx_rows_bytes((uint32_t)routes, w->ffn, 3));
+    return bytes;
 }
 
 int oco_experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype, const uint32_t *ids,
@@ -390,9 +396,55 @@ int oco_experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype, co
     float *act = (float *)(ws + align256(oco_route_plan_words(routes, w->experts) * 4));
     uint16_t *x16 = (uint16_t *)((uint8_t *)act + align256((uint64_t)routes * w->ffn * 4));
     uint32_t *rowmax = (uint32_t *)((uint8_t *)x16 + align256((uint64_t)tokens * w->hidden * 2));
-    float *down = routed ? routed : (float *)((uint8_t *)rowmax + align256((uint64_t)routes * 4));
+    uint8_t *own_down = (uint8_t *)rowmax + align256((uint64_t)routes * 4);
+    float *down = routed ? routed : (float *)own_down;
+    uint8_t *xrec = own_down + align256((uint64_t)routes * w->hidden * 4);  // MXFP4 only
+    uint8_t *arec = xrec + align256(mx_rows_bytes(tokens, w->hidden, 3));
 
-    if (tokens >= MOE_MFMA_TOKENS) {
+    static const uint32_t mx_tokens =
+        getenv("OCO_MOE_MX_TOKENS") ? (uint32_t)atoi(getenv("OCO_MOE_MX_TOKENS")) : MOE_MX_TOKENS;  // tuning runs only
+    if (w->format == OCO_MXFP4 && tokens >= mx_tokens) {
+        // MXFP4 banks: block-scaled FP8 x FP4 MFMA on the GGUF bytes (no
+        // weight decode); activations split per row into E4M3 terms.
+        OCO_TRY(oco_route_plan(ids, routes, w->experts, 32, 0, 0, plan, stream));
+        const int xterms = x_dtype == OCO_DT_BF16 ? 2 : 3;  // bf16 rows are exact in two terms
+        OCO_TRY(mx_rows_split(x, x_dtype == OCO_DT_BF16, xrec, tokens, w->hidden, xterms, s));
+        MatmulArgs g = {};
+        g.w = (const uint8_t *)w->gate;
+        g.w2 = (const uint8_t *)w->up;
+        g.bias = w->gate_bias;
+        g.bias2 = w->up_bias;
+        g.y = act;  // f32 [routes][ffn], expert-sorted rows
+        g.m = routes;
+        g.n = w->ffn;
+        g.k = w->hidden;
+        g.row_bytes = oco_row_bytes(w->format, w->hidden);
+        g.expert_bytes = g.row_bytes * w->ffn;
+        g.plan = plan;
+        g.routes = routes;
+        g.experts = w->experts;
+        g.topk = w->k;
+        g.act = w->activation;
+        g.up_one = w->up_bias_one;
+        OCO_TRY(mx_experts_launch(MM_GATE_UP, g, xrec, xterms, s));
+        OCO_TRY(mx_rows_split(act, false, arec, routes, w->ffn, 3, s));
+        MatmulArgs d = g;
+        d.w = (const uint8_t *)w->down;
+        d.w2 = nullptr;
+        d.bias = w->down_bias;
+        d.bias2 = nullptr;
+        d.y = down;
+        d.y_bf16 = routed ? 0 : 1;
+        d.n = w->hidden;
+        d.k = w->ffn;
+        d.row_bytes = oco_row_bytes(w->format, w->ffn);
+        d.expert_bytes = d.row_bytes * w->hidden;
+        OCO_TRY(mx_experts_launch(MM_DOWN, d, arec, 3, s));
+        return oco_moe_sum(down, routed ? OCO_DT_F32 : OCO_DT_BF16, probs, out, w->hidden, tokens, w->k, stream);
+    }
+
+    static const uint32_t mfma_tokens = getenv("OCO_MOE_MFMA_TOKENS") ? (uint32_t)atoi(getenv("OCO_MOE_MFMA_TOKENS")) : MOE_MFMA_TOKENS;  // tuning runs only
+    if (tokens >= mfma_tokens) {
         // Prefill: grouped MFMA GEMMs (expert_up_tensor / moe_activate /
         // expert_down_tensor, projections.metal:192-376, routing.metal:44-64).
         const bool q4 = w->format == OCO_Q4_K && !getenv("OCO_MOE_LDS");  // OCO_MOE_LDS: tuning comparisons

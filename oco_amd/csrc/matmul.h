@@ -27,6 +27,22 @@ constexpr int MM_DENSE = 0;  // Y = X W^T
 constexpr int MM_GATE_UP = 1;  // per expert tile: act = f(X W_gate^T, X W_up^T), f32 at expert-sorted rows
 constexpr int MM_DOWN = 2;     // per expert tile: routed[route] = act W_down^T (+ bias), f32
 
+// Expert activations (projections.metal:4-13 clipped SwiGLU; elementwise.metal:
+// 70-88 SwiGLU), in f32; non-finite inputs give NaN.
+__device__ __forceinline__ float expert_activation(uint32_t act, float g, float u) {
+    if ((__float_as_uint(g) & 0x7f800000u) == 0x7f800000u || (__float_as_uint(u) & 0x7f800000u) == 0x7f800000u)
+        return __uint_as_float(0x7fc00000u);
+    float scale = 1.0f;
+    if (act == OCO_ACT_SWIGLU_CLIPPED) {
+        g = fminf(g, 7.0f);
+        u = fminf(fmaxf(u, -6.0f), 8.0f);
+        scale = 1.702f;
+    }
+    const float e = expf(-fabsf(g) * scale);
+    const float sig = (g < 0 ? e : 1.0f) / (1.0f + e);
+    return sig * g * u;
+}
+
 // One grouped GEMM over a route plan built with tile_rows = bm (32 or 64):
 // MM_GATE_UP writes f32 activations at expert-sorted rows and each row's
 // max |activation| (rowmax, zeroed by the caller); MM_DOWN reads them with
@@ -36,5 +52,11 @@ int grouped_matmul_launch(int mode, uint32_t fmt, const MatmulArgs &a, uint32_t 
 // The same for Q4_K banks with weights decoded in registers (route plan with
 // tile_rows = bm: 32, 48 or 64).
 int moe_q4k_launch(int mode, const MatmulArgs &a, uint32_t bm, hipStream_t stream);
+
+// MXFP4 banks on the block-scaled MFMA: activations split per row into E4M3
+// records (mx_rows_bytes each matrix), route plan with tile_rows = 32.
+uint64_t mx_rows_bytes(uint32_t rows, uint32_t k, int terms);
+int mx_rows_split(const void *x, bool bf16, uint8_t *rec, uint32_t rows, uint32_t k, int terms, hipStream_t stream);
+int mx_experts_launch(int mode, const MatmulArgs &a, const uint8_t *xrec, int terms, hipStream_t stream);
 
 }  // namespace oco

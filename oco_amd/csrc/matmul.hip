@@ -57,21 +57,6 @@ __device__ __forceinline__ float row_gain(uint32_t bits) {
     return __builtin_ldexpf(1.0f, max(-100, min(100, 14 - e)));
 }
 
-// Expert activations (projections.metal:4-13 clipped SwiGLU; elementwise.metal:
-// 70-88 SwiGLU), in f32; non-finite inputs give NaN.
-__device__ __forceinline__ float expert_activation(uint32_t act, float g, float u) {
-    if ((__float_as_uint(g) & 0x7f800000u) == 0x7f800000u || (__float_as_uint(u) & 0x7f800000u) == 0x7f800000u)
-        return __uint_as_float(0x7fc00000u);
-    float scale = 1.0f;
-    if (act == OCO_ACT_SWIGLU_CLIPPED) {
-        g = fminf(g, 7.0f);
-        u = fminf(fmaxf(u, -6.0f), 8.0f);
-        scale = 1.702f;
-    }
-    const float e = expf(-fabsf(g) * scale);
-    const float sig = (g < 0 ? e : 1.0f) / (1.0f + e);
-    return sig * g * u;
-}
 
 // One thread's share of a weight tile step: a 32-coefficient piece of one
 // row, decoded to MFMA operand bits as four runs of eight consecutive

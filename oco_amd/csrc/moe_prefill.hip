@@ -33,19 +33,6 @@ struct Q4Raw {  // one lane's bytes of one super-block: header and its 32 qs byt
     uint4 hdr, q0, q1;
 };
 
-__device__ __forceinline__ float q4_expert_activation(uint32_t act, float g, float u) {
-    if ((__float_as_uint(g) & 0x7f800000u) == 0x7f800000u || (__float_as_uint(u) & 0x7f800000u) == 0x7f800000u)
-        return __uint_as_float(0x7fc00000u);
-    float scale = 1.0f;
-    if (act == OCO_ACT_SWIGLU_CLIPPED) {
-        g = fminf(g, 7.0f);
-        u = fminf(fmaxf(u, -6.0f), 8.0f);
-        scale = 1.702f;
-    }
-    const float e = expf(-fabsf(g) * scale);
-    const float sig = (g < 0 ? e : 1.0f) / (1.0f + e);
-    return sig * g * u;
-}
 
 __device__ __forceinline__ float q4_row_gain(uint32_t bits) {
     if (bits == 0 || bits >= 0x7f800000u) return 1.0f;
@@ -286,7 +273,7 @@ __global__ __launch_bounds__(64 * NW) void moe_q4k_kernel(MatmulArgs a) {
 #pragma unroll
             for (int v = 0; v < 4; v++) {
                 const uint32_t r = i * 16 + cr + v;
-                const float act = q4_expert_activation(a.act, acc[i][0][v] + bg, acc[i][1][v] + bu);
+                const float act = expert_activation(a.act, acc[i][0][v] + bg, acc[i][1][v] + bu);
                 if (cok && r < rows) reinterpret_cast<float *>(a.y)[(uint64_t)(sorted0 + r) * a.n + col] = act;
                 uint32_t m = cok ? __float_as_uint(act) & 0x7fffffffu : 0u;
 #pragma unroll
