@@ -331,6 +331,11 @@ static int check_bank(const oco_experts *w) {
         return fail(OCO_ERR_INVALID, "experts: need 0 < k <= 8, k <= experts <= 256");
     if (w->activation > OCO_ACT_SWIGLU) return fail(OCO_ERR_INVALID, "experts: unknown activation");
     if (w->hidden == 0 || w->ffn == 0) return fail(OCO_ERR_INVALID, "experts: empty geometry");
+    uint32_t be, bb;
+    OCO_TRY(oco_block_layout(w->format, &be, &bb));
+    if (w->hidden % be || w->ffn % be || w->hidden % 32 || w->ffn % 32)
+        return fail(OCO_ERR_INVALID, "experts: hidden=%u and ffn=%u must be multiples of 32 and of the block (%u)",
+                    w->hidden, w->ffn, be);
     return OCO_OK;
 }
 

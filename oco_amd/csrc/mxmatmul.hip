@@ -184,7 +184,7 @@ struct MxRing {
     const uint8_t *arec[MI];  // this lane's records, step 0
     const uint8_t *brow[P::BU];
     uint32_t bdst[P::BU], bd[P::BU];
-    uint4 ra[D][MI][4];  // A of step t in slot t % D: [tile][term * 2 + block]
+    i32x8 ra[D][MI][2];  // A of step t in slot t % D: [tile][term], already in MFMA operand form
     uint32_t rs[D][MI];
     uint32_t rb[D][P::BU];  // B of step t (awaiting its LDS store) in slot t % D
 
@@ -209,7 +209,11 @@ struct MxRing {
         for (int i = 0; i < MI; i++) {
             const uint8_t *rec = arec[i] + (uint64_t)s * MX_REC;
 #pragma unroll
-            for (int q = 0; q < 4; q++) ra[SLOT][i][q] = *reinterpret_cast<const uint4 *>(rec + q * 1024);
+            for (int t = 0; t < 2; t++) {
+                const uint4 lo = *reinterpret_cast<const uint4 *>(rec + (2 * t) * 1024);
+                const uint4 hi = *reinterpret_cast<const uint4 *>(rec + (2 * t + 1) * 1024);
+                ra[SLOT][i][t] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+            }
             rs[SLOT][i] = *reinterpret_cast<const uint32_t *>(rec - lane * 16 + MX_DATA + lane * 4);
         }
     }
@@ -282,9 +286,7 @@ __global__ __launch_bounds__(256 * NW) void mx_matmul_kernel(MxArgs a) {
         for (int t = 0; t < 2; t++)
 #pragma unroll
             for (int i = 0; i < MI; i++) {
-                const uint4 *r = ring.ra[SL][i] + 2 * t;
-                const i32x8 av{(int)r[0].x, (int)r[0].y, (int)r[0].z, (int)r[0].w,
-                               (int)r[1].x, (int)r[1].y, (int)r[1].z, (int)r[1].w};
+                const i32x8 &av = ring.ra[SL][i][t];
 #pragma unroll
                 for (int j = 0; j < CW; j++) {
                     if (t == 0)

@@ -44,3 +44,24 @@ def test_host_helpers_without_gpu():
     assert lib.oco_row_bytes(39, 2880) == 1530
     assert lib.oco_row_bytes(12, 100) == 0
     assert lib.oco_route_plan_words(68, 32) == 6 + 2 * (5 + 32) + 32 * 69 + 32 + 68
+
+
+def test_argument_validation_without_gpu():
+    """Geometry checks fail with OCO_ERR_INVALID before any GPU work (the
+    pointers are never dereferenced), and workspace sizes follow the layouts."""
+    lib = oco_amd.load_library()
+    fake = ctypes.c_void_p(0x1000)
+    bad = oco_amd.ExpertsDesc(39, 100, 256, 8, 2, 0, 1, fake, fake, fake, None, None, None)
+    rc = lib.oco_experts_apply(ctypes.byref(bad), fake, 0, fake, fake, 4, fake, None, fake, 1 << 30, None)
+    assert rc == 1 and b"multiples of 32" in lib.oco_last_error()
+    q4 = oco_amd.ExpertsDesc(12, 2048, 768, 128, 8, 1, 0, fake, fake, fake, None, None, None)
+    assert lib.oco_experts_workspace(ctypes.byref(q4), 512) > 512 * 8 * 2048 * 2
+    p = oco_amd.Matrix(100, 64, 16, 0, 1, 1, 0)  # k = 100 is not a multiple of 32
+    assert lib.oco_matmul(12, fake, fake, 1, fake, 0, None, ctypes.byref(p), None) == 1
+    p = oco_amd.Matrix(2880, 5760, 512, 0, 1, 1, 0)
+    need = lib.oco_matmul_workspace(39, 1, ctypes.byref(p))
+    assert need == (512 // 32) * (2880 // 64) * 4352
+    assert lib.oco_matmul_workspace(12, 1, ctypes.byref(p)) == 0
+    assert lib.oco_matmul_ws(39, fake, fake, 1, fake, 0, None, ctypes.byref(p), fake, need - 1, None) == 1
+    assert b"workspace" in lib.oco_last_error()
+    assert lib.oco_route_plan(fake, 64, 32, 8, 0, 0, fake, None) == 1  # tile_rows < 16
