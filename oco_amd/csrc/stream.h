@@ -167,27 +167,22 @@ struct Tile<OCO_Q4_K> {
     }
     __device__ __forceinline__ static float dot(const Raw &r, const float *x, const float *s, int c) {
         const uint32_t g = (uint32_t)c >> 1;
-        uint32_t sb[12];
+        // (scale, min) of sub-blocks 2g and 2g+1 (weights.metal:70-71) from
+        // scales[12] = hdr.y (bytes 0..3), hdr.z (4..7), hdr.w (8..11):
+        // runtime bit offsets, one select between the j < 4 and j >= 4
+        // forms (a runtime index into a byte array costs a compare/select
+        // chain per byte).
+        uint32_t scm[2][2];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            sb[i] = byte_of(r.hdr.y, i);
-            sb[4 + i] = byte_of(r.hdr.z, i);
-            sb[8 + i] = byte_of(r.hdr.w, i);
+        for (int h = 0; h < 2; h++) {
+            const uint32_t t = 8 * ((2 * g + h) & 3);
+            const uint32_t sc_lo = __builtin_amdgcn_ubfe(r.hdr.y, t, 6), mn_lo = __builtin_amdgcn_ubfe(r.hdr.z, t, 6);
+            const uint32_t sc_hi = __builtin_amdgcn_ubfe(r.hdr.w, t, 4) | (__builtin_amdgcn_ubfe(r.hdr.y, t + 6, 2) << 4);
+            const uint32_t mn_hi = __builtin_amdgcn_ubfe(r.hdr.w, t + 4, 4) | (__builtin_amdgcn_ubfe(r.hdr.z, t + 6, 2) << 4);
+            scm[h][0] = g < 2 ? sc_lo : sc_hi;
+            scm[h][1] = g < 2 ? mn_lo : mn_hi;
         }
-        // (scale, min) of sub-blocks 2g and 2g+1 (weights.metal:70-71).
-        uint32_t sc0, mn0, sc1, mn1;
-        if (g < 2) {
-            sc0 = sb[2 * g] & 63u;
-            mn0 = sb[2 * g + 4] & 63u;
-            sc1 = sb[2 * g + 1] & 63u;
-            mn1 = sb[2 * g + 5] & 63u;
-        } else {
-            uint32_t s0 = 2 * g, s1 = s0 + 1;
-            sc0 = (sb[s0 + 4] & 15u) | ((sb[s0 - 4] >> 6) << 4);
-            mn0 = (sb[s0 + 4] >> 4) | ((sb[s0] >> 6) << 4);
-            sc1 = (sb[s1 + 4] & 15u) | ((sb[s1 - 4] >> 6) << 4);
-            mn1 = (sb[s1 + 4] >> 4) | ((sb[s1] >> 6) << 4);
-        }
+        const uint32_t sc0 = scm[0][0], mn0 = scm[0][1], sc1 = scm[1][0], mn1 = scm[1][1];
         const uint32_t w[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
         float a0 = 0.f, a1 = 0.f;
 #pragma unroll
