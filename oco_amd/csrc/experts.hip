@@ -324,7 +324,10 @@ static int moe_launch(uint32_t fmt, bool gated, MoeArgs a, uint32_t tiles, uint3
     return launch_check("experts projection");
 }
 
-static int check_bank(const oco_experts *w) {
+// hidden is the reduction length of gate/up and must be whole blocks; ffn is
+// the reduction length of down, so only callers that run down (need_down)
+// require it in whole blocks (expand alone takes any ffn).
+static int check_bank(const oco_experts *w, bool need_down) {
     if (!w) return fail(OCO_ERR_INVALID, "experts: null descriptor");
     if (!w->gate || !w->up || !w->down) return fail(OCO_ERR_INVALID, "experts: null weights");
     if (w->experts == 0 || w->experts > 256 || w->k == 0 || w->k > 8 || w->k > w->experts)
@@ -333,9 +336,9 @@ static int check_bank(const oco_experts *w) {
     if (w->hidden == 0 || w->ffn == 0) return fail(OCO_ERR_INVALID, "experts: empty geometry");
     uint32_t be, bb;
     OCO_TRY(oco_block_layout(w->format, &be, &bb));
-    if (w->hidden % be || w->ffn % be || w->hidden % 32 || w->ffn % 32)
-        return fail(OCO_ERR_INVALID, "experts: hidden=%u and ffn=%u must be multiples of 32 and of the block (%u)",
-                    w->hidden, w->ffn, be);
+    if (w->hidden % be) return fail(OCO_ERR_INVALID, "experts: hidden=%u must be whole blocks of %u", w->hidden, be);
+    if (need_down && w->ffn % be)
+        return fail(OCO_ERR_INVALID, "experts: ffn=%u must be whole blocks of %u", w->ffn, be);
     return OCO_OK;
 }
 
@@ -386,7 +389,7 @@ uint64_t oco_experts_workspace(const oco_experts *w, uint32_t tokens) {
 int oco_experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype, const uint32_t *ids,
                       const float *probs, uint32_t tokens, uint16_t *out, float *routed, void *workspace,
                       uint64_t workspace_bytes, oco_stream stream) {
-    OCO_TRY(check_bank(w));
+    OCO_TRY(check_bank(w, true));
     if (!tokens) return OCO_OK;
     if (!x || !ids || !probs || !out || !workspace) return fail(OCO_ERR_INVALID, "oco_experts_apply: null pointer");
     if (x_dtype != OCO_DT_F32 && x_dtype != OCO_DT_BF16)
@@ -408,7 +411,10 @@ int oco_experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype, co
 
     static const uint32_t mx_tokens =
         getenv("OCO_MOE_MX_TOKENS") ? (uint32_t)atoi(getenv("OCO_MOE_MX_TOKENS")) : MOE_MX_TOKENS;  // tuning runs only
-    if (w->format == OCO_MXFP4 && tokens >= mx_tokens) {
+    // The MFMA tiles and the E4M3 row split read whole 32-element k groups
+    // and n tiles; other geometries take the routed matvec path below.
+    const bool tiled = w->hidden % 32 == 0 && w->ffn % 32 == 0;
+    if (tiled && w->format == OCO_MXFP4 && tokens >= mx_tokens) {
         // MXFP4 banks: block-scaled FP8 x FP4 MFMA on the GGUF bytes (no
         // weight decode); activations split per row into E4M3 terms.
         OCO_TRY(oco_route_plan(ids, routes, w->experts, 32, 0, 0, plan, stream));
@@ -449,7 +455,7 @@ int oco_experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype, co
     }
 
     static const uint32_t mfma_tokens = getenv("OCO_MOE_MFMA_TOKENS") ? (uint32_t)atoi(getenv("OCO_MOE_MFMA_TOKENS")) : MOE_MFMA_TOKENS;  // tuning runs only
-    if (tokens >= mfma_tokens) {
+    if (tiled && tokens >= mfma_tokens) {
         // Prefill: grouped MFMA GEMMs (expert_up_tensor / moe_activate /
         // expert_down_tensor, projections.metal:192-376, routing.metal:44-64).
         const bool q4 = w->format == OCO_Q4_K && !getenv("OCO_MOE_LDS");  // OCO_MOE_LDS: tuning comparisons
@@ -554,7 +560,7 @@ int oco_experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype, co
 
 int oco_expert_expand(const oco_experts *w, const void *x, oco_dtype x_dtype, const float *logits, uint32_t *ids,
                       float *probs, float *up_out, float *act_out, oco_stream stream) {
-    OCO_TRY(check_bank(w));
+    OCO_TRY(check_bank(w, false));
     if (!x || !logits || !ids || !probs || !act_out) return fail(OCO_ERR_INVALID, "oco_expert_expand: null pointer");
     if (w->experts > 64) return fail(OCO_ERR_UNSUPPORTED, "oco_expert_expand: fused selection covers <= 64 experts");
     if (x_dtype != OCO_DT_F32 && x_dtype != OCO_DT_BF16)

@@ -77,8 +77,20 @@ __device__ __forceinline__ float decode_scalar(uint32_t fmt, const uint8_t *b, u
 // ---------------------------------------------------------------------------
 // Piece decoders for the streaming matvec.
 // ---------------------------------------------------------------------------
-// Converts byte i of w (unsigned) to float exactly (v_cvt_f32_ubyte{0..3}).
-__device__ __forceinline__ float ub(uint32_t w, int i) { return (float)((w >> (8 * i)) & 0xffu); }
+// Converts byte i of w (unsigned) to float exactly with one
+// v_cvt_f32_ubyte{0..3}.  i must be a constant after unrolling.  Written as
+// asm because the compiler otherwise folds the caller's nibble mask into a
+// v_bfe_u32 and converts byte 0, two instructions per weight.
+__device__ __forceinline__ float ub(uint32_t w, int i) {
+    float f;
+    switch (i) {
+    case 0: asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(f) : "v"(w)); break;
+    case 1: asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(f) : "v"(w)); break;
+    case 2: asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(f) : "v"(w)); break;
+    default: asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(f) : "v"(w)); break;
+    }
+    return f;
+}
 
 template <int FMT>
 struct Piece;

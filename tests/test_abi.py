@@ -53,7 +53,11 @@ def test_argument_validation_without_gpu():
     fake = ctypes.c_void_p(0x1000)
     bad = oco_amd.ExpertsDesc(39, 100, 256, 8, 2, 0, 1, fake, fake, fake, None, None, None)
     rc = lib.oco_experts_apply(ctypes.byref(bad), fake, 0, fake, fake, 4, fake, None, fake, 1 << 30, None)
-    assert rc == 1 and b"multiples of 32" in lib.oco_last_error()
+    assert rc == 1 and b"hidden=100 must be whole blocks" in lib.oco_last_error()
+    # ffn is the down projection's reduction length: apply needs whole blocks
+    odd = oco_amd.ExpertsDesc(39, 2880, 33, 8, 2, 0, 1, fake, fake, fake, None, None, None)
+    rc = lib.oco_experts_apply(ctypes.byref(odd), fake, 0, fake, fake, 4, fake, None, fake, 1 << 30, None)
+    assert rc == 1 and b"ffn=33 must be whole blocks" in lib.oco_last_error()
     q4 = oco_amd.ExpertsDesc(12, 2048, 768, 128, 8, 1, 0, fake, fake, fake, None, None, None)
     assert lib.oco_experts_workspace(ctypes.byref(q4), 512) > 512 * 8 * 2048 * 2
     p = oco_amd.Matrix(100, 64, 16, 0, 1, 1, 0)  # k = 100 is not a multiple of 32
