@@ -549,7 +549,7 @@ int grouped_matmul_launch(int mode, uint32_t fmt, const MatmulArgs &a, uint32_t 
     return launch_check("experts grouped matmul");
 }
 
-uint64_t mx_workspace_bytes(uint32_t m, uint32_t k);
+uint64_t mx_workspace_bytes(uint32_t m, uint32_t n, uint32_t k);
 int mx_matmul_launch(const void *w, const void *x, void *y, bool y_bf16, const float *bias, uint32_t m, uint32_t n,
                      uint32_t k, void *workspace, hipStream_t stream);
 
@@ -610,7 +610,7 @@ using namespace oco;
 extern "C" uint64_t oco_matmul_workspace(uint32_t format, oco_dtype x_dtype, const oco_matrix *p) {
     (void)x_dtype;
     if (!p || !use_mx(format)) return 0;
-    return mx_workspace_bytes(p->m, p->k);
+    return mx_workspace_bytes(p->m, p->n, p->k);
 }
 
 extern "C" int oco_matmul_ws(uint32_t format, const void *w, const void *x, oco_dtype x_dtype, void *y,
@@ -619,7 +619,7 @@ extern "C" int oco_matmul_ws(uint32_t format, const void *w, const void *x, oco_
     OCO_TRY(matmul_check(format, w, x, x_dtype, y, y_dtype, bias, p));
     if (p->m == 0 || p->n == 0) return OCO_OK;
     if (use_mx(format)) {
-        const uint64_t need = mx_workspace_bytes(p->m, p->k);
+        const uint64_t need = mx_workspace_bytes(p->m, p->n, p->k);
         if (!workspace || workspace_bytes < need)
             return fail(OCO_ERR_INVALID, "oco_matmul_ws: workspace of %llu bytes, need %llu",
                         (unsigned long long)workspace_bytes, (unsigned long long)need);

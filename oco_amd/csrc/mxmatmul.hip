@@ -22,6 +22,11 @@
 //    elements 16..31 the same bytes of lane r + 32;
 //  * block b's scale is in lane r + 32b (A and B), byte chosen by op_sel.
 // The accumulator holds column l % 32, rows 8 (v / 4) + 4 (l / 32) + v % 4.
+#include <stdio.h>
+#include <stdlib.h>
+
+#include <algorithm>
+
 #include "stream.h"
 
 namespace oco {
@@ -59,77 +64,66 @@ __device__ __forceinline__ int mx_scale_exp(float amax) {
     return E < -127 ? -127 : E;
 }
 
+// One workgroup per record: four lanes per (row, block), each holding 8 of
+// the block's 32 values (q = lane % 4: values 8q .. 8q + 7).  The block's
+// maximum meets over the quad through DPP; in the record, chunk p of a
+// (term, block) interleaves groups p and p + 2 (byte 2i: value 8p + i,
+// byte 2i + 1: value 8p + 16 + i), so partner lanes q and q ^ 2 swap their
+// codes and each stores 8 of the chunk's 16 bytes.
 __global__ __launch_bounds__(256) void mx_split_kernel(MxSplitArgs a) {
-    const uint32_t rec = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (rec >= a.records) return;
+    const uint32_t rec = blockIdx.x;
     const uint32_t tile = rec / a.ksteps, s = rec % a.ksteps;
-    const int l = threadIdx.x & 63, r = l & 31, blk = l >> 5;
+    const int tid = threadIdx.x, q = tid & 3, pair = tid >> 2, r = pair & 31, blk = pair >> 5;
     const uint32_t row = tile * 32 + r, k0 = s * 64 + 32 * blk;
-    float v[32];
+    float v[8];
     if (row < a.m && k0 < a.k) {
-        const uint4 *src = reinterpret_cast<const uint4 *>(a.x + (uint64_t)row * a.k + k0);
+        const uint4 u = *reinterpret_cast<const uint4 *>(a.x + (uint64_t)row * a.k + k0 + 8 * q);
+        const uint32_t w4[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const uint4 u = src[q];
-            const uint32_t w4[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                v[8 * q + 2 * j] = __uint_as_float(w4[j] << 16);
-                v[8 * q + 2 * j + 1] = __uint_as_float(w4[j] & 0xffff0000u);
-            }
+        for (int j = 0; j < 4; j++) {
+            v[2 * j] = __uint_as_float(w4[j] << 16);
+            v[2 * j + 1] = __uint_as_float(w4[j] & 0xffff0000u);
         }
     } else {
 #pragma unroll
-        for (int i = 0; i < 32; i++) v[i] = 0.f;
+        for (int i = 0; i < 8; i++) v[i] = 0.f;
     }
     uint8_t *out = a.frag + (uint64_t)rec * MX_REC;
     uint32_t scales = 0;
 #pragma unroll
     for (int t = 0; t < 2; t++) {
-        float amax = 0.f;
-        bool nan = false;
+        // |x| bit patterns order like the values, with Inf above every
+        // finite value and NaN above Inf: the integer maximum carries both.
+        uint32_t m = 0;
 #pragma unroll
-        for (int i = 0; i < 32; i++) {
-            amax = fmaxf(amax, fabsf(v[i]));
-            nan |= v[i] != v[i];
-        }
-        if (nan) amax = __uint_as_float(0x7fc00000u);
-        const int E = mx_scale_exp(amax);
+        for (int i = 0; i < 8; i++) m = max(m, __float_as_uint(v[i]) & 0x7fffffffu);
+        m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0xB1, 0xf, 0xf, false));  // quad xor 1
+        m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x4E, 0xf, 0xf, false));  // quad xor 2
+        const int E = mx_scale_exp(__uint_as_float(m));
         scales |= (uint32_t)(E + 127) << (8 * t);
         const float inv = E == 128 ? 0.f : __builtin_ldexpf(1.f, -E), sc = E == 128 ? 0.f : __builtin_ldexpf(1.f, E);
-        uint32_t codes[8];  // 32 E4M3 codes, block value order
+        uint32_t c[2];  // codes of values 8q .. 8q + 3 and 8q + 4 .. 8q + 7
 #pragma unroll
-        for (int i = 0; i < 32; i += 4) {
-            int p = __builtin_amdgcn_cvt_pk_fp8_f32(v[i] * inv, v[i + 1] * inv, 0, false);
-            p = __builtin_amdgcn_cvt_pk_fp8_f32(v[i + 2] * inv, v[i + 3] * inv, p, true);
-            codes[i / 4] = (uint32_t)p;
+        for (int h = 0; h < 2; h++) {
+            int pk = __builtin_amdgcn_cvt_pk_fp8_f32(v[4 * h] * inv, v[4 * h + 1] * inv, 0, false);
+            pk = __builtin_amdgcn_cvt_pk_fp8_f32(v[4 * h + 2] * inv, v[4 * h + 3] * inv, pk, true);
+            c[h] = (uint32_t)pk;
+            v[4 * h] -= __builtin_amdgcn_cvt_f32_fp8(pk, 0) * sc;
+            v[4 * h + 1] -= __builtin_amdgcn_cvt_f32_fp8(pk, 1) * sc;
+            v[4 * h + 2] -= __builtin_amdgcn_cvt_f32_fp8(pk, 2) * sc;
+            v[4 * h + 3] -= __builtin_amdgcn_cvt_f32_fp8(pk, 3) * sc;
         }
-#pragma unroll
-        for (int q = 0; q < 8; q++) {
-            v[4 * q] -= __builtin_amdgcn_cvt_f32_fp8((int)codes[q], 0) * sc;
-            v[4 * q + 1] -= __builtin_amdgcn_cvt_f32_fp8((int)codes[q], 1) * sc;
-            v[4 * q + 2] -= __builtin_amdgcn_cvt_f32_fp8((int)codes[q], 2) * sc;
-            v[4 * q + 3] -= __builtin_amdgcn_cvt_f32_fp8((int)codes[q], 3) * sc;
-        }
-        // Lane r + 32p, byte e of this block: the value W keeps in nibble e & 1 of
-        // payload byte 8p + e / 2, i.e. value 8p + e / 2 + 16 (e & 1).
-#pragma unroll
-        for (int p = 0; p < 2; p++) {
-            uint32_t o[4];
-#pragma unroll
-            for (int d = 0; d < 4; d++) {
-                uint32_t word = 0;
-#pragma unroll
-                for (int bb = 0; bb < 4; bb++) {
-                    const int e = 4 * d + bb, idx = 8 * p + e / 2 + 16 * (e & 1);
-                    word |= ((codes[idx / 4] >> (8 * (idx & 3))) & 0xffu) << (8 * bb);
-                }
-                o[d] = word;
-            }
-            *reinterpret_cast<uint4 *>(out + ((t * 2 + blk) * 64 + r + 32 * p) * 16) = make_uint4(o[0], o[1], o[2], o[3]);
-        }
+        const uint32_t o0 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)c[0], 0x4E, 0xf, 0xf, false);
+        const uint32_t o1 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)c[1], 0x4E, 0xf, 0xf, false);
+        // Lane q < 2 (group p = q) stores bytes 0..7 of chunk p: its values
+        // 0..3 with the partner's; lane q >= 2 (group p + 2) bytes 8..15: the
+        // partner's values 4..7 with its own.
+        const uint32_t ev = q < 2 ? c[0] : o1, od = q < 2 ? o0 : c[1];
+        const uint32_t lo = __builtin_amdgcn_perm(od, ev, 0x05010400u), hi = __builtin_amdgcn_perm(od, ev, 0x07030602u);
+        const int p = q & 1;
+        *reinterpret_cast<uint2 *>(out + ((t * 2 + blk) * 64 + r + 32 * p) * 16 + (q >= 2 ? 8 : 0)) = make_uint2(lo, hi);
     }
-    *reinterpret_cast<uint32_t *>(out + MX_DATA + (r + 32 * blk) * 4) = scales;
+    if (q == 0) *reinterpret_cast<uint32_t *>(out + MX_DATA + (r + 32 * blk) * 4) = scales;
 }
 
 struct MxArgs {
@@ -140,21 +134,8 @@ struct MxArgs {
     uint32_t m, n, k, ksteps, tiles;
     uint64_t row_bytes;
     uint32_t y_bf16;
+    uint32_t wspan;  // weight bytes from the dword-aligned base, rounded up to 4 (< 4 GiB)
 };
-
-// Workgroup tile: 4 x NW wavefronts; wavefront (wm, wn) owns MI activation
-// row tiles of 32 and CW = CT / NW weight row tiles of 32 (workgroup tile
-// BM = 128 MI rows x BN = 32 CT columns).
-//  * A (the split activations) goes straight from the split records
-//    (16-byte lanes, coalesced) into registers, D steps ahead.
-//  * B (the GGUF bytes) is shared by the workgroup and staged through LDS:
-//    per K step of 64, each weight row's two blocks (34 bytes) are fetched
-//    as the dword-aligned span that holds them, ten consecutive lanes per
-//    row, so each byte crosses the address units once.  Three LDS buffers:
-//    at step t the MFMAs of t run on operands already in registers while
-//    the B fragments of t + 1 are read from LDS and B of t + 2 is written.
-// One barrier per step; the MFMA pipe never waits for LDS.
-constexpr int MX_BSLOT = 44;  // LDS bytes per weight row per step: 34 + alignment, 11 dwords (odd: no bank conflicts)
 
 template <int I>
 struct Int {
@@ -168,226 +149,270 @@ __device__ __forceinline__ void static_for(F &&f) {
     }
 }
 
-template <int MI, int CT, int NW, int D>
+typedef void (*MxFn)(MxArgs);
+
+// A buffer resource the compiler keeps in SGPRs: every field goes through
+// readfirstlane (the values are uniform; without this a resource built next
+// to divergent code may land in VGPRs and every load becomes a waterfall loop).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void *p, uint32_t bytes) {
+    const uint64_t v = (uint64_t)(uintptr_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return __builtin_amdgcn_make_buffer_rsrc((void *)(uintptr_t)(((uint64_t)hi << 32) | lo), 0,
+                                             __builtin_amdgcn_readfirstlane(bytes), 0x00020000);
+}
+
+// ---------------------------------------------------------------------------
+// Prefill tile: workgroup = four wavefronts, WM along the activation rows
+// and 4 / WM along the weight rows (output columns); each wavefront owns one
+// 32-row activation tile and CTW 32-column weight tiles, so a K step is
+// 2 CTW independent MFMAs (the two activation terms of every column tile).
+//
+// Sizing (measured on MI355X): an L2-resident operand stream reaches about
+// 33 bytes/clock per CU, and a 32x32x64 MFMA takes 64 clocks.  A workgroup
+// tile of BM rows x BN columns loads 2 BM x 64 bytes of activations and
+// 34 BN / 32 bytes of weights per K step.  At 128 x 96 (WM = 4) that is
+// 53 bytes per 384 MFMA clocks: the L2 stream, not the MFMA, sets the pace.
+// At 64 x 192 (WM = 2) the two wavefronts of a row tile read the same
+// activation records (the second from the CU's L1), and L2 traffic falls to
+// 39 bytes per 384 clocks for the same number of workgroups.
+//
+//  * A: each wavefront's split records go straight into a register ring RA
+//    K steps deep, through a buffer resource whose step offset is scalar.
+//  * B: GGUF rows staged a double step (4 blocks, 68 bytes) at a time: each
+//    thread moves whole blocks (the 20-byte dword-aligned span holding 17
+//    bytes), realigned into LDS as [block][row] 16-byte payloads and scale
+//    words whose byte (step parity) the MFMA's op_sel picks.  A register
+//    ring RB double steps deep feeds three LDS stages; one barrier per
+//    double step.
+template <int WM, int CTW, int RB>
 struct MxPlan {
-    static constexpr int THREADS = 256 * NW, CW = CT / NW;  // CW column tiles per wavefront
-    static constexpr int BM = 128 * MI, BN = 32 * CT;
-    static constexpr int BD = BN * 10, BU = (BD + THREADS - 1) / THREADS;  // B dwords per step, per thread
-    static constexpr int STAGE = BN * MX_BSLOT, LDS = 3 * STAGE;
-    static_assert(CT % NW == 0, "column tiles split evenly");
-    static_assert(D % 2 == 0 && D >= 2, "even ring depth");
+    static constexpr int WN = 4 / WM, BM = 32 * WM, BN = 32 * CTW * WN, BLOCKS = 4 * BN, BU = (BLOCKS + 255) / 256;
+    static constexpr int PAY = 4 * BN * 16, SCL = 2 * BN * 4, STAGE = PAY + SCL + 16;  // + landing pad of unused slots
+    static constexpr int NST = 3, LDS = NST * STAGE, RA = 6;
+    static_assert(WM * WN == 4, "four wavefronts");
+    static_assert(RB % 3 == 0 && RB >= 3, "the B ring is a whole number of LDS stage rounds");
 };
 
-template <int MI, int CT, int NW, int D>
-struct MxRing {
-    using P = MxPlan<MI, CT, NW, D>;
-    const uint8_t *arec[MI];  // this lane's records, step 0
-    const uint8_t *brow[P::BU];
-    uint32_t bdst[P::BU], bd[P::BU];
-    i32x8 ra[D][MI][2];  // A of step t in slot t % D: [tile][term], already in MFMA operand form
-    uint32_t rs[D][MI];
-    uint32_t rb[D][P::BU];  // B of step t (awaiting its LDS store) in slot t % D
-
-    __device__ __forceinline__ void init(const MxArgs &a, int tid, int lane, uint32_t tile0, uint32_t col0) {
-#pragma unroll
-        for (int i = 0; i < MI; i++)
-            arec[i] = a.frag + (uint64_t)min(tile0 + i, a.tiles - 1) * a.ksteps * MX_REC + lane * 16;
-#pragma unroll
-        for (int u = 0; u < P::BU; u++) {
-            const int f = min(tid + P::THREADS * u, P::BD - 1), col = f / 10;  // surplus lanes repeat the last dword
-            bd[u] = f % 10;
-            brow[u] = a.w + (uint64_t)min(col0 + col, a.n - 1) * a.row_bytes;
-            bdst[u] = col * MX_BSLOT + bd[u] * 4;
-        }
-    }
-    // Loads are unconditional (a step past the end re-reads the last one):
-    // a branch around a load makes the compiler wait for all loads at the join.
-    template <int SLOT>
-    __device__ __forceinline__ void load_a(const MxArgs &a, int lane, uint32_t s) {
-        s = min(s, a.ksteps - 1);
-#pragma unroll
-        for (int i = 0; i < MI; i++) {
-            const uint8_t *rec = arec[i] + (uint64_t)s * MX_REC;
-#pragma unroll
-            for (int t = 0; t < 2; t++) {
-                const uint4 lo = *reinterpret_cast<const uint4 *>(rec + (2 * t) * 1024);
-                const uint4 hi = *reinterpret_cast<const uint4 *>(rec + (2 * t + 1) * 1024);
-                ra[SLOT][i][t] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-            }
-            rs[SLOT][i] = *reinterpret_cast<const uint32_t *>(rec - lane * 16 + MX_DATA + lane * 4);
-        }
-    }
-    template <int SLOT>
-    __device__ __forceinline__ void load_b(const MxArgs &a, uint32_t s) {
-        s = min(s, a.ksteps - 1);
-        const uint32_t len = 2 * s + 1 < a.k / 32 ? 34 : 17;
-#pragma unroll
-        for (int u = 0; u < P::BU; u++) {
-            const uint8_t *p = brow[u] + (uint64_t)s * 34;
-            const uint32_t lo = (uint32_t)(uintptr_t)p & 3u, last = (lo + len - 1) / 4;
-            // only dwords holding bytes of this step's blocks
-            rb[SLOT][u] = *reinterpret_cast<const uint32_t *>(p - lo + 4 * min(bd[u], last));
-        }
-    }
-    template <int SLOT>
-    __device__ __forceinline__ void store_b(uint8_t *base) const {
-#pragma unroll
-        for (int u = 0; u < P::BU; u++) *reinterpret_cast<uint32_t *>(base + bdst[u]) = rb[SLOT][u];
-    }
-};
-
-template <int MI, int CT, int NW, int D>
-__global__ __launch_bounds__(256 * NW) void mx_matmul_kernel(MxArgs a) {
-    using P = MxPlan<MI, CT, NW, D>;
-    constexpr int CW = P::CW;
-    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];  // [3][STAGE]
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane & 31, part = lane >> 5;
-    const int wm = wave & 3, wn = wave >> 2;
-    // Logical (column tile, row tile), column-major per XCD: the row tiles of
-    // one weight column tile share its GGUF bytes in one L2, and each XCD's
-    // share of the split activations stays resident.
+template <int WM, int CTW, int RB>
+__global__ __launch_bounds__(256) void mx_matmul_kernel(MxArgs a) {
+    using P = MxPlan<WM, CTW, RB>;
+    constexpr int BN = P::BN, BU = P::BU, STAGE = P::STAGE, RA = P::RA, CT = CTW;
+    constexpr int PER = RB;  // double steps per unrolled round: RB, 3 stages and RA / 2 all divide it
+    static_assert(PER % 3 == 0 && (2 * PER) % RA == 0, "ring periods");
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    // The wavefront index is uniform: readfirstlane keeps the A resource in SGPRs.
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, c = lane & 31,
+              part = lane >> 5;
+    const int wm = wave % WM, wn = wave / WM;
+    // Logical (column tile, row group), column-major per XCD: the row groups
+    // of one weight column tile share its GGUF bytes in one L2.
     const uint32_t lin = xcd_order(blockIdx.x + gridDim.x * blockIdx.y, gridDim.x * gridDim.y);
     const uint32_t bx = lin / gridDim.y, by = lin % gridDim.y;
-    const uint32_t tile0 = by * (4 * MI) + wm * MI, col0 = bx * P::BN;
-    const uint32_t nblk = a.k / 32;
+    const uint32_t tile = by * WM + wm, col0 = bx * BN;
+    const uint32_t nblk = a.k / 32, nsteps = a.ksteps;
 
-    MxRing<MI, CT, NW, D> ring;
-    ring.init(a, tid, lane, tile0, col0);
-    uint32_t wlow[CW];  // weight row address mod 4 (fixes the span alignment)
+    // A: this wavefront's records; steps past the end read as zero.
+    const __amdgpu_buffer_rsrc_t ra_rs =
+        uniform_rsrc(a.frag + (uint64_t)min(tile, a.tiles - 1) * a.ksteps * MX_REC, a.ksteps * MX_REC);
+    // B: the tensor from its dword-aligned base; bytes past the end read as zero.
+    const uint32_t wsh = (uint32_t)((uintptr_t)a.w & 3u);
+    const __amdgpu_buffer_rsrc_t rb_rs = uniform_rsrc(a.w - wsh, a.wspan);
+    const uint32_t rbytes = (uint32_t)a.row_bytes;
+    // Staging: thread slot g = tid + 256 u moves block g % 4 of row g / 4 of
+    // each double step, realigned into the payload and scale arrays.
+    uint32_t boff[BU], bsh[BU], bpay[BU], bscl[BU];
 #pragma unroll
-    for (int j = 0; j < CW; j++)
-        wlow[j] = (uint32_t)(uintptr_t)(a.w + (uint64_t)min(col0 + (wn * CW + j) * 32 + c, a.n - 1) * a.row_bytes) & 3u;
+    for (int u = 0; u < BU; u++) {
+        const uint32_t g = tid + 256 * u, row = min(g / 4, (uint32_t)BN - 1), blk = g % 4;
+        const uint32_t at = wsh + min(col0 + row, a.n - 1) * rbytes + 17 * blk;
+        const bool live = g < (uint32_t)P::BLOCKS;
+        boff[u] = at & ~3u;
+        bsh[u] = at & 3u;
+        bpay[u] = live ? (blk * BN + row) * 16 : P::PAY + P::SCL;  // unused slots: the landing pad
+        bscl[u] = live ? P::PAY + ((blk & 1) * BN + row) * 4 + (blk >> 1) : P::PAY + P::SCL;
+    }
+    const uint32_t wcol = wn * CT * 32;  // this wavefront's first column within the tile
 
-    f32x16 acc[MI][CW];
+    i32x8 av[RA][2];
+    uint32_t as[RA];
+    u32x4 bv[RB][BU];
+    uint32_t bx4[RB][BU];
+    auto load_a = [&](auto slot, uint32_t s) {
+        constexpr int U = decltype(slot)::value;
+        const uint32_t so = s * MX_REC;
 #pragma unroll
-    for (int i = 0; i < MI; i++)
+        for (int t = 0; t < 2; t++) {
+            const u32x4 lo = __builtin_amdgcn_raw_buffer_load_b128(ra_rs, lane * 16 + 2 * t * 1024, so, 0);
+            const u32x4 hi = __builtin_amdgcn_raw_buffer_load_b128(ra_rs, lane * 16 + (2 * t + 1) * 1024, so, 0);
+            av[U][t] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+        }
+        as[U] = __builtin_amdgcn_raw_buffer_load_b32(ra_rs, MX_DATA + lane * 4, so, 0);
+    };
+    auto load_b = [&](auto slot, uint32_t j) {
+        constexpr int U = decltype(slot)::value;
 #pragma unroll
-        for (int j = 0; j < CW; j++) acc[i][j] = f32x16{};
-
-    i32x8 bf[2][CW];  // B fragments of steps of parity 0 / 1
-    int sb[2][CW];
-    auto frags = [&](auto par, uint32_t t) {  // B fragments of step t from LDS buffer t % 3
-        constexpr int PA = decltype(par)::value;
-        const uint8_t *base = lds + (t % 3) * P::STAGE;
-        const bool live = 2 * t + part < nblk;
-#pragma unroll
-        for (int j = 0; j < CW; j++) {
-            const uint8_t *row = base + ((wn * CW + j) * 32 + c) * MX_BSLOT;
-            const uint32_t off = ((wlow[j] + 34 * t) & 3u) + 17 * part;  // scale byte of block 2t + part
-            uint32_t q[4];
-            lds_bytes<16>(row + off + 1, q);
-            bf[PA][j] = live ? i32x8{(int)q[0], (int)q[1], (int)q[2], (int)q[3], 0, 0, 0, 0} : i32x8{};
-            sb[PA][j] = live ? row[off] : 127;
+        for (int u = 0; u < BU; u++) {
+            bv[U][u] = __builtin_amdgcn_raw_buffer_load_b128(rb_rs, boff[u], j * 68, 0);
+            bx4[U][u] = __builtin_amdgcn_raw_buffer_load_b32(rb_rs, boff[u] + 16, j * 68, 0);
         }
     };
-    auto mma = [&](auto slot, auto par) {
-        constexpr int SL = decltype(slot)::value, PA = decltype(par)::value;
+    auto store_b = [&](auto slot, auto stage) {
+        constexpr int U = decltype(slot)::value, S = decltype(stage)::value;
 #pragma unroll
-        for (int t = 0; t < 2; t++)
-#pragma unroll
-            for (int i = 0; i < MI; i++) {
-                const i32x8 &av = ring.ra[SL][i][t];
-#pragma unroll
-                for (int j = 0; j < CW; j++) {
-                    if (t == 0)
-                        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, bf[PA][j], acc[i][j], 0, 4, 0,
-                                                                                     (int)ring.rs[SL][i], 0, sb[PA][j]);
-                    else
-                        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, bf[PA][j], acc[i][j], 0, 4, 1,
-                                                                                     (int)ring.rs[SL][i], 0, sb[PA][j]);
-                }
-            }
+        for (int u = 0; u < BU; u++) {
+            const u32x4 v = bv[U][u];
+            const uint32_t w4 = bx4[U][u], sh = bsh[u];
+            // Span bytes: scale at sh, payload at sh + 1 .. sh + 16.
+            // alignbyte shifts by 0..3 bytes: a shift of 4 is the next dword.
+            const uint32_t sh1 = sh + 1;
+            const uint32_t d0 = sh1 == 4 ? v.y : __builtin_amdgcn_alignbyte(v.y, v.x, sh1);
+            const uint32_t d1 = sh1 == 4 ? v.z : __builtin_amdgcn_alignbyte(v.z, v.y, sh1);
+            const uint32_t d2 = sh1 == 4 ? v.w : __builtin_amdgcn_alignbyte(v.w, v.z, sh1);
+            const uint32_t d3 = sh1 == 4 ? w4 : __builtin_amdgcn_alignbyte(w4, v.w, sh1);
+            *reinterpret_cast<u32x4 *>(lds + S * STAGE + bpay[u]) = u32x4{d0, d1, d2, d3};
+            lds[S * STAGE + bscl[u]] = (uint8_t)(v.x >> (8 * sh));
+        }
     };
-    // One step t (u = t mod D): read B fragments of t + 1, multiply t, load
-    // A of t + D, store B of t + 2 to LDS and load B of t + 2 + D.
-    auto body = [&](auto u, uint32_t t) {
-        constexpr int U = decltype(u)::value, B2 = (U + 2) % D;
-        frags(Int<(U + 1) & 1>{}, t + 1);  // harmless past the end
-        mma(u, Int<U & 1>{});
-        ring.template load_a<U>(a, lane, t + D);
-        ring.template store_b<B2>(lds + ((t + 2) % 3) * P::STAGE);
-        ring.template load_b<B2>(a, t + 2 + D);
+
+    // One accumulator per column tile; a step issues term 0 over all tiles,
+    // then term 1, so consecutive MFMAs never share an accumulator.
+    f32x16 acc[CT];
+#pragma unroll
+    for (int j = 0; j < CT; j++) acc[j] = f32x16{};
+
+    // B fragments: payload per step (double-buffered by parity), scales per
+    // double step (byte = step parity, chosen by op_sel).
+    i32x8 bf[2][CT];
+    uint32_t sw[CT];
+    auto frag_read = [&](auto stage, auto par) {
+        constexpr int S = decltype(stage)::value, PA = decltype(par)::value;
+        const uint8_t *base = lds + S * STAGE;
+#pragma unroll
+        for (int j = 0; j < CT; j++) {
+            const u32x4 q = *reinterpret_cast<const u32x4 *>(base + ((2 * PA + part) * BN + wcol + j * 32 + c) * 16);
+            bf[PA][j] = i32x8{(int)q.x, (int)q.y, (int)q.z, (int)q.w, 0, 0, 0, 0};
+            if (PA == 0)
+                sw[j] = *reinterpret_cast<const uint32_t *>(base + P::PAY + (part * BN + wcol + j * 32 + c) * 4);
+        }
+    };
+    // Local K step s = 2 j + PA (A slot U): read step s + 1's payload (and,
+    // at the end of a double step, the next double step's scales) from LDS
+    // stage NS, then multiply step s.
+    auto step = [&](auto par, auto aslot, auto nstage, uint32_t s) {
+        constexpr int PA = decltype(par)::value, U = decltype(aslot)::value;
+        if (s < nsteps) {
+            uint32_t scl[CT];
+#pragma unroll
+            for (int j = 0; j < CT; j++) scl[j] = sw[j];
+            frag_read(nstage, Int<1 - PA>{});
+            // A block past K (odd block count, last step): its scale byte may be
+            // E8M0 255 (NaN); the activations there are zero, so scale 1 keeps it out.
+            const bool dead = part && (nblk & 1) && s == a.ksteps - 1;
+#pragma unroll
+            for (int j = 0; j < CT; j++) scl[j] = dead ? 0x7f7f7f7fu : scl[j];
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int j = 0; j < CT; j++) {
+                    if (t == 0)
+                        acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av[U][0], bf[PA][j], acc[j], 0, 4, 0,
+                                                                                  (int)as[U], PA, (int)scl[j]);
+                    else
+                        acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av[U][1], bf[PA][j], acc[j], 0, 4, 1,
+                                                                                  (int)as[U], PA, (int)scl[j]);
+                }
+        }
+    };
+
+    // Double step j (ring position Q = j mod PER): stage j % 3 holds B of j
+    // (steps 2j, 2j + 1) and stage (j + 1) % 3 B of j + 1 (read for step
+    // 2j + 2 before this round's barrier); B of j + 2 goes to stage
+    // (j + 2) % 3, last read before the previous barrier.
+    auto body = [&](auto q, uint32_t j) {
+        constexpr int Q = decltype(q)::value;
+        store_b(Int<(Q + 2) % RB>{}, Int<(Q + 2) % 3>{});
+        load_b(Int<(Q + 2) % RB>{}, j + 2 + RB);
+        step(Int<0>{}, Int<(2 * Q) % RA>{}, Int<Q % 3>{}, 2 * j);
+        load_a(Int<(2 * Q) % RA>{}, 2 * j + RA);
+        step(Int<1>{}, Int<(2 * Q + 1) % RA>{}, Int<(Q + 1) % 3>{}, 2 * j + 1);
+        load_a(Int<(2 * Q + 1) % RA>{}, 2 * j + 1 + RA);
         __syncthreads();
     };
 
-    static_for<D>([&](auto u) {
-        ring.template load_a<u.value>(a, lane, u.value);
-        ring.template load_b<u.value>(a, u.value);
-    });
-    ring.template store_b<0>(lds);
-    ring.template store_b<1>(lds + P::STAGE);
-    ring.template load_b<0>(a, D);
-    ring.template load_b<1>(a, D + 1);
+    // Prologue, in the order the first steps need the data.
+    load_b(Int<0>{}, 0);
+    load_b(Int<1>{}, 1);
+    static_for<RA>([&](auto u) { load_a(u, u.value); });
+    static_for<RB - 2>([&](auto u) { load_b(Int<u.value + 2>{}, u.value + 2); });
+    store_b(Int<0>{}, Int<0>{});
+    store_b(Int<1>{}, Int<1>{});
+    load_b(Int<0>{}, RB);
+    load_b(Int<1>{}, RB + 1);
     __syncthreads();
-    frags(Int<0>{}, 0);
-    uint32_t s = 0;
-    for (; s + D <= a.ksteps; s += D)  // whole rounds: no branch between a load and its use
-        static_for<D>([&](auto u) { body(u, s + u.value); });
-    static_for<D>([&](auto u) {
-        if (s + u.value < a.ksteps) body(u, s + u.value);
-    });
+    frag_read(Int<0>{}, Int<0>{});
+    const uint32_t nd = (nsteps + 1) / 2;
+    for (uint32_t j = 0; j < nd; j += PER)
+        static_for<PER>([&](auto q) { body(q, j + q.value); });
 
+    if (tile >= a.tiles) return;
 #pragma unroll
-    for (int j = 0; j < CW; j++) {
-        const uint32_t col = col0 + (wn * CW + j) * 32 + c;
+    for (int j = 0; j < CT; j++) {
+        const uint32_t col = col0 + wcol + j * 32 + c;
         if (col >= a.n) continue;
         const float bias = a.bias ? round_bf16(a.bias[col]) : 0.f;
 #pragma unroll
-        for (int i = 0; i < MI; i++)
-#pragma unroll
-            for (int v = 0; v < 16; v++) {
-                const uint32_t row = (tile0 + i) * 32 + 8 * (v / 4) + 4 * part + (v % 4);
-                if (row >= a.m) continue;
-                const float r = acc[i][j][v] + bias;
-                const uint64_t o = (uint64_t)row * a.n + col;
-                if (a.y_bf16)
-                    reinterpret_cast<uint16_t *>(a.y)[o] = f32_to_bf16_bits(r);
-                else
-                    reinterpret_cast<float *>(a.y)[o] = r;
-            }
+        for (int v = 0; v < 16; v++) {
+            const uint32_t row = tile * 32 + 8 * (v / 4) + 4 * part + (v % 4);
+            if (row >= a.m) continue;
+            const float r = acc[j][v] + bias;
+            const uint64_t o = (uint64_t)row * a.n + col;
+            if (a.y_bf16)
+                reinterpret_cast<uint16_t *>(a.y)[o] = f32_to_bf16_bits(r);
+            else
+                reinterpret_cast<float *>(a.y)[o] = r;
+        }
     }
 }
 
-uint64_t mx_workspace_bytes(uint32_t m, uint32_t k) {
+// Tile plan of one call: wavefronts along the activation rows (WM) and
+// column tiles per wavefront (CTW).
+struct MxTilePlan {
+    int wm, ctw;
+    uint32_t col_tiles, groups;
+};
+static MxTilePlan mx_plan(uint32_t m, uint32_t n) {
+    int wm = 4, ctw = 3;  // 128 x 96: measured fastest at 512 x 5760 x 2880
+    if (const char *env = getenv("OCO_MX_TILE")) {  // "wm,ctw" (tuning runs only)
+        int w2 = 0, c2 = 0;
+        if (sscanf(env, "%d,%d", &w2, &c2) == 2 && (w2 == 2 || w2 == 4) && (c2 == 3 || c2 == 6)) {
+            wm = w2;
+            ctw = c2;
+        }
+    }
+    MxTilePlan p;
+    p.wm = wm;
+    p.ctw = ctw;
+    const uint32_t bn = 32 * ctw * (4 / wm), bm = 32 * wm;
+    p.col_tiles = (n + bn - 1) / bn;
+    p.groups = (m + bm - 1) / bm;
+    return p;
+}
+
+uint64_t mx_workspace_bytes(uint32_t m, uint32_t n, uint32_t k) {
+    (void)n;
     return (uint64_t)((m + 31) / 32) * ((k + 63) / 64) * MX_REC;
 }
 
-typedef void (*MxFn)(MxArgs);
-
-template <int MI, int CT, int NW, int D>
-static MxFn mx_kernel(int &rows, int &cols, int &threads, size_t &lds) {
-    using P = MxPlan<MI, CT, NW, D>;
-    rows = P::BM;
-    cols = P::BN;
-    threads = P::THREADS;
-    lds = (size_t)P::LDS;
-    return mx_matmul_kernel<MI, CT, NW, D>;
-}
-
-// Tile shapes: workgroup rows x columns = 128 MI x 32 CT.  Measured on
-// MI355X: 128 x 64 with four wavefronts while 128 x 128 tiles would not
-// cover the 256 CUs (gpt-oss 5760 x 2880 at 512 tokens), else 128 x 192
-// with eight.
-static MxFn mx_pick(uint32_t m, uint32_t n, int &rows, int &cols, int &threads, size_t &lds) {
-    int choice = -1;
-    if (const char *env = getenv("OCO_MX_TILE")) choice = atoi(env);  // tuning runs only
-    if (choice < 0) {
-        const uint64_t big = (uint64_t)((m + 127) / 128) * ((n + 127) / 128);
-        choice = big < 256 ? 2 : 5;
-    }
-    switch (choice) {
-    case 1: return mx_kernel<1, 4, 1, 2>(rows, cols, threads, lds);  // 128 x 128, 4 waves
-    case 2: return mx_kernel<1, 2, 1, 2>(rows, cols, threads, lds);  // 128 x 64, 4 waves
-    case 3: return mx_kernel<1, 4, 2, 2>(rows, cols, threads, lds);  // 128 x 128, 8 waves
-    case 4: return mx_kernel<2, 2, 1, 2>(rows, cols, threads, lds);  // 256 x 64, 4 waves
-    case 5: return mx_kernel<1, 6, 2, 2>(rows, cols, threads, lds);  // 128 x 192, 8 waves
-    default: return mx_kernel<1, 2, 2, 2>(rows, cols, threads, lds);  // 128 x 64, 8 waves
-    }
+template <int WM, int CTW>
+static MxFn mx_kernel_fn(size_t &lds) {
+    lds = (size_t)MxPlan<WM, CTW, 3>::LDS;
+    return mx_matmul_kernel<WM, CTW, 3>;
 }
 
 int mx_matmul_launch(const void *w, const void *x, void *y, bool y_bf16, const float *bias, uint32_t m, uint32_t n,
                      uint32_t k, void *workspace, hipStream_t stream) {
     const uint32_t ksteps = (k + 63) / 64, tiles = (m + 31) / 32;
+    const MxTilePlan plan = mx_plan(m, n);
     MxSplitArgs sa;
     sa.x = (const uint16_t *)x;
     sa.frag = (uint8_t *)workspace;
@@ -395,11 +420,11 @@ int mx_matmul_launch(const void *w, const void *x, void *y, bool y_bf16, const f
     sa.k = k;
     sa.ksteps = ksteps;
     sa.records = tiles * ksteps;
-    hipLaunchKernelGGL(mx_split_kernel, dim3((sa.records + 3) / 4), dim3(256), 0, stream, sa);
+    hipLaunchKernelGGL(mx_split_kernel, dim3(sa.records), dim3(256), 0, stream, sa);
     OCO_TRY(launch_check("oco_matmul (mx split)"));
-    int rows, cols, threads;
-    size_t lds;
-    MxFn fn = mx_pick(m, n, rows, cols, threads, lds);
+    size_t lds = 0;
+    MxFn fn = plan.wm == 2 ? (plan.ctw == 3 ? mx_kernel_fn<2, 3>(lds) : mx_kernel_fn<2, 6>(lds))
+                           : (plan.ctw == 3 ? mx_kernel_fn<4, 3>(lds) : mx_kernel_fn<4, 6>(lds));
     if (lds > 64 * 1024)
         OCO_TRY(hip_check(hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
                           "hipFuncSetAttribute"));
@@ -415,7 +440,12 @@ int mx_matmul_launch(const void *w, const void *x, void *y, bool y_bf16, const f
     a.tiles = tiles;
     a.row_bytes = (uint64_t)(k / 32) * 17;
     a.y_bf16 = y_bf16;
-    hipLaunchKernelGGL(fn, dim3((n + cols - 1) / cols, (m + rows - 1) / rows), dim3(threads), lds, stream, a);
+    const uint64_t wspan = ((uint64_t)n * a.row_bytes + ((uintptr_t)w & 3u) + 3) & ~3ull;
+    if (wspan > 0xffffff00ull)
+        return fail(OCO_ERR_UNSUPPORTED, "oco_matmul: MXFP4 weight of %llu bytes (4 GiB limit)",
+                    (unsigned long long)wspan);
+    a.wspan = (uint32_t)wspan;
+    hipLaunchKernelGGL(fn, dim3(plan.col_tiles, plan.groups), dim3(256), lds, stream, a);
     return launch_check("oco_matmul (mx)");
 }
 

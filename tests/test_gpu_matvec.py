@@ -193,3 +193,27 @@ def test_matvec_exact_integer_answers(lib):
             say("matvec exact", fmt, xv)
             got, _ = run_matvec(lib, fmt, data, np.full(k, xv, np.float32), O.Matrix(k, n, 1, 0, 1, 1, 0))
             np.testing.assert_array_equal(got, np.full(n, k * xv, np.float32))
+
+
+STREAM_PLANS = ["1,1,1", "2,1,2", "1,2,2", "2,2,1", "2,4,1", "1,4,3"]
+
+
+@pytest.mark.parametrize("plan", STREAM_PLANS)
+def test_matvec_stream_plans(lib, plan, monkeypatch):
+    """Every streaming-kernel geometry (rows per half-wavefront, K split,
+    workgroups per CU) on ragged row counts, f32 and
+    bf16 activations, routed rows with bias."""
+    from oco_amd import synth
+    monkeypatch.setenv("OCO_STREAM_PLAN", plan)
+    for fmt, n, k in [(O.MXFP4, 131, 2880), (P.Q8_0, 77, 4096), (P.Q4_K, 257, 2048), (P.Q6_K, 300, 4096)]:
+        say("matvec plan", plan, fmt, n, k)
+        data = synth.weights(fmt, n, k, seed=11)
+        x = synth.activations(12, k)
+        check_matvec(lib, fmt, data, x, O.Matrix(k, n, 1, 0, 1, 1, 0))
+        check_matvec(lib, fmt, data, synth.bf16_bits(x), O.Matrix(k, n, 1, 0, 1, 1, 0), x_bf16=True, y_bf16=True)
+    E, n, k = 5, 45, 1024
+    data = synth.weights(P.Q6_K, E * n, k, seed=13)
+    ids = np.array([3, 0, 4, 1], np.uint32)
+    bias = np.random.default_rng(14).normal(size=E * n).astype(np.float32)
+    x = synth.activations(15, 2 * k).reshape(2, k)
+    check_matvec(lib, P.Q6_K, data, x, O.Matrix(k, n, 4, 0, 2, E, 2), bias=bias, ids=ids)
