@@ -113,6 +113,93 @@ class MatvecStack(Workload):
         return float(self.bytes)
 
 
+class LmHeadArgmax(Workload):
+    """The decode tail: Qwen3-8B lm_head [151936 x 4096] Q6_K with f32 logits,
+    then greedy argmax over them (Compute::argmax, compute.rs:132-140).
+    Work = lm_head weight bytes (the logits add 0.6 MB)."""
+    name = "lm_head_argmax_qwen3_8b"
+
+    def setup(self, oco, stream):
+        from oco_amd import synth
+        self.oco, self.stream = oco, stream
+        self.n, self.k = 151936, 4096
+        data = synth.weights(14, self.n, self.k, 34)
+        self.bytes = data.nbytes
+        self.w = oco.DeviceBuffer.from_array(data)
+        self.x = oco.DeviceBuffer.from_array(synth.activations(36, self.k))
+        self.y = oco.DeviceBuffer(self.n * 4)
+        self.tok = oco.DeviceBuffer(4)
+        self.ws_bytes = oco.argmax_workspace(self.n)
+        self.ws = oco.DeviceBuffer(max(self.ws_bytes, 4))
+        self.p = oco.Matrix(self.k, self.n, 1, 0, 1, 1, 0)
+
+    def launch(self, i):
+        self.oco.matvec(14, self.w, self.x, self.y, self.p, stream=self.stream)
+        self.oco.argmax(self.y, self.n, self.tok, stream=self.stream, workspace=self.ws,
+                        workspace_bytes=self.ws_bytes)
+
+    def work_per_step(self):
+        return float(self.bytes)
+
+
+class Argmax(Workload):
+    """argmax over Qwen3-8B's 151936 f32 logits alone (latency-bound; GB/s of logits)."""
+    name = "argmax_f32_151936"
+
+    def setup(self, oco, stream):
+        import numpy as np
+        self.oco, self.stream = oco, stream
+        self.n = 151936
+        self.y = oco.DeviceBuffer.from_array(np.random.default_rng(1).normal(size=self.n).astype(np.float32))
+        self.tok = oco.DeviceBuffer(4)
+        self.ws_bytes = oco.argmax_workspace(self.n)
+        self.ws = oco.DeviceBuffer(max(self.ws_bytes, 4))
+
+    def launch(self, i):
+        self.oco.argmax(self.y, self.n, self.tok, stream=self.stream, workspace=self.ws,
+                        workspace_bytes=self.ws_bytes)
+
+    def work_per_step(self):
+        return float(self.n * 4)
+
+
+class NormUpGate(Workload):
+    """Qwen3-8B FFN entry: RMS norm of the bf16 residual row, then ffn_up and
+    ffn_gate [12288 x 4096] Q4_K.  fused: the norm inside both matvecs'
+    activation staging (oco_matvec_norm); else oco_norm then two matvecs.
+    Work = the two weight matrices' bytes."""
+
+    def __init__(self, fused):
+        self.fused = fused
+        self.name = "norm_up_gate_qwen3_8b" + ("_fused" if fused else "_unfused")
+
+    def setup(self, oco, stream):
+        import numpy as np
+        from oco_amd import synth
+        self.oco, self.stream = oco, stream
+        self.n, self.k = 12288, 4096
+        self.mats = [oco.DeviceBuffer.from_array(synth.weights(12, self.n, self.k, s)) for s in (31, 32)]
+        self.bytes = 2 * self.n * (self.k // 256) * 144
+        self.x = oco.DeviceBuffer.from_array(synth.bf16_bits(synth.activations(37, self.k)))
+        self.nw = oco.DeviceBuffer.from_array((1 + 0.1 * np.random.default_rng(2).normal(size=self.k)).astype(np.float32))
+        self.normed = oco.DeviceBuffer(self.k * 2)
+        self.y = [oco.DeviceBuffer(self.n * 4) for _ in range(2)]
+        self.p = oco.Matrix(self.k, self.n, 1, 0, 1, 1, 0)
+
+    def launch(self, i):
+        o = self.oco
+        if self.fused:
+            for w, y in zip(self.mats, self.y):
+                o.matvec_norm(12, w, self.x, self.nw, 1e-6, y, self.p, True, stream=self.stream)
+        else:
+            o.norm(self.x, self.nw, self.normed, 1, self.k, 1e-6, True, stream=self.stream)
+            for w, y in zip(self.mats, self.y):
+                o.matvec(12, w, self.normed, y, self.p, o.DType.BF16, stream=self.stream)
+
+    def work_per_step(self):
+        return float(self.bytes)
+
+
 class MoeDecode(Workload):
     """gpt-oss-20b expert layer: 32 experts, gate/up [2880 x 2880] and down
     [2880 x 2880] MXFP4, top-4 of softmax(N(0,1) logits), clipped SwiGLU,
@@ -278,6 +365,10 @@ WORKLOADS = {
     "moe_decode_gpt_oss_b16": lambda: MoeDecode(16),
     "prefill_mxfp4_5760x2880_m512": lambda: Prefill("prefill_mxfp4_5760x2880_m512", 39, 5760, 2880, 512),
     "moe_prefill_qwen3_30b_a3b": MoePrefill,
+    "lm_head_argmax_qwen3_8b": LmHeadArgmax,
+    "argmax_f32_151936": Argmax,
+    "norm_up_gate_qwen3_8b_fused": lambda: NormUpGate(True),
+    "norm_up_gate_qwen3_8b_unfused": lambda: NormUpGate(False),
 }
 PEAK_TFLOPS = {"bf16": 2500.0, "fp4": 10100.0}
 HEADLINE = "mxfp4_decode_matvec_5760x2880"
@@ -404,7 +495,8 @@ def main():
         for name in ["q8_0_matvec_4096x4096", "q4_k_matvec_12288x4096", "q6_k_matvec_4096x12288",
                      "q6_k_lm_head_151936x4096", "qwen3_8b_q4km_decode_stack", "moe_decode_gpt_oss_b1",
                      "moe_decode_gpt_oss_b4", "moe_decode_gpt_oss_b16", "prefill_mxfp4_5760x2880_m512",
-                     "moe_prefill_qwen3_30b_a3b"]:
+                     "moe_prefill_qwen3_30b_a3b", "lm_head_argmax_qwen3_8b", "argmax_f32_151936",
+                     "norm_up_gate_qwen3_8b_fused", "norm_up_gate_qwen3_8b_unfused"]:
             if name == wl.name:
                 continue
             w2 = WORKLOADS[name]()

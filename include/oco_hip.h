@@ -271,6 +271,42 @@ int oco_expert_expand(const oco_experts *w, const void *x, oco_dtype x_dtype,
 int oco_moe_sum(const void *routes, oco_dtype routes_dtype, const float *probs, uint16_t *out,
                 uint32_t hidden, uint32_t tokens, uint32_t k, oco_stream stream);
 
+/* ---- the steps either side of the decode matvec -------------------------- */
+
+/* RMS normalisation of `rows` bf16 rows of n: y = bf16(x * inv * w) with
+ * inv = 1/sqrt(mean(x^2) + epsilon); full_layer == 0 rounds x * inv and w to
+ * bf16 before the product, as the reference does.  w: f32 [n].
+ * Replaces Compute::norm / the norm kernel (elementwise.metal:6-28). */
+int oco_norm(const void *x, const float *w, void *y, uint32_t rows, uint32_t n, float epsilon,
+             int full_layer, oco_stream stream);
+
+/* Residual add then normalisation: x = bf16(x + y) (x is updated in place,
+ * the residual stream), out = norm(x).  Replaces add_norm
+ * (elementwise.metal:32-58). */
+int oco_add_norm(void *x, const void *y, const float *w, void *out, uint32_t rows, uint32_t n,
+                 float epsilon, int full_layer, oco_stream stream);
+
+/* oco_matvec whose bf16 input rows are RMS-normalised on the way in (the
+ * norm fused into the matvec's activation staging): the result equals
+ * oco_norm followed by oco_matvec with bf16 x, bit for bit, without the
+ * normalised row ever reaching memory.  Replaces the norm -> matvec pair of
+ * the reference's layer step (elementwise.metal:6-28 feeding
+ * vector.metal:66-394). */
+int oco_matvec_norm(uint32_t format, const void *w, const void *x, const float *norm_w, float epsilon,
+                    int full_layer, void *y, oco_dtype y_dtype, const float *bias,
+                    const uint32_t *ids, const oco_matrix *p, oco_stream stream);
+
+/* Greedy token selection over n f32 logits: out[0] = index of the largest
+ * value (ties: lowest index; -0 == +0), or 0xffffffff if any logit is Inf or
+ * NaN or n == 0.  Replaces Compute::argmax / argmax_f32
+ * (compute.rs:132-140, argmax.metal:1-47). */
+int oco_argmax_f32(const float *logits, uint32_t n, uint32_t *out, oco_stream stream);
+/* Workspace form: the partial results of large n live in caller memory of
+ * oco_argmax_workspace(n) bytes (0: none needed). */
+uint64_t oco_argmax_workspace(uint32_t n);
+int oco_argmax_f32_ws(const float *logits, uint32_t n, uint32_t *out, void *workspace,
+                      uint64_t workspace_bytes, oco_stream stream);
+
 #ifdef __cplusplus
 }
 #endif

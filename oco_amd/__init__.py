@@ -136,6 +136,12 @@ SIGNATURES = {
     "oco_experts_apply": (_i32, [_EP, _vp, _i32, _vp, _vp, _u32, _vp, _vp, _vp, _u64, _vp]),
     "oco_expert_expand": (_i32, [_EP, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
     "oco_moe_sum": (_i32, [_vp, _i32, _vp, _vp, _u32, _u32, _u32, _vp]),
+    "oco_norm": (_i32, [_vp, _vp, _vp, _u32, _u32, ctypes.c_float, _i32, _vp]),
+    "oco_add_norm": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, ctypes.c_float, _i32, _vp]),
+    "oco_matvec_norm": (_i32, [_u32, _vp, _vp, _vp, ctypes.c_float, _i32, _vp, _i32, _vp, _vp, _MP, _vp]),
+    "oco_argmax_f32": (_i32, [_vp, _u32, _vp, _vp]),
+    "oco_argmax_workspace": (_u64, [_u32]),
+    "oco_argmax_f32_ws": (_i32, [_vp, _u32, _vp, _vp, _u64, _vp]),
 }
 
 _lib = None
@@ -373,6 +379,40 @@ def route_plan(ids, routes, experts, tile_rows, up_tiles, down_tiles, plan, stre
 def moe_sum(routes, routes_dtype, probs, out, hidden, tokens, k, stream=None):
     _check(load_library().oco_moe_sum(_addr(routes), int(routes_dtype), _addr(probs), _addr(out),
                                       hidden, tokens, k, _stream(stream)))
+
+
+def norm(x, w, y, rows: int, n: int, epsilon: float, full_layer: bool = True, stream=None):
+    """Compute::norm (elementwise.metal:6-28) over bf16 rows."""
+    _check(load_library().oco_norm(_addr(x), _addr(w), _addr(y), rows, n, epsilon, int(full_layer),
+                                   _stream(stream)))
+
+
+def add_norm(x, y, w, out, rows: int, n: int, epsilon: float, full_layer: bool = True, stream=None):
+    """add_norm (elementwise.metal:32-58): x = bf16(x + y) in place, out = norm(x)."""
+    _check(load_library().oco_add_norm(_addr(x), _addr(y), _addr(w), _addr(out), rows, n, epsilon,
+                                       int(full_layer), _stream(stream)))
+
+
+def matvec_norm(fmt: int, w, x, norm_w, epsilon: float, y, p: Matrix, full_layer: bool = True,
+                y_dtype=DType.F32, bias=None, ids=None, stream=None):
+    """norm -> matvec with the norm fused into the matvec's activation staging."""
+    _check(load_library().oco_matvec_norm(int(fmt), _addr(w), _addr(x), _addr(norm_w), epsilon,
+                                          int(full_layer), _addr(y), int(y_dtype), _addr(bias), _addr(ids),
+                                          ctypes.byref(as_matrix(p)), _stream(stream)))
+
+
+def argmax_workspace(n: int) -> int:
+    return int(load_library().oco_argmax_workspace(n))
+
+
+def argmax(logits, n: int, out, stream=None, workspace=None, workspace_bytes: int = 0):
+    """Compute::argmax (compute.rs:132-140): greedy token over f32 logits."""
+    lib = load_library()
+    if workspace is None:
+        _check(lib.oco_argmax_f32(_addr(logits), n, _addr(out), _stream(stream)))
+    else:
+        _check(lib.oco_argmax_f32_ws(_addr(logits), n, _addr(out), _addr(workspace), int(workspace_bytes),
+                                     _stream(stream)))
 
 
 # ---- operator mirror -----------------------------------------------------------

@@ -18,6 +18,7 @@
 #include <algorithm>
 
 #include "stream.h"
+#include "norm.h"
 
 namespace oco {
 
@@ -135,6 +136,11 @@ struct StreamArgs {
     uint32_t ks;            // wavefronts sharing a row set (K slices)
     uint32_t slice_blocks;  // blocks per K slice
     uint32_t ngroups;       // row groups per route
+    // Fused RMS norm of the (bf16) input row during staging: 0 off, 1 norm,
+    // 2 norm with full_layer rounding (elementwise.metal:6-28).
+    uint32_t norm_mode;
+    float norm_eps;
+    const float *norm_w;
 };
 
 // Loads per tile row: enough 16-byte chunks for NPL pieces per lane of a
@@ -208,9 +214,15 @@ __global__ __launch_bounds__(256) void stream_kernel(StreamArgs a) {
     uint32_t g = blockIdx.x;
     if (g < a.ngroups) issue(g);
 
-    // Stage x (f32) in piece-major order, then the per-piece sums.
+    // Stage x (f32) in piece-major order, then the per-piece sums.  With a
+    // fused norm, x is the bf16 row before normalisation: every workgroup
+    // takes its inverse RMS (the same routine and order as oco_norm, so the
+    // staged values equal oco_norm's output bit for bit) and normalises
+    // while staging.
     {
         const XT *xr = reinterpret_cast<const XT *>(a.x) + (uint64_t)input * p.k;
+        float inv = 1.f;
+        if (a.norm_mode) inv = block_inv_rms(reinterpret_cast<const uint16_t *>(xr), p.k, a.norm_eps, part);
         // Four loads in flight per thread before any store: x arrives in one
         // memory round trip, not one per loop iteration.
         for (uint32_t f0 = threadIdx.x; f0 < p.k / 4; f0 += 4 * 256) {
@@ -233,6 +245,19 @@ __global__ __launch_bounds__(256) void stream_kernel(StreamArgs a) {
             for (int u = 0; u < 4; u++) {
                 const uint32_t f = f0 + 256 * u;
                 if (f < p.k / 4) {
+                    if (a.norm_mode) {
+                        float wn[4];
+                        if (((uintptr_t)a.norm_w & 15u) == 0) {
+                            const float4 t = reinterpret_cast<const float4 *>(a.norm_w)[f];
+                            wn[0] = t.x; wn[1] = t.y; wn[2] = t.z; wn[3] = t.w;
+                        } else {
+#pragma unroll
+                            for (int e = 0; e < 4; e++) wn[e] = a.norm_w[4 * f + e];
+                        }
+#pragma unroll
+                        for (int e = 0; e < 4; e++)
+                            v[u][e] = bf16_bits_to_f32(norm_value_bits(v[u][e], inv, wn[e], a.norm_mode == 2));
+                    }
                     uint32_t pp, tt;
                     T::map(f, pp, tt);
                     xs4[tt * PT + pp] = make_float4(v[u][0], v[u][1], v[u][2], v[u][3]);
@@ -457,9 +482,18 @@ MatvecPlan matvec_plan(uint32_t fmt, uint32_t k, uint32_t n, uint32_t m) {
 
 using namespace oco;
 
-extern "C" int oco_matvec(uint32_t format, const void *w, const void *x, oco_dtype x_dtype, void *y,
-                          oco_dtype y_dtype, const float *bias, const uint32_t *ids,
-                          const oco_matrix *p, oco_stream stream) {
+struct NormSpec {
+    const float *w;
+    float epsilon;
+    int full_layer;
+};
+
+// oco_matvec, optionally with the RMS norm of each bf16 input row fused
+// into the streaming kernel's staging (norm != nullptr, x bf16).  Formats
+// without a streaming kernel normalise into a stream-ordered temporary first.
+static int matvec_impl(uint32_t format, const void *w, const void *x, oco_dtype x_dtype, void *y,
+                       oco_dtype y_dtype, const float *bias, const uint32_t *ids, const oco_matrix *p,
+                       const NormSpec *norm, oco_stream stream) {
     if (!p || !w || !x || !y) return fail(OCO_ERR_INVALID, "oco_matvec: null argument");
     uint32_t e, bb;
     OCO_TRY(oco_block_layout(format, &e, &bb));
@@ -517,6 +551,9 @@ extern "C" int oco_matvec(uint32_t format, const void *w, const void *x, oco_dty
             a.y_bf16 = (y_dtype == OCO_DT_BF16) && !routed_f32;
             a.ks = sp.ks;
             a.slice_blocks = slice_blocks;
+            a.norm_mode = norm ? (norm->full_layer ? 2u : 1u) : 0u;
+            a.norm_eps = norm ? norm->epsilon : 0.f;
+            a.norm_w = norm ? norm->w : nullptr;
             const uint32_t rows_per_group = (4 / sp.ks) * 2 * sp.r;
             a.ngroups = (p->n + rows_per_group - 1) / rows_per_group;
             const uint32_t nsum = format == OCO_Q8_0 ? 1 : format == OCO_Q4_K ? 2 : format == OCO_Q6_K ? 4 : 0;
@@ -532,6 +569,17 @@ extern "C" int oco_matvec(uint32_t format, const void *w, const void *x, oco_dty
             hipLaunchKernelGGL(fn, dim3(grid, p->m), dim3(256), lds, (hipStream_t)stream, a);
             return launch_check("oco_matvec");
         }
+    }
+    if (norm) {  // no streaming kernel: normalise the input rows, then the plain matvec
+        const uint32_t in_rows =
+            (p->experts > 1 && !p->route_major) ? (p->m + p->routes - 1) / p->routes : p->m;
+        void *tmp = nullptr;
+        const size_t bytes = (size_t)in_rows * p->k * 2;
+        OCO_TRY(hip_check(hipMallocAsync(&tmp, bytes, (hipStream_t)stream), "oco_matvec_norm: hipMallocAsync"));
+        int rc = oco_norm(x, norm->w, tmp, in_rows, p->k, norm->epsilon, norm->full_layer, stream);
+        if (rc == OCO_OK) rc = matvec_impl(format, w, tmp, OCO_DT_BF16, y, y_dtype, bias, ids, p, nullptr, stream);
+        const int rc2 = hip_check(hipFreeAsync(tmp, (hipStream_t)stream), "oco_matvec_norm: hipFreeAsync");
+        return rc != OCO_OK ? rc : rc2;
     }
     MatvecPlan plan = matvec_plan(format, p->k, p->n, p->m);
     MatvecFn fn = x_dtype == OCO_DT_F32 ? pick_format<float>(format, plan.r, plan.ks)
@@ -551,4 +599,18 @@ extern "C" int oco_matvec(uint32_t format, const void *w, const void *x, oco_dty
     dim3 grid((p->n + rows_per_group - 1) / rows_per_group, p->m);
     hipLaunchKernelGGL(fn, grid, dim3(256), 0, (hipStream_t)stream, a);
     return launch_check("oco_matvec");
+}
+
+extern "C" int oco_matvec(uint32_t format, const void *w, const void *x, oco_dtype x_dtype, void *y,
+                          oco_dtype y_dtype, const float *bias, const uint32_t *ids,
+                          const oco_matrix *p, oco_stream stream) {
+    return matvec_impl(format, w, x, x_dtype, y, y_dtype, bias, ids, p, nullptr, stream);
+}
+
+extern "C" int oco_matvec_norm(uint32_t format, const void *w, const void *x, const float *norm_w, float epsilon,
+                               int full_layer, void *y, oco_dtype y_dtype, const float *bias,
+                               const uint32_t *ids, const oco_matrix *p, oco_stream stream) {
+    if (!norm_w) return fail(OCO_ERR_INVALID, "oco_matvec_norm: null norm weights");
+    const NormSpec n{norm_w, epsilon, full_layer};
+    return matvec_impl(format, w, x, OCO_DT_BF16, y, y_dtype, bias, ids, p, &n, stream);
 }

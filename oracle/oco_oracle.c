@@ -28,6 +28,13 @@
  *   - oo_swiglu_clipped: closed form in fp64 (mxfp4.rs:139-147) and the
  *     NaN/Inf propagation rules.
  *   - oo_moe_sum: hand-computed cases and the bf16 rounding points.
+ *   - oo_argmax_f32: the reference's own known answers
+ *     (src/weights/dispatch_tests/numerics.rs:14-69: every non-finite class
+ *     at index 2049 of 2051, signed zeros, ties at 31/32, 1023/1024,
+ *     1024/2048) and brute force against numpy's argmax on finite data.
+ *   - oo_norm / oo_add_norm: the fp64 closed form checked against numpy
+ *     (rms of a constant row is the constant; scaling x leaves y unchanged up
+ *     to rounding; full_layer 0 and 1 differ only in the rounding point).
  * The fp32 summation order of the Metal kernels is not reproducible without
  * Metal; it is bounded, not pinned (the tests use relative L2 and the bound).
  */
@@ -414,4 +421,56 @@ void oo_moe_sum(const uint16_t *routes, const float *probs, uint16_t *out,
             s += oo_bf16(routes[(t * k + r) * hidden + d]) * probs[t * k + r];
         out[i] = oo_f32_to_bf16(oo_bf16(out[i]) + oo_bf16(oo_f32_to_bf16(s)));
     }
+}
+
+/* Greedy token selection: shaders/argmax.metal:1-47.  Finite logits order as
+ * integers after folding the sign (-0 counts as +0); ties go to the lowest
+ * index; any Inf or NaN makes the answer 0xffffffff, as does n == 0. */
+uint32_t oo_argmax_f32(const float *logits, uint32_t n) {
+    uint32_t val = 0, id = 0xffffffffu;
+    for (uint32_t i = 0; i < n; i++) {
+        uint32_t bits;
+        memcpy(&bits, &logits[i], 4);
+        if ((bits & 0x7f800000u) == 0x7f800000u) return 0xffffffffu;
+        bits = (bits & 0x7fffffffu) == 0 ? 0u : bits;
+        const uint32_t v = bits ^ ((bits & 0x80000000u) ? 0xffffffffu : 0x80000000u);
+        if (v > val) {
+            val = v;
+            id = i;
+        }
+    }
+    return id;
+}
+
+/* RMS normalisation of bf16 rows: elementwise.metal:6-28.
+ * inv = 1 / sqrt(mean(x^2) + epsilon) in fp64; y = bf16(x inv w) when
+ * full_layer, else bf16(bf16(x inv) * bf16(w)) (the two rounding points of
+ * the reference).  Returns the f64 row values before the final rounding in
+ * `exact` (may be NULL) so tests can bound the rounding. */
+void oo_norm(const uint16_t *x, const float *w, uint16_t *y, double *exact, uint32_t rows, uint32_t n,
+             float epsilon, int full_layer) {
+    for (uint32_t r = 0; r < rows; r++) {
+        const uint16_t *xr = x + (uint64_t)r * n;
+        double s = 0;
+        for (uint32_t i = 0; i < n; i++) {
+            const double v = oo_bf16(xr[i]);
+            s += v * v;
+        }
+        const double inv = 1.0 / sqrt(s / n + (double)epsilon);
+        for (uint32_t i = 0; i < n; i++) {
+            const double t = oo_bf16(xr[i]) * inv;
+            const double v = full_layer ? t * (double)w[i]
+                                        : (double)oo_bf16(oo_f32_to_bf16((float)t)) * oo_bf16(oo_f32_to_bf16(w[i]));
+            if (exact) exact[(uint64_t)r * n + i] = v;
+            y[(uint64_t)r * n + i] = oo_f32_to_bf16((float)v);
+        }
+    }
+}
+
+/* Residual add then normalisation: elementwise.metal:32-58.  x (the
+ * residual stream, bf16) becomes bf16(x + y); out is its normalised form. */
+void oo_add_norm(uint16_t *x, const uint16_t *y, const float *w, uint16_t *out, double *exact, uint32_t rows,
+                 uint32_t n, float epsilon, int full_layer) {
+    for (uint64_t i = 0; i < (uint64_t)rows * n; i++) x[i] = oo_f32_to_bf16(oo_bf16(x[i]) + oo_bf16(y[i]));
+    oo_norm(x, w, out, exact, rows, n, epsilon, full_layer);
 }

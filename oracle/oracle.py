@@ -59,6 +59,10 @@ def lib():
         L.oo_route_plan.argtypes = [vp, u32, u32, u32, u32, u32, vp]
         L.oo_route_plan.restype = u64
         L.oo_moe_sum.argtypes = [vp, vp, vp, u32, u32, u32]
+        L.oo_argmax_f32.argtypes = [vp, u32]
+        L.oo_argmax_f32.restype = u32
+        L.oo_norm.argtypes = [vp, vp, vp, vp, u32, u32, ctypes.c_float, i32]
+        L.oo_add_norm.argtypes = [vp, vp, vp, vp, vp, u32, u32, ctypes.c_float, i32]
         _lib = L
     return _lib
 
@@ -275,3 +279,32 @@ def matmul_reference(fmt, w, x, n, k, half_operands: bool):
         W = W.astype(np.float16).astype(np.float64)
         X = X.astype(np.float16).astype(np.float64)
     return X @ W.T, np.abs(X) @ np.abs(W).T
+
+
+def argmax_f32(logits: np.ndarray) -> int:
+    """Greedy selection (argmax.metal:1-47); 0xffffffff for any non-finite logit."""
+    x = np.ascontiguousarray(logits, np.float32)
+    return int(lib().oo_argmax_f32(_p(x), x.size))
+
+
+def norm(x_bf16: np.ndarray, w: np.ndarray, epsilon: float, full_layer: bool):
+    """RMS norm of bf16 rows (elementwise.metal:6-28): (bf16 bits, f64 values before rounding)."""
+    x = np.ascontiguousarray(x_bf16, np.uint16)
+    rows, n = x.shape
+    w = np.ascontiguousarray(w, np.float32)
+    y = np.empty_like(x)
+    exact = np.empty(x.shape, np.float64)
+    lib().oo_norm(_p(x), _p(w), _p(y), _p(exact), rows, n, epsilon, 1 if full_layer else 0)
+    return y, exact
+
+
+def add_norm(x_bf16: np.ndarray, y_bf16: np.ndarray, w: np.ndarray, epsilon: float, full_layer: bool):
+    """Residual add then norm (elementwise.metal:32-58): (new residual, normed, f64 values)."""
+    x = np.ascontiguousarray(x_bf16, np.uint16).copy()
+    y = np.ascontiguousarray(y_bf16, np.uint16)
+    rows, n = x.shape
+    w = np.ascontiguousarray(w, np.float32)
+    out = np.empty_like(x)
+    exact = np.empty(x.shape, np.float64)
+    lib().oo_add_norm(_p(x), _p(y), _p(w), _p(out), _p(exact), rows, n, epsilon, 1 if full_layer else 0)
+    return x, out, exact

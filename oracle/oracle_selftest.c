@@ -17,6 +17,9 @@ float oo_swiglu_clipped(float, float);
 uint64_t oo_route_plan_words(uint32_t, uint32_t);
 uint64_t oo_route_plan(const uint32_t *, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t *);
 void oo_moe_sum(const uint16_t *, const float *, uint16_t *, uint32_t, uint32_t, uint32_t);
+uint32_t oo_argmax_f32(const float *, uint32_t);
+void oo_norm(const uint16_t *, const float *, uint16_t *, double *, uint32_t, uint32_t, float, int);
+void oo_add_norm(uint16_t *, const uint16_t *, const float *, uint16_t *, double *, uint32_t, uint32_t, float, int);
 
 int main(void) {
     const uint32_t fmts[] = {0, 1, 2, 3, 8, 12, 13, 14, 30, 39};
@@ -56,6 +59,17 @@ int main(void) {
     uint16_t r16[4 * 2 * 3] = {0}, o16[2 * 3] = {0};
     float pr[8] = {.25f, .25f, .25f, .25f, .5f, .5f, 0, 0};
     oo_moe_sum(r16, pr, o16, 3, 2, 4);
+    if (oo_argmax_f32(logits, 128) >= 128 || oo_argmax_f32(logits, 0) != 0xffffffffu) return 6;
+    uint16_t xb[2 * 96], yb[2 * 96], nb[2 * 96];
+    float nw[96];
+    double ex[2 * 96];
+    for (int i = 0; i < 2 * 96; i++) {
+        xb[i] = (uint16_t)(0x3f00 + rand() % 256);
+        yb[i] = (uint16_t)(0xbf00 + rand() % 256);
+    }
+    for (int i = 0; i < 96; i++) nw[i] = 1.0f + (float)i / 96;
+    oo_norm(xb, nw, nb, ex, 2, 96, 1e-6f, 0);
+    oo_add_norm(xb, yb, nw, nb, NULL, 2, 96, 1e-6f, 1);
     puts("oracle selftest ok");
     return 0;
 }

@@ -324,3 +324,55 @@ def test_oracle_under_sanitizers():
     assert r.returncode == 0, r.stderr
     r = subprocess.run([os.path.join(here, "oracle_asan")], capture_output=True, text=True)
     assert r.returncode == 0, r.stdout + r.stderr
+
+
+def test_argmax_reference_known_answers():
+    """The reference's own cases (numerics.rs:14-69)."""
+    import argmax_cases as A
+    for bits, want in A.cases():
+        assert O.argmax_f32(A.logits(bits)) == want
+    assert O.argmax_f32(np.zeros(0, np.float32)) == A.NONE
+
+
+def test_argmax_brute_force_finite():
+    rng = np.random.default_rng(3)
+    for n in (1, 5, 1000, 151936):
+        x = rng.normal(size=n).astype(np.float32)
+        assert O.argmax_f32(x) == int(np.argmax(x))
+        x = np.round(x * 2).astype(np.float32)  # many ties: numpy also keeps the first
+        assert O.argmax_f32(x) == int(np.argmax(x))
+
+
+def test_norm_closed_forms():
+    n = 256
+    # a constant row c normalises to c / sqrt(c^2 + eps) = 1 (eps -> 0)
+    x = O.f32_to_bf16(np.full((1, n), 3.0, np.float32)).reshape(1, n)
+    y, exact = O.norm(x, np.ones(n, np.float32), 0.0, True)
+    assert np.allclose(exact, 1.0, rtol=0, atol=1e-12) and np.all(O.bf16_to_f32(y) == 1.0)
+    # numpy fp64 restatement of the same formula on random rows, both rounding modes
+    rng = np.random.default_rng(4)
+    xr = O.f32_to_bf16(rng.normal(size=(3, n)).astype(np.float32)).reshape(3, n)
+    w = rng.normal(size=n).astype(np.float32)
+    X = O.bf16_to_f32(xr).astype(np.float64).reshape(3, n)
+    inv = 1.0 / np.sqrt((X * X).mean(axis=1, keepdims=True) + 1e-5)
+    y1, e1 = O.norm(xr, w, 1e-5, True)
+    assert np.allclose(e1, X * inv * w.astype(np.float64), rtol=1e-6, atol=0)
+    y0, e0 = O.norm(xr, w, 1e-5, False)
+    want0 = O.bf16_round((X * inv).astype(np.float32)).astype(np.float64) * O.bf16_round(w).astype(np.float64)
+    assert np.allclose(e0, want0, rtol=1e-6, atol=0)
+    # scale invariance: 4x the row gives the same normalised row (powers of two are exact in bf16)
+    y4, _ = O.norm(O.f32_to_bf16(X.astype(np.float32) * 4).reshape(3, n), w, 0.0, True)
+    yz, _ = O.norm(xr, w, 0.0, True)
+    assert np.array_equal(y4, yz)
+
+
+def test_add_norm_is_add_then_norm():
+    rng = np.random.default_rng(5)
+    n = 96
+    x = O.f32_to_bf16(rng.normal(size=(2, n)).astype(np.float32)).reshape(2, n)
+    y = O.f32_to_bf16(rng.normal(size=(2, n)).astype(np.float32)).reshape(2, n)
+    w = rng.normal(size=n).astype(np.float32)
+    xs, out, _ = O.add_norm(x, y, w, 1e-6, True)
+    want_x = O.f32_to_bf16((O.bf16_to_f32(x) + O.bf16_to_f32(y)).astype(np.float32)).reshape(2, n)
+    assert np.array_equal(xs, want_x)
+    assert np.array_equal(out, O.norm(want_x, w, 1e-6, True)[0])
