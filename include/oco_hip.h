@@ -40,7 +40,8 @@ enum {
     OCO_ERR_INVALID = 1,     /* bad argument or geometry (Error::Request)      */
     OCO_ERR_UNSUPPORTED = 2, /* format/variant without a kernel               */
     OCO_ERR_HIP = 3,         /* HIP runtime failure (Error::Gpu)              */
-    OCO_ERR_MEMORY = 4       /* allocation failure                            */
+    OCO_ERR_MEMORY = 4,      /* allocation failure                            */
+    OCO_ERR_CHECKPOINT = 5   /* malformed or unsupported GGUF (Error::Checkpoint) */
 };
 
 /* GGUF format codes: src/tensor.rs:9-20 (WeightFormat). */
@@ -306,6 +307,61 @@ int oco_argmax_f32(const float *logits, uint32_t n, uint32_t *out, oco_stream st
 uint64_t oco_argmax_workspace(uint32_t n);
 int oco_argmax_f32_ws(const float *logits, uint32_t n, uint32_t *out, void *workspace,
                       uint64_t workspace_bytes, oco_stream stream);
+
+/* ---- GGUF checkpoints and residency (src/gguf.rs) ------------------------- */
+
+/* An open GGUF v3 file: memory-mapped, metadata structurally validated,
+ * the requested keys indexed.  Replaces Gguf::open (gguf.rs:108-150). */
+typedef struct oco_gguf oco_gguf;
+int oco_gguf_open(const char *path, const char *const *keep, uint32_t nkeep, oco_gguf **out);
+int oco_gguf_close(oco_gguf *gguf);
+
+/* Typed metadata reads (gguf.rs:239-348); strings point into the mapping
+ * (valid until oco_gguf_close) and are not NUL-terminated. */
+int oco_gguf_has(const oco_gguf *gguf, const char *key);
+int oco_gguf_text(const oco_gguf *gguf, const char *key, const char **text, size_t *len);
+int oco_gguf_number(const oco_gguf *gguf, const char *key, double *out);
+int oco_gguf_boolean(const oco_gguf *gguf, const char *key, int *out);
+int oco_gguf_unsigned(const oco_gguf *gguf, const char *key, uint64_t *out);
+int oco_gguf_array(const oco_gguf *gguf, const char *key, uint32_t *element_kind, uint64_t *count);
+int oco_gguf_array_string(const oco_gguf *gguf, const char *key, uint64_t index, const char **text,
+                          size_t *len);
+int oco_gguf_array_unsigned(const oco_gguf *gguf, const char *key, uint64_t *out, uint64_t capacity);
+
+/* Tensor directory entry: shape (GGUF order, shape[0] is the row width),
+ * GGUF type code, absolute byte offset in the file and the extent up to the
+ * next tensor.  Replaces Entry (gguf.rs:24-33). */
+typedef struct oco_gguf_entry {
+    uint64_t shape[4];
+    uint32_t rank;
+    uint32_t code;
+    uint64_t offset;
+    uint64_t extent;
+} oco_gguf_entry;
+
+/* Build and check the directory (alignment, overlap, bounds): gguf.rs:156-237. */
+int oco_gguf_directory(oco_gguf *gguf, uint64_t *count);
+int oco_gguf_entry_at(const oco_gguf *gguf, uint64_t index, const char **name, oco_gguf_entry *out);
+int oco_gguf_find(const oco_gguf *gguf, const char *name, oco_gguf_entry *out);
+
+/* A tensor checked for execution (format alignment, whole blocks, index
+ * range, payload inside its extent): Entry::select / Tensor (gguf.rs:17-87). */
+typedef struct oco_gguf_tensor {
+    uint32_t format;
+    uint32_t rank;
+    uint64_t shape[4];
+    uint64_t offset;
+    uint64_t bytes;
+} oco_gguf_tensor;
+int oco_gguf_select(const oco_gguf_entry *entry, oco_gguf_tensor *out);
+
+/* Host view of a selected tensor's bytes in the mapping (NULL if outside). */
+const void *oco_gguf_data(const oco_gguf *gguf, const oco_gguf_tensor *tensor);
+
+/* Device residency: copy a selected tensor once into device memory `dst`
+ * (>= tensor->bytes), blocking until done.  Replaces the zero-copy Metal
+ * views over the mapping (buffer.rs:145-297): here the weights live in HBM. */
+int oco_gguf_upload(const oco_gguf *gguf, const oco_gguf_tensor *tensor, void *dst, oco_stream stream);
 
 #ifdef __cplusplus
 }

@@ -97,6 +97,18 @@ class ExpertsDesc(ctypes.Structure):
                 ("down_bias", ctypes.c_void_p)]
 
 
+class GgufEntry(ctypes.Structure):
+    """oco_gguf_entry (Entry, gguf.rs:24-33)."""
+    _fields_ = [("shape", ctypes.c_uint64 * 4), ("rank", ctypes.c_uint32), ("code", ctypes.c_uint32),
+                ("offset", ctypes.c_uint64), ("extent", ctypes.c_uint64)]
+
+
+class GgufTensor(ctypes.Structure):
+    """oco_gguf_tensor (Tensor, gguf.rs:17-22)."""
+    _fields_ = [("format", ctypes.c_uint32), ("rank", ctypes.c_uint32), ("shape", ctypes.c_uint64 * 4),
+                ("offset", ctypes.c_uint64), ("bytes", ctypes.c_uint64)]
+
+
 # Every symbol include/oco_hip.h declares, with its ctypes signature.
 _vp, _u32, _u64, _i32, _sz = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int, ctypes.c_size_t
 _MP = ctypes.POINTER(Matrix)
@@ -142,6 +154,22 @@ SIGNATURES = {
     "oco_argmax_f32": (_i32, [_vp, _u32, _vp, _vp]),
     "oco_argmax_workspace": (_u64, [_u32]),
     "oco_argmax_f32_ws": (_i32, [_vp, _u32, _vp, _vp, _u64, _vp]),
+    "oco_gguf_open": (_i32, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_char_p), _u32, ctypes.POINTER(_vp)]),
+    "oco_gguf_close": (_i32, [_vp]),
+    "oco_gguf_has": (_i32, [_vp, ctypes.c_char_p]),
+    "oco_gguf_text": (_i32, [_vp, ctypes.c_char_p, ctypes.POINTER(_vp), ctypes.POINTER(_sz)]),
+    "oco_gguf_number": (_i32, [_vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_double)]),
+    "oco_gguf_boolean": (_i32, [_vp, ctypes.c_char_p, ctypes.POINTER(_i32)]),
+    "oco_gguf_unsigned": (_i32, [_vp, ctypes.c_char_p, ctypes.POINTER(_u64)]),
+    "oco_gguf_array": (_i32, [_vp, ctypes.c_char_p, ctypes.POINTER(_u32), ctypes.POINTER(_u64)]),
+    "oco_gguf_array_string": (_i32, [_vp, ctypes.c_char_p, _u64, ctypes.POINTER(_vp), ctypes.POINTER(_sz)]),
+    "oco_gguf_array_unsigned": (_i32, [_vp, ctypes.c_char_p, _vp, _u64]),
+    "oco_gguf_directory": (_i32, [_vp, ctypes.POINTER(_u64)]),
+    "oco_gguf_entry_at": (_i32, [_vp, _u64, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(GgufEntry)]),
+    "oco_gguf_find": (_i32, [_vp, ctypes.c_char_p, ctypes.POINTER(GgufEntry)]),
+    "oco_gguf_select": (_i32, [ctypes.POINTER(GgufEntry), ctypes.POINTER(GgufTensor)]),
+    "oco_gguf_data": (_vp, [_vp, ctypes.POINTER(GgufTensor)]),
+    "oco_gguf_upload": (_i32, [_vp, ctypes.POINTER(GgufTensor), _vp, _vp]),
 }
 
 _lib = None
@@ -413,6 +441,105 @@ def argmax(logits, n: int, out, stream=None, workspace=None, workspace_bytes: in
     else:
         _check(lib.oco_argmax_f32_ws(_addr(logits), n, _addr(out), _addr(workspace), int(workspace_bytes),
                                      _stream(stream)))
+
+
+# ---- GGUF checkpoints (src/gguf.rs) ---------------------------------------------
+
+class Gguf:
+    """Gguf (gguf.rs:98-348): an open, structurally validated GGUF v3 file."""
+
+    def __init__(self, path: str, keep=()):
+        lib = load_library()
+        keys = [k.encode() for k in keep]
+        arr = (ctypes.c_char_p * max(len(keys), 1))(*keys)
+        h = ctypes.c_void_p()
+        _check(lib.oco_gguf_open(os.fsencode(path), arr, len(keys), ctypes.byref(h)))
+        self.handle = h
+
+    def close(self):
+        if self.handle:
+            load_library().oco_gguf_close(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _bytes(self, fn, key, *extra):
+        p, n = ctypes.c_void_p(), ctypes.c_size_t()
+        _check(fn(self.handle, key.encode(), *extra, ctypes.byref(p), ctypes.byref(n)))
+        return ctypes.string_at(p.value, n.value).decode() if n.value else ""
+
+    def has(self, key: str) -> bool:
+        return bool(load_library().oco_gguf_has(self.handle, key.encode()))
+
+    def text(self, key: str) -> str:
+        return self._bytes(load_library().oco_gguf_text, key)
+
+    def number(self, key: str) -> float:
+        v = ctypes.c_double()
+        _check(load_library().oco_gguf_number(self.handle, key.encode(), ctypes.byref(v)))
+        return v.value
+
+    def boolean(self, key: str) -> bool:
+        v = ctypes.c_int()
+        _check(load_library().oco_gguf_boolean(self.handle, key.encode(), ctypes.byref(v)))
+        return bool(v.value)
+
+    def optional_unsigned(self, key: str):
+        if not self.has(key):
+            return None
+        v = ctypes.c_uint64()
+        _check(load_library().oco_gguf_unsigned(self.handle, key.encode(), ctypes.byref(v)))
+        return v.value
+
+    def strings(self, key: str) -> list:
+        kind, count = ctypes.c_uint32(), ctypes.c_uint64()
+        _check(load_library().oco_gguf_array(self.handle, key.encode(), ctypes.byref(kind), ctypes.byref(count)))
+        return [self._bytes(load_library().oco_gguf_array_string, key, ctypes.c_uint64(i)) for i in range(count.value)]
+
+    def unsigned_integers(self, key: str) -> list:
+        kind, count = ctypes.c_uint32(), ctypes.c_uint64()
+        _check(load_library().oco_gguf_array(self.handle, key.encode(), ctypes.byref(kind), ctypes.byref(count)))
+        out = np.zeros(max(count.value, 1), np.uint64)
+        _check(load_library().oco_gguf_array_unsigned(self.handle, key.encode(), out.ctypes.data, count.value))
+        return [int(v) for v in out[:count.value]]
+
+    def directory(self) -> dict:
+        lib = load_library()
+        n = ctypes.c_uint64()
+        _check(lib.oco_gguf_directory(self.handle, ctypes.byref(n)))
+        out = {}
+        for i in range(n.value):
+            name, e = ctypes.c_char_p(), GgufEntry()
+            _check(lib.oco_gguf_entry_at(self.handle, i, ctypes.byref(name), ctypes.byref(e)))
+            out[name.value.decode()] = e
+        return out
+
+    @staticmethod
+    def select(entry: GgufEntry) -> GgufTensor:
+        t = GgufTensor()
+        _check(load_library().oco_gguf_select(ctypes.byref(entry), ctypes.byref(t)))
+        return t
+
+    def data(self, t: GgufTensor) -> np.ndarray:
+        p = load_library().oco_gguf_data(self.handle, ctypes.byref(t))
+        if not p:
+            raise OcoError(5, "tensor outside the mapping")
+        return np.ctypeslib.as_array((ctypes.c_uint8 * t.bytes).from_address(p)).copy()
+
+    def upload(self, t: GgufTensor, dst=None, stream=None) -> "DeviceBuffer":
+        buf = dst if dst is not None else DeviceBuffer(t.bytes)
+        _check(load_library().oco_gguf_upload(self.handle, ctypes.byref(t), _addr(buf), _stream(stream)))
+        return buf
 
 
 # ---- operator mirror -----------------------------------------------------------
