@@ -359,6 +359,9 @@ WORKLOADS = {
     "q4_k_matvec_12288x4096": lambda: Matvec("q4_k_matvec_12288x4096", 12, 12288, 4096),
     "q6_k_matvec_4096x12288": lambda: Matvec("q6_k_matvec_4096x12288", 14, 4096, 12288),
     "q6_k_lm_head_151936x4096": lambda: Matvec("q6_k_lm_head_151936x4096", 14, 151936, 4096),
+    "q4_0_matvec_4096x4096": lambda: Matvec("q4_0_matvec_4096x4096", 2, 4096, 4096),
+    "q4_1_matvec_4096x4096": lambda: Matvec("q4_1_matvec_4096x4096", 3, 4096, 4096),
+    "q5_k_matvec_12288x4096": lambda: Matvec("q5_k_matvec_12288x4096", 13, 12288, 4096),
     "qwen3_8b_q4km_decode_stack": MatvecStack,
     "moe_decode_gpt_oss_b1": lambda: MoeDecode(1),
     "moe_decode_gpt_oss_b4": lambda: MoeDecode(4),

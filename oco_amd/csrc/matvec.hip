@@ -110,7 +110,7 @@ __global__ __launch_bounds__(256) void matvec_kernel(MatvecArgs a) {
 
 
 // ---------------------------------------------------------------------------
-// Streaming matvec (Q8_0, Q4_K, Q6_K, MXFP4).
+// Streaming matvec (Q8_0, Q4_0, Q4_1, Q4_K, Q5_K, Q6_K, MXFP4).
 //
 // Persistent workgroups of four wavefronts loop over row groups.  The
 // activation vector is staged once per workgroup into LDS in piece-major
@@ -388,14 +388,15 @@ static StreamFn stream_pick_format(uint32_t fmt, int r, int npl, int &lpr) {
     case FM:                                                                                    \
         lpr = stream_lpr<FM>(npl);                                                              \
         return r == 1 ? stream_pick_npl<FM, XT, 1>(npl) : stream_pick_npl<FM, XT, 2>(npl);
-        F(OCO_Q8_0) F(OCO_MXFP4) F(OCO_Q4_K) F(OCO_Q6_K)
+        F(OCO_Q8_0) F(OCO_MXFP4) F(OCO_Q4_K) F(OCO_Q6_K) F(OCO_Q4_0) F(OCO_Q4_1) F(OCO_Q5_K)
 #undef F
     }
     return nullptr;
 }
 
 static bool streamable(uint32_t fmt) {
-    return fmt == OCO_Q8_0 || fmt == OCO_MXFP4 || fmt == OCO_Q4_K || fmt == OCO_Q6_K;
+    return fmt == OCO_Q8_0 || fmt == OCO_MXFP4 || fmt == OCO_Q4_K || fmt == OCO_Q6_K || fmt == OCO_Q4_0 ||
+           fmt == OCO_Q4_1 || fmt == OCO_Q5_K;
 }
 
 struct StreamPlan {
@@ -523,7 +524,7 @@ static int matvec_impl(uint32_t format, const void *w, const void *x, oco_dtype 
         }
         uint32_t be, bbytes;
         oco_block_layout(format, &be, &bbytes);
-        const uint32_t P = (format == OCO_Q4_K || format == OCO_Q6_K) ? 8 : 1;
+        const uint32_t P = (format == OCO_Q4_K || format == OCO_Q5_K || format == OCO_Q6_K) ? 8 : 1;
         const uint32_t nblocks = p->k / be;
         StreamPlan sp = stream_plan(format, p->k, p->n, p->m);
         if (sp.ks != 1 && sp.ks != 2 && sp.ks != 4) sp.ks = 1;
@@ -556,7 +557,10 @@ static int matvec_impl(uint32_t format, const void *w, const void *x, oco_dtype 
             a.norm_w = norm ? norm->w : nullptr;
             const uint32_t rows_per_group = (4 / sp.ks) * 2 * sp.r;
             a.ngroups = (p->n + rows_per_group - 1) / rows_per_group;
-            const uint32_t nsum = format == OCO_Q8_0 ? 1 : format == OCO_Q4_K ? 2 : format == OCO_Q6_K ? 4 : 0;
+            const uint32_t nsum = (format == OCO_Q8_0 || format == OCO_Q4_0 || format == OCO_Q4_1) ? 1
+                                  : (format == OCO_Q4_K || format == OCO_Q5_K)                    ? 2
+                                  : format == OCO_Q6_K                                            ? 4
+                                                                                                  : 0;
             const size_t tile = (size_t)2 * sp.r * lpr * 1024;
             const size_t lds = (size_t)p->k * 4 + (size_t)nsum * (p->k / 32) * 4 + 4 * tile + 32 * sizeof(float);
             if (lds > 160 * 1024)

@@ -255,11 +255,135 @@ struct Tile<OCO_Q6_K> {
     }
 };
 
+// Q4_0: piece = block {f16 d, 16 code bytes}; byte i holds columns i (low
+// nibble) and 16 + i (high nibble); w = d (q - 8) (weights.metal:55-59),
+// computed as d (sum q x - 8 sum x).
+template <>
+struct Tile<OCO_Q4_0> {
+    static constexpr int BLOCK = 32, BYTES = 18, P = 1, NSUM = 1;
+    struct Raw {
+        uint4 q;
+        uint32_t d;
+    };
+    __device__ __forceinline__ static void map(uint32_t f, uint32_t &p, uint32_t &t) {
+        p = f >> 3;
+        t = f & 7;
+    }
+    __device__ __forceinline__ static void sums(const float *x, float *s) {
+        float a = 0.f;
+#pragma unroll
+        for (int i = 0; i < 32; i++) a += x[i];
+        s[0] = a;
+    }
+    __device__ __forceinline__ static Raw load(const uint8_t *blk, int) {
+        Raw r;
+        r.d = lds_u16(blk);
+        r.q = lds_u128(blk + 2);
+        return r;
+    }
+    __device__ __forceinline__ static float nibble_dot(const uint4 &q, const float *x) {
+        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+        float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t lo = w[j] & 0x0f0f0f0fu, hi = (w[j] >> 4) & 0x0f0f0f0fu;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                a0 = fmaf(ub(lo, i), x[4 * j + i], a0);
+                a1 = fmaf(ub(hi, i), x[16 + 4 * j + i], a1);
+            }
+        }
+        return a0 + a1;
+    }
+    __device__ __forceinline__ static float dot(const Raw &r, const float *x, const float *s) {
+        return half_bits_to_f32(r.d) * fmaf(-8.f, s[0], nibble_dot(r.q, x));
+    }
+};
+
+// Q4_1: piece = block {f16 d, f16 m, 16 code bytes}; w = d q + m
+// (weights.metal:55-59), computed as d sum q x + m sum x.
+template <>
+struct Tile<OCO_Q4_1> {
+    static constexpr int BLOCK = 32, BYTES = 20, P = 1, NSUM = 1;
+    struct Raw {
+        uint4 q;
+        uint32_t dm;
+    };
+    __device__ __forceinline__ static void map(uint32_t f, uint32_t &p, uint32_t &t) {
+        p = f >> 3;
+        t = f & 7;
+    }
+    __device__ __forceinline__ static void sums(const float *x, float *s) { Tile<OCO_Q4_0>::sums(x, s); }
+    __device__ __forceinline__ static Raw load(const uint8_t *blk, int) {
+        Raw r;
+        uint32_t o[5];
+        lds_bytes<20>(blk, o);
+        r.dm = o[0];
+        r.q = make_uint4(o[1], o[2], o[3], o[4]);
+        return r;
+    }
+    __device__ __forceinline__ static float dot(const Raw &r, const float *x, const float *s) {
+        return fmaf(half_bits_to_f32(r.dm & 0xffffu), Tile<OCO_Q4_0>::nibble_dot(r.q, x),
+                    half_bits_to_f32(r.dm >> 16) * s[0]);
+    }
+};
+
+// Q5_K: the Q4_K piece (qs at byte 48 instead of 16) plus the fifth bit of
+// each code from qh[32] at byte 16: column j takes bit j / 32 of qh[j % 32]
+// (weights.metal:67-77).  Piece c's low-nibble columns (sub-block 2g) and
+// high-nibble columns (sub-block 2g + 1) share the qh bytes 16 (c & 1) ..
+// + 15, bits 2g and 2g + 1.
+template <>
+struct Tile<OCO_Q5_K> {
+    static constexpr int BLOCK = 256, BYTES = 176, P = 8, NSUM = 2;
+    struct Raw {
+        uint4 hdr, qh, qs;
+    };
+    __device__ __forceinline__ static void map(uint32_t f, uint32_t &p, uint32_t &t) { Tile<OCO_Q4_K>::map(f, p, t); }
+    __device__ __forceinline__ static void sums(const float *x, float *s) { Tile<OCO_Q4_K>::sums(x, s); }
+    __device__ __forceinline__ static Raw load(const uint8_t *blk, int c) {
+        Raw r;
+        r.hdr = lds_u128(blk);
+        r.qh = lds_u128(blk + 16 + 16 * (c & 1));
+        r.qs = lds_u128(blk + 48 + 16 * c);
+        return r;
+    }
+    __device__ __forceinline__ static float dot(const Raw &r, const float *x, const float *s, int c) {
+        const uint32_t g = (uint32_t)c >> 1;
+        uint32_t scm[2][2];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const uint32_t t = 8 * ((2 * g + h) & 3);
+            const uint32_t sc_lo = __builtin_amdgcn_ubfe(r.hdr.y, t, 6), mn_lo = __builtin_amdgcn_ubfe(r.hdr.z, t, 6);
+            const uint32_t sc_hi = __builtin_amdgcn_ubfe(r.hdr.w, t, 4) | (__builtin_amdgcn_ubfe(r.hdr.y, t + 6, 2) << 4);
+            const uint32_t mn_hi = __builtin_amdgcn_ubfe(r.hdr.w, t + 4, 4) | (__builtin_amdgcn_ubfe(r.hdr.z, t + 6, 2) << 4);
+            scm[h][0] = g < 2 ? sc_lo : sc_hi;
+            scm[h][1] = g < 2 ? mn_lo : mn_hi;
+        }
+        const uint32_t w[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
+        const uint32_t hb[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
+        float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t lo = (w[j] & 0x0f0f0f0fu) | (((hb[j] >> (2 * g)) & 0x01010101u) << 4);
+            const uint32_t hi = ((w[j] >> 4) & 0x0f0f0f0fu) | (((hb[j] >> (2 * g + 1)) & 0x01010101u) << 4);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                a0 = fmaf(ub(lo, i), x[4 * j + i], a0);
+                a1 = fmaf(ub(hi, i), x[16 + 4 * j + i], a1);
+            }
+        }
+        const float d = half_bits_to_f32(r.hdr.x & 0xffffu), dmin = half_bits_to_f32(r.hdr.x >> 16);
+        const float v = fmaf(d * (float)scm[0][0], a0, -(dmin * (float)scm[0][1]) * s[0]);
+        return fmaf(d * (float)scm[1][0], a1, fmaf(-(dmin * (float)scm[1][1]), s[1], v));
+    }
+};
+
 // Uniform call shape for formats whose dot ignores the piece index.
 template <int FMT>
 __device__ __forceinline__ float tile_dot(const typename Tile<FMT>::Raw &r, const float *x,
                                           const float *s, int c) {
-    if constexpr (FMT == OCO_Q4_K || FMT == OCO_Q6_K)
+    if constexpr (FMT == OCO_Q4_K || FMT == OCO_Q5_K || FMT == OCO_Q6_K)
         return Tile<FMT>::dot(r, x, s, c);
     else
         return Tile<FMT>::dot(r, x, s);

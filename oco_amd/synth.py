@@ -10,6 +10,9 @@ shaders/matrix/weights.metal:40-85):
           (2^-9 .. 2^-4)
 - Q4_K  : 6-bit scales and mins uniform, f16 d and dmin = |N(0, 0.01)|, codes uniform
 - Q6_K  : 6-bit codes uniform, int8 sub-block scales uniform, f16 d = |N(0, 0.01)|
+- Q4_0  : 4-bit codes uniform, f16 d = |N(0, 0.01)|
+- Q4_1  : 4-bit codes uniform, f16 d = |N(0, 0.01)|, f16 m = N(0, 0.01)
+- Q5_K  : as Q4_K plus uniform fifth bits (qh)
 """
 from __future__ import annotations
 
@@ -93,7 +96,35 @@ def q6_k(rows: int, k: int, seed: int) -> np.ndarray:
     return blocks.reshape(-1)
 
 
-GENERATORS = {8: q8_0, 39: mxfp4, 12: q4_k, 14: q6_k}
+def q4_0(rows: int, k: int, seed: int) -> np.ndarray:
+    nb = rows * (k // 32)
+    blocks = random_bytes(seed, nb * 18).reshape(nb, 18)
+    d = (np.abs(normal(seed + 1, nb)) * 0.01).astype(np.float16)
+    blocks[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+    return blocks.reshape(-1)
+
+
+def q4_1(rows: int, k: int, seed: int) -> np.ndarray:
+    nb = rows * (k // 32)
+    blocks = random_bytes(seed, nb * 20).reshape(nb, 20)
+    d = (np.abs(normal(seed + 1, nb)) * 0.01).astype(np.float16)
+    m = (normal(seed + 2, nb) * 0.01).astype(np.float16)
+    blocks[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+    blocks[:, 2:4] = m.view(np.uint8).reshape(nb, 2)
+    return blocks.reshape(-1)
+
+
+def q5_k(rows: int, k: int, seed: int) -> np.ndarray:
+    nb = rows * (k // 256)
+    blocks = random_bytes(seed, nb * 176).reshape(nb, 176)
+    d = (np.abs(normal(seed + 1, nb)) * 0.01).astype(np.float16)
+    dmin = (np.abs(normal(seed + 2, nb)) * 0.01).astype(np.float16)
+    blocks[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+    blocks[:, 2:4] = dmin.view(np.uint8).reshape(nb, 2)
+    return blocks.reshape(-1)
+
+
+GENERATORS = {8: q8_0, 39: mxfp4, 12: q4_k, 14: q6_k, 2: q4_0, 3: q4_1, 13: q5_k}
 
 
 def weights(fmt: int, rows: int, k: int, seed: int) -> np.ndarray:

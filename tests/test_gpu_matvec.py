@@ -95,12 +95,13 @@ def check_matvec(oco, fmt, data, x, p, **kw):
     return err
 
 
-SHAPES = {  # BASELINE shapes (lm_head is covered by its own row-slice test)
+SHAPES = {  # BASELINE shapes (lm_head is covered by its own row-slice test), and the other streamed formats
     P.Q8_0: (4096, 4096), O.MXFP4: (5760, 2880), P.Q4_K: (12288, 4096), P.Q6_K: (4096, 12288),
+    P.Q4_0: (4096, 4096), P.Q4_1: (4096, 4096), P.Q5_K: (12288, 4096),
 }
 
 
-@pytest.mark.parametrize("fmt", [P.Q8_0, O.MXFP4, P.Q4_K, P.Q6_K])
+@pytest.mark.parametrize("fmt", [P.Q8_0, O.MXFP4, P.Q4_K, P.Q6_K, P.Q4_0, P.Q4_1, P.Q5_K])
 def test_matvec_baseline_shapes_f32(lib, fmt):
     from oco_amd import synth
     n, k = SHAPES[fmt]
@@ -129,7 +130,7 @@ def test_matvec_reference_packer_tails(lib, fmt, n):
     check_matvec(lib, fmt, data, x, p, x_bf16=True, y_bf16=True)
 
 
-@pytest.mark.parametrize("fmt", [O.MXFP4, P.Q8_0, P.Q4_K, P.Q6_K])
+@pytest.mark.parametrize("fmt", [O.MXFP4, P.Q8_0, P.Q4_K, P.Q6_K, P.Q4_0, P.Q4_1, P.Q5_K])
 def test_matvec_routed_semantics(lib, fmt):
     """experts > 1: rows through ids[route], input route/routes, f32 output,
     has_bias 2 adds bf16(bias + 1) (vector.metal:76-78, 140-146)."""
@@ -205,7 +206,8 @@ def test_matvec_stream_plans(lib, plan, monkeypatch):
     bf16 activations, routed rows with bias."""
     from oco_amd import synth
     monkeypatch.setenv("OCO_STREAM_PLAN", plan)
-    for fmt, n, k in [(O.MXFP4, 131, 2880), (P.Q8_0, 77, 4096), (P.Q4_K, 257, 2048), (P.Q6_K, 300, 4096)]:
+    for fmt, n, k in [(O.MXFP4, 131, 2880), (P.Q8_0, 77, 4096), (P.Q4_K, 257, 2048), (P.Q6_K, 300, 4096),
+                      (P.Q4_0, 90, 4096), (P.Q4_1, 65, 2048), (P.Q5_K, 130, 4096)]:
         say("matvec plan", plan, fmt, n, k)
         data = synth.weights(fmt, n, k, seed=11)
         x = synth.activations(12, k)
