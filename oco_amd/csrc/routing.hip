@@ -44,7 +44,7 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const XT *x, const f
 // two dispatch grids at words 0-5.  Routes are taken 1024 at a time; a
 // route's place in its expert's list is the expert's running count plus the
 // number of earlier routes of the chunk with the same expert, so lists keep
-// route order: up to 256 experts from lane comparisons inside each
+// route order: up to 256 experts from ballot-matched peers inside each
 // wavefront and per-wavefront histograms in LDS, beyond that by broadcast
 // LDS reads of the whole chunk.  Ids >= experts are left out.
 constexpr uint32_t PLAN_THREADS = 1024;
@@ -136,22 +136,25 @@ __global__ __launch_bounds__(PLAN_THREADS) void route_plan_kernel(const uint32_t
     // 3. stable placement, 1024 routes at a time: a route's place in its
     // expert's list is the running count plus its rank among the chunk's
     // earlier routes of the same expert
+    const uint32_t id_bits = experts > 1 ? 32u - (uint32_t)__builtin_clz(experts - 1) : 0u;
     uint32_t e_next = tid < routes ? ids[tid] : 0xffffffffu;
     for (uint32_t base = 0; base < routes; base += PLAN_THREADS) {
         const uint32_t i = base + tid, e = e_next;
         e_next = i + PLAN_THREADS < routes ? ids[i + PLAN_THREADS] : 0xffffffffu;  // next chunk, in flight
         uint32_t rank = 0;
         if (experts <= PLAN_HIST_EXPERTS) {
-            // rank among earlier lanes of the wavefront; whether this is the
-            // expert's last lane in it
-            bool last = true;
-            for (int b = 0; b < 64; b++) {
-                const uint32_t eb = (uint32_t)__builtin_amdgcn_readlane((int)e, b);
-                if (eb == e) {
-                    if ((uint32_t)b < lane) rank++;
-                    if ((uint32_t)b > lane) last = false;
-                }
+            // Lanes of the wavefront holding the same expert: one ballot per
+            // bit of the id (and one for validity) narrows each lane's peer
+            // mask; the rank is the count of earlier peers, and the last peer
+            // carries the wavefront's count.
+            uint64_t peers = __ballot(e < experts);
+            if (e >= experts) peers = ~peers;
+            for (uint32_t bit = 0; bit < id_bits; bit++) {
+                const uint64_t b = __ballot((e >> bit) & 1u);
+                peers &= ((e >> bit) & 1u) ? b : ~b;
             }
+            rank = (uint32_t)__popcll(peers & ((1ull << lane) - 1ull));
+            const bool last = (peers >> lane) == 1ull;
             for (uint32_t t = tid; t < 16 * experts; t += PLAN_THREADS) hist[t] = 0;
             __syncthreads();
             if (e < experts && last) hist[wave * experts + e] = rank + 1;
@@ -201,6 +204,35 @@ __global__ __launch_bounds__(256) void moe_sum_kernel(const RT *routes, const fl
         s = fmaf(v, probs[t * k + r], s);
     }
     out[i] = f32_to_bf16_bits(bf16_bits_to_f32(out[i]) + round_bf16(s));
+}
+
+// The same for bf16 routes and hidden % 8 == 0, eight outputs per thread
+// with 16-byte loads; the per-element arithmetic and order are unchanged.
+__global__ __launch_bounds__(256) void moe_sum8_kernel(const uint16_t *routes, const float *probs, uint16_t *out,
+                                                       uint32_t hidden, uint32_t tokens, uint32_t k) {
+    const uint64_t i8 = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i8 * 8 >= (uint64_t)hidden * tokens) return;
+    const uint64_t i = i8 * 8, t = i / hidden, d = i % hidden;
+    float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (uint32_t r = 0; r < k; r++) {
+        const uint4 v = *reinterpret_cast<const uint4 *>(routes + (t * k + r) * hidden + d);
+        const float p = probs[t * k + r];
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            s[2 * j] = fmaf(__uint_as_float(w[j] << 16), p, s[2 * j]);
+            s[2 * j + 1] = fmaf(__uint_as_float(w[j] & 0xffff0000u), p, s[2 * j + 1]);
+        }
+    }
+    uint4 o = *reinterpret_cast<const uint4 *>(out + i);
+    uint32_t ow[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const uint32_t lo = f32_to_bf16_bits(bf16_bits_to_f32(ow[j] & 0xffffu) + round_bf16(s[2 * j]));
+        const uint32_t hi = f32_to_bf16_bits(bf16_bits_to_f32(ow[j] >> 16) + round_bf16(s[2 * j + 1]));
+        ow[j] = lo | (hi << 16);
+    }
+    *reinterpret_cast<uint4 *>(out + i) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
 }
 
 }  // namespace oco
@@ -281,6 +313,9 @@ int oco_moe_sum(const void *routes, oco_dtype routes_dtype, const float *probs, 
     if (routes_dtype == OCO_DT_F32)
         hipLaunchKernelGGL(moe_sum_kernel<float>, dim3(grid), dim3(256), 0, s, (const float *)routes, probs,
                            out, hidden, tokens, k);
+    else if (routes_dtype == OCO_DT_BF16 && hidden % 8 == 0 && ((uintptr_t)routes & 15) == 0 && ((uintptr_t)out & 15) == 0)
+        hipLaunchKernelGGL(moe_sum8_kernel, dim3((unsigned)((n / 8 + 255) / 256)), dim3(256), 0, s,
+                           (const uint16_t *)routes, probs, out, hidden, tokens, k);
     else if (routes_dtype == OCO_DT_BF16)
         hipLaunchKernelGGL(moe_sum_kernel<bf16_t>, dim3(grid), dim3(256), 0, s, (const bf16_t *)routes, probs,
                            out, hidden, tokens, k);

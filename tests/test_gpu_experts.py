@@ -96,8 +96,10 @@ def test_route_plan_bit_exact(lib, batch, experts, tile):
     np.testing.assert_array_equal(got[defined], want[defined])
 
 
-def test_moe_sum(lib):
-    hidden, tokens, k = 2880, 16, 4
+@pytest.mark.parametrize("hidden", [2880, 2884])
+def test_moe_sum(lib, hidden):
+    """hidden % 8 == 0 takes the eight-wide kernel, else the scalar one."""
+    tokens, k = 16, 4
     rng = np.random.default_rng(5)
     routes = O.f32_to_bf16(rng.normal(size=(tokens * k, hidden)).astype(np.float32))
     probs = O.bf16_round(rng.dirichlet(np.ones(k), size=tokens)).astype(np.float32)
@@ -110,6 +112,13 @@ def test_moe_sum(lib):
     # fp32 sums may differ by fused rounding: at most one bf16 step apart
     diff = np.abs(got.astype(np.int32) - want.astype(np.int32))
     assert diff.max() <= 1 and (diff > 0).mean() < 0.01
+    # the eight-wide and scalar kernels agree bit for bit (an output 2 bytes
+    # past a 16-byte boundary takes the scalar kernel)
+    buf = lib.DeviceBuffer(resid.nbytes + 16)
+    buf.upload(resid, 2)
+    lib.moe_sum(dev(lib, routes), lib.DType.BF16, dev(lib, probs), buf.ptr + 2, hidden, tokens, k)
+    lib.synchronize()
+    assert np.array_equal(buf.download(np.uint16, tokens * hidden, 2).reshape(tokens, hidden), got)
 
 
 # ---- expert projections -------------------------------------------------------
