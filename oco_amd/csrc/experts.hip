@@ -375,6 +375,27 @@ __global__ __launch_bounds__(256) void to_f16_kernel(const XT *x, uint16_t *y, u
     }
 }
 
+// Gate/up activations to f16 rows for the Q4_K down tiles: each row scaled
+// by the power of two (row_gain) that brings its max |activation| into
+// [2^14, 2^15), which is exact, then rounded to f16; the down epilogue
+// multiplies the gain back out, also exactly.  Four elements per thread
+// (cols % 4 == 0).
+__global__ __launch_bounds__(256) void act_f16_kernel(const float *x, const uint32_t *rowmax, uint16_t *y,
+                                                      uint32_t cols, uint64_t n) {
+    const uint64_t i = ((uint64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i >= n) return;
+    const float g = row_gain(rowmax[i / cols]);
+    const float4 v = *reinterpret_cast<const float4 *>(x + i);
+    const float e[4] = {v.x * g, v.y * g, v.z * g, v.w * g};
+    uint16_t b[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const _Float16 h = (_Float16)e[j];
+        __builtin_memcpy(&b[j], &h, 2);
+    }
+    *reinterpret_cast<uint2 *>(y + i) = make_uint2(b[0] | ((uint32_t)b[1] << 16), b[2] | ((uint32_t)b[3] << 16));
+}
+
 }  // namespace oco
 
 using namespace oco;
@@ -385,10 +406,11 @@ uint64_t oco_experts_workspace(const oco_experts *w, uint32_t tokens) {
     if (!w) return 0;
     const uint64_t routes = (uint64_t)tokens * w->k;
     // plan, f32 activations, f16 copy of f32 inputs and activation row maxima
-    // (prefill), route outputs; MXFP4 banks also the E4M3 splits of the
-    // inputs and of the activations
+    // (prefill), route outputs, f16 activations (Q4_K prefill); MXFP4 banks
+    // also the E4M3 splits of the inputs and of the activations
     uint64_t bytes = align256(oco_route_plan_words((uint32_t)routes, w->experts) * 4) + align256(routes * w->ffn * 4) +
                      align256((uint64_t)tokens * w->hidden * 2) + align256(routes * 4) + align256(routes * w->hidden * 4);
+    if (w->format == OCO_Q4_K) bytes += align256(routes * w->ffn * 2);
     if (w->format == OCO_MXFP4)
         bytes += align256(mx_rows_bytes(tokens, w->hidden, 3)) + align256(mx_rows_bytes((uint32_t)routes, w->ffn, 3));
     return bytes;
@@ -416,6 +438,7 @@ int oco_experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype, co
     float *down = routed ? routed : (float *)own_down;
     uint8_t *xrec = own_down + align256((uint64_t)routes * w->hidden * 4);  // MXFP4 only
     uint8_t *arec = xrec + align256(mx_rows_bytes(tokens, w->hidden, 3));
+    uint16_t *act16 = (uint16_t *)xrec;  // Q4_K only (in place of the MXFP4 splits)
 
     static const uint32_t mx_tokens =
         getenv("OCO_MOE_MX_TOKENS") ? (uint32_t)atoi(getenv("OCO_MOE_MX_TOKENS")) : MOE_MX_TOKENS;  // tuning runs only
@@ -470,7 +493,7 @@ int oco_experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype, co
         // Rows per tile: most experts in one tile (mean routes per expert,
         // plus room for the spread).
         const uint32_t mean = routes / w->experts;
-        const uint32_t bm = q4 ? (mean <= 20 ? 32 : mean <= 36 ? 48 : 64) : (mean <= 40 ? 32 : 64);
+        const uint32_t bm = q4 ? (getenv("OCO_Q4_BM") ? (uint32_t)atoi(getenv("OCO_Q4_BM")) : mean <= 20 ? 32 : mean <= 36 ? 48 : 64) : (mean <= 40 ? 32 : 64);
         OCO_TRY(oco_route_plan(ids, routes, w->experts, bm, 0, 0, plan, stream));
         // The tiles take f16 rows (the reference's half(x)).
         const uint64_t nx = (uint64_t)tokens * w->hidden;
@@ -510,6 +533,13 @@ int oco_experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype, co
         d.bias2 = nullptr;
         d.x = act;
         d.x_f16 = 1;
+        if (q4) {
+            const uint64_t na = (uint64_t)routes * w->ffn;
+            hipLaunchKernelGGL(act_f16_kernel, dim3((unsigned)((na / 4 + 255) / 256)), dim3(256), 0, s, act, rowmax,
+                               act16, w->ffn, na);
+            OCO_TRY(launch_check("experts f16 activations"));
+            d.x = act16;
+        }
         // Route outputs: f32 when the caller asks for them, else bf16 as the
         // reference stores them (moe_sum rounds f32 routes to bf16 anyway).
         d.y = down;

@@ -22,6 +22,15 @@ struct MatmulArgs {
     uint32_t *rowmax;      // [routes] max |activation| bits per expert-sorted row (gate/up writes, down reads)
 };
 
+// Power of two that brings a row with max |value| `bits` (f32 bits) into
+// [2^14, 2^15) -- f16 range with its full precision; 1 for zero or
+// non-finite rows.
+__device__ __forceinline__ float row_gain(uint32_t bits) {
+    if (bits == 0 || bits >= 0x7f800000u) return 1.0f;
+    const int e = (int)(bits >> 23) - 127;  // floor(log2(max)), subnormals count as 2^-127
+    return __builtin_ldexpf(1.0f, max(-100, min(100, 14 - e)));
+}
+
 // Grouped modes of matmul_kernel.
 constexpr int MM_DENSE = 0;  // Y = X W^T
 constexpr int MM_GATE_UP = 1;  // per expert tile: act = f(X W_gate^T, X W_up^T), f32 at expert-sorted rows

@@ -48,14 +48,6 @@ struct BlockShape {
 
 __device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) { return (uint32_t)lo | ((uint32_t)hi << 16); }
 
-// Power of two that brings a row with max |value| `bits` (f32 bits) into
-// [2^14, 2^15) -- f16 range with its full precision; 1 for zero or
-// non-finite rows.
-__device__ __forceinline__ float row_gain(uint32_t bits) {
-    if (bits == 0 || bits >= 0x7f800000u) return 1.0f;
-    const int e = (int)(bits >> 23) - 127;  // floor(log2(max)), subnormals count as 2^-127
-    return __builtin_ldexpf(1.0f, max(-100, min(100, 14 - e)));
-}
 
 
 // One thread's share of a weight tile step: a 32-coefficient piece of one

@@ -16,13 +16,25 @@
 // exactly the weights it multiplies (half(d sc q - dmin mn), as the
 // reference's half tiles: tile.metal:35-52); no weight goes through LDS.
 //
-// Workgroup: NW wavefronts, each owning 16 weight columns (gate/up: the 16
-// gate rows and the same 16 up rows, so the activation is fused in-lane;
-// down: two groups of 16 rows), over one route-plan tile of 16 MI routes.
-// Activations are staged per super-block into LDS (double-buffered, f16);
-// weights are loaded a super-block ahead.
+// Work: a unit is (route-plan tile of 16 MI rows, column chunk of NW x 16
+// gate/up columns or NW x 32 down columns).  The grid is persistent: each
+// workgroup takes a contiguous range of units (tile-major) and runs one flat
+// pipeline of (unit, super-block) steps across them, so the prefetch does
+// not restart per unit.  Each step:
+//   - activations of the step two ahead go straight from global memory into
+//     a three-stage LDS ring (global_load_lds_dwordx4, no registers), rows
+//     swizzled so that the MFMA A reads are conflict-free;
+//   - weights of the step two ahead load into a three-set register ring;
+//   - the wavefront decodes and multiplies its two 16-row fragments
+//     (gate/up: the 16 gate rows and the same 16 up rows, so the activation
+//     is fused in-lane; down: two groups of 16 rows).
+// Both GEMMs read f16 rows: the caller's inputs (gathered per route) for
+// gate/up, and for down the gate/up activations already scaled per row by a
+// power of two into f16 range (act_f16_kernel).
 #include "matmul.h"
 #include "formats.h"
+
+#include <algorithm>
 
 namespace oco {
 
@@ -32,21 +44,6 @@ typedef float q4f32x4 __attribute__((ext_vector_type(4)));
 struct Q4Raw {  // one lane's bytes of one super-block: header and its 32 qs bytes
     uint4 hdr, q0, q1;
 };
-
-
-__device__ __forceinline__ float q4_row_gain(uint32_t bits) {
-    if (bits == 0 || bits >= 0x7f800000u) return 1.0f;
-    const int e = (int)(bits >> 23) - 127;
-    return __builtin_ldexpf(1.0f, max(-100, min(100, 14 - e)));
-}
-
-__device__ __forceinline__ uint32_t f16_pair(float lo, float hi) {
-    const _Float16 a = (_Float16)lo, b = (_Float16)hi;
-    uint16_t x, y;
-    __builtin_memcpy(&x, &a, 2);
-    __builtin_memcpy(&y, &b, 2);
-    return (uint32_t)x | ((uint32_t)y << 16);
-}
 
 // Scales of sub-block pair q: a = d sc, m = dmin mn for the low (0) and high
 // (1) nibbles (get_scale_min_k4, weights.metal:67-77).
@@ -73,24 +70,26 @@ __device__ __forceinline__ Q4Scales q4_scales(const uint4 &hdr, int q) {
     return {d * (float)sc[0], dmin * (float)mn[0], d * (float)sc[1], dmin * (float)mn[1]};
 }
 
-// Four weights from the nibbles of one dword, rounded to f16 as a * q - m:
-// byte i -> v_cvt_f32_ubyte<i>, then v_fma_mix{lo,hi}_f16 writes each
-// result into its half of the packed pair (a * q is exact, so this is the
-// reference's scale * value - minimum rounded to half).
+// Four weights from the nibbles of one dword (one per byte, high nibbles
+// clear), rounded to f16 as a * q - m (the reference's scale * value -
+// minimum, then half(); a * q is exact in f32):
+//   - a byte c < 16 read as E4M3 is c * 2^-9 (exponent 0: c/8 * 2^-6;
+//     exponent 1: (8 + c - 8)/8 * 2^-6), so v_cvt_scalef32_pk_f32_fp8 with
+//     scale 2^9 gives two exact f32 codes per instruction;
+//   - v_fma_f32 gives fl32(a q - m); v_cvt_pk_f16_f32 rounds a pair to f16.
+// Measured on gfx950, this costs about two thirds of v_cvt_f32_ubyte +
+// v_fma_mix{lo,hi}_f16 per weight (the mixed-precision FMA issues at a
+// fraction of the full rate).
+typedef float q4f32x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ void q4_four(uint32_t n, float a, float m, uint32_t &p01, uint32_t &p23) {
-    float f0, f1, f2, f3;
-    asm volatile("v_cvt_f32_ubyte0 %0, %1" : "=v"(f0) : "v"(n));
-    asm volatile("v_cvt_f32_ubyte1 %0, %1" : "=v"(f1) : "v"(n));
-    asm volatile("v_cvt_f32_ubyte2 %0, %1" : "=v"(f2) : "v"(n));
-    asm volatile("v_cvt_f32_ubyte3 %0, %1" : "=v"(f3) : "v"(n));
-    const float nm = -m;
-    uint32_t lo, hi;  // mixlo's high half is don't-care: mixhi overwrites it
-    asm volatile("v_fma_mixlo_f16 %0, %1, %2, %3" : "=v"(lo) : "v"(a), "v"(f0), "v"(nm));
-    asm volatile("v_fma_mixhi_f16 %0, %1, %2, %3" : "+v"(lo) : "v"(a), "v"(f1), "v"(nm));
-    asm volatile("v_fma_mixlo_f16 %0, %1, %2, %3" : "=v"(hi) : "v"(a), "v"(f2), "v"(nm));
-    asm volatile("v_fma_mixhi_f16 %0, %1, %2, %3" : "+v"(hi) : "v"(a), "v"(f3), "v"(nm));
-    p01 = lo;
-    p23 = hi;
+    const q4f32x2 c01 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(n, 512.0f, false);
+    const q4f32x2 c23 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(n, 512.0f, true);
+    const float f0 = __builtin_fmaf(a, c01[0], -m), f1 = __builtin_fmaf(a, c01[1], -m);
+    const float f2 = __builtin_fmaf(a, c23[0], -m), f3 = __builtin_fmaf(a, c23[1], -m);
+    // inline asm keeps the compiler from folding each FMA and its conversion
+    // back into a mixed-precision FMA
+    asm volatile("v_cvt_pk_f16_f32 %0, %1, %2" : "=v"(p01) : "v"(f0), "v"(f1));
+    asm volatile("v_cvt_pk_f16_f32 %0, %1, %2" : "=v"(p23) : "v"(f2), "v"(f3));
 }
 
 // Eight f16 weights of chunk c from the lane's qs bytes (q0 = bytes 0..15,
@@ -109,219 +108,403 @@ __device__ __forceinline__ q4f16x8 q4_chunk(const Q4Raw &r, const Q4Scales &s) {
     return v;
 }
 
+// A workgroup's range holds at most Q4_UNITS units over at most Q4_TILES
+// tiles (the launch sizes the grid for that); their route rows and biases
+// are read once, into LDS, before the pipeline starts.
+constexpr int Q4_TILES = 4, Q4_UNITS = 8;
+
+template <int B, int E, typename F>
+__device__ __forceinline__ void q4_static_for(F &&f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        q4_static_for<B + 1, E>(f);
+    }
+}
+
+// s_waitcnt vmcnt(N) (gfx9 encoding; expcnt and lgkmcnt left at their maxima).
+template <int N>
+__device__ __forceinline__ void q4_vm_wait() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Max over the 16 lanes of a DPP row (lanes 16 r .. 16 r + 15).
+__device__ __forceinline__ uint32_t q4_row_max(uint32_t m) {
+    m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0xB1, 0xf, 0xf, false));   // quad xor 1
+    m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x4E, 0xf, 0xf, false));   // quad xor 2
+    m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x141, 0xf, 0xf, false));  // half-row mirror
+    m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x140, 0xf, 0xf, false));  // row mirror
+    return m;
+}
+
+// LDS reads outside the ring, as inline asm: the compiler cannot tell the
+// arrays they read from the ring's stages, so a read it sees waits for every
+// global->LDS load in flight.  The caller's s_waitcnt lgkmcnt(0) (inline asm
+// too) takes the results as operands, so no use moves above it.
+__device__ __forceinline__ uint32_t q4_lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+__device__ __forceinline__ uint32_t q4_lds_b32(const void *p) {
+    uint32_t v;
+    asm volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"(q4_lds_addr(p)));
+    return v;
+}
+typedef uint32_t q4u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ q4u32x4 q4_lds_b128(const void *p) {
+    q4u32x4 v;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(q4_lds_addr(p)));
+    return v;
+}
+
+// A use of v the compiler cannot see through (it must have landed here).
+__device__ __forceinline__ void q4_touch(const uint4 &v) {
+    q4u32x4 t;
+    __builtin_memcpy(&t, &v, 16);
+    asm volatile("" ::"v"(t));
+}
+
+// 16 bytes per lane from global memory straight into LDS: lane l writes
+// lds + 16 l (global_load_lds_dwordx4; lds must be uniform).
+__device__ __forceinline__ void q4_load_lds16(const void *src, void *lds) {
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)lds, 16, 0, 0);
+}
+
+
 template <int G, int MI, int NW>
-__global__ __launch_bounds__(64 * NW) void moe_q4k_kernel(MatmulArgs a) {
-    constexpr int THREADS = 64 * NW, ROWS = 16 * MI;
-    constexpr int LD = 256 + 8;                                    // f16 per staged row (+16 bytes: no bank conflicts)
-    constexpr int XV = ROWS * 256 / THREADS;                       // activations per thread per super-block
-    static_assert(ROWS * 256 % (8 * THREADS) == 0, "whole 16-byte runs per thread");
-    __shared__ __attribute__((aligned(16))) uint16_t xs[2][ROWS * LD];
-    __shared__ uint32_t tile_route[ROWS];
+__global__ __launch_bounds__(64 * NW) void moe_q4k_kernel(MatmulArgs a, uint32_t chunks) {
+    constexpr int ROWS = 16 * MI;
+    constexpr int XL = ROWS / (2 * NW);  // activation loads per lane per step (16 bytes each)
+    constexpr int STAGE = ROWS * 512;    // one super-block of f16 rows
+    constexpr int COLS = G == MM_GATE_UP ? 16 : 32;
+    constexpr int LOADS = XL + 6;        // vector loads per lane per step
+    static_assert(ROWS % (2 * NW) == 0, "whole 16-byte runs per lane");
+    static_assert(Q4_TILES * ROWS <= 64 * NW, "one thread per (tile, row) in the prologue");
+    // Three separate arrays, so the compiler can tell an LDS load of one stage
+    // from the asynchronous global->LDS loads into another (one array would
+    // make it wait for every outstanding load before each LDS read).
+    __shared__ __attribute__((aligned(16))) uint8_t xs0[STAGE], xs1[STAGE], xs2[STAGE];
+    __shared__ __attribute__((aligned(16))) uint32_t t_route[Q4_TILES][ROWS];
+    __shared__ __attribute__((aligned(16))) float t_inv[G == MM_DOWN ? Q4_TILES : 1][ROWS];
+    __shared__ __attribute__((aligned(16))) uint32_t t_info[Q4_TILES][4];  // expert, rows, first sorted row
+    __shared__ float u_bias[Q4_UNITS][2 * 16 * NW];  // gate/up: gate then up biases; down: biases
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c16 = lane & 15, q = lane >> 4;
-    // Logical (column group, tile), tile-major per XCD: the column groups of
-    // one tile share its activation rows in one L2.
-    const uint32_t used = gridDim.x * min(a.plan[1], gridDim.y);  // the plan's real tiles
-    const uint32_t lin = xcd_order(blockIdx.x + gridDim.x * blockIdx.y, used);
-    if (lin >= used) return;  // uniform: a surplus workgroup
-    const uint32_t bx = lin % gridDim.x, y = lin / gridDim.x;
-    const uint32_t expert = a.plan[6 + 2 * y], first = a.plan[7 + 2 * y];
+    const uint32_t grid = gridDim.x, lg = xcd_order(blockIdx.x, grid);
+    const uint32_t U = a.plan[1] * chunks;
+    const uint32_t lo = (uint32_t)((uint64_t)lg * U / grid), hi = (uint32_t)((uint64_t)(lg + 1) * U / grid);
+    if (lo >= hi) return;  // uniform
+    const uint32_t y0 = lo / chunks, ny = (hi - 1) / chunks - y0 + 1;  // <= Q4_TILES (launch)
+    const uint32_t nu = hi - lo;                                        // <= Q4_UNITS (launch)
+
+    // Tile prologue: per (tile, row) the route, the inverse row gain (down),
+    // and the tile's expert / row count / first expert-sorted row.
     const uint64_t grouped = 6 + 2 * ((uint64_t)(a.routes + 15) / 16 + a.experts);
-    const uint64_t list = grouped + (uint64_t)expert * (a.routes + 1);
     const uint64_t sorted = grouped + (uint64_t)a.experts * (a.routes + 1);
-    const uint32_t rows = min((uint32_t)ROWS, a.plan[list] - first);
-    const uint32_t sorted0 = a.plan[sorted + expert] + first;
-    for (uint32_t r = tid; r < rows; r += THREADS) tile_route[r] = a.plan[list + 1 + first + r];
+    {
+        const uint32_t ti = tid / ROWS, r = tid % ROWS;
+        if (ti < ny) {
+            const uint32_t y = y0 + ti;
+            const uint32_t expert = a.plan[6 + 2 * y], first = a.plan[7 + 2 * y];
+            const uint64_t list = grouped + (uint64_t)expert * (a.routes + 1);
+            const uint32_t rows = min((uint32_t)ROWS, a.plan[list] - first);
+            const uint32_t sorted0 = a.plan[sorted + expert] + first;
+            const uint32_t rr = min(r, rows - 1);  // padding rows repeat the last row (discarded)
+            t_route[ti][r] = a.plan[list + 1 + first + rr];
+            if constexpr (G == MM_DOWN) t_inv[ti][r] = 1.0f / row_gain(a.rowmax[sorted0 + rr]);
+            if (r == 0) {
+                t_info[ti][0] = expert;
+                t_info[ti][1] = rows;
+                t_info[ti][2] = sorted0;
+            }
+        }
+    }
+    // Biases of each unit's columns (as bf16, the reference's bias tensors;
+    // the up bias folds in the clipped SwiGLU's + 1).
+    for (uint32_t e = tid; e < nu * 2 * 16 * NW; e += 64 * NW) {
+        const uint32_t j = e / (2 * 16 * NW), c = e % (2 * 16 * NW), u = lo + j, y = u / chunks, ch = u - y * chunks;
+        const uint32_t expert = a.plan[6 + 2 * y];
+        float b = 0.f;
+        if constexpr (G == MM_GATE_UP) {
+            const bool up = c >= 16 * NW;
+            const uint32_t col = ch * (NW * COLS) + c % (16 * NW);
+            const float *bias = up ? a.bias2 : a.bias;
+            const float one = up && a.up_one ? 1.0f : 0.0f;
+            b = col < a.n && bias ? round_bf16(bias[(uint64_t)expert * a.n + col] + one) : one;
+        } else {
+            const uint32_t col = ch * (NW * COLS) + c;
+            b = col < a.n && a.bias ? round_bf16(a.bias[(uint64_t)expert * a.n + col]) : 0.f;
+        }
+        u_bias[j][c] = b;
+    }
     __syncthreads();
 
-    // This wavefront's two 16-row weight fragments.
-    const uint32_t col0 = (bx * NW + wave) * (G == MM_GATE_UP ? 16 : 32);
+    const uint32_t nsb = a.k / 256, T = nu * nsb;
+    const uint64_t xrow = (uint64_t)a.k * 2;
+    const uint8_t *x8 = reinterpret_cast<const uint8_t *>(a.x);
+
+    // Prefetch cursor: unit pu, super-block psb; per-lane source offsets.
+    uint32_t pu = lo, psb = 0;
+    uint32_t xoff[XL];
     const uint8_t *wrow[2];
+    auto set_unit = [&](uint32_t u) __attribute__((always_inline)) {
+        const uint32_t y = u / chunks, ch = u - y * chunks, ti = y - y0;
+        const uint32_t expert = __builtin_amdgcn_readfirstlane(t_info[ti][0]);
+        const uint32_t rows = __builtin_amdgcn_readfirstlane(t_info[ti][1]);
+        const uint32_t sorted0 = __builtin_amdgcn_readfirstlane(t_info[ti][2]);
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
-        const uint32_t col = G == MM_GATE_UP ? col0 + c16 : col0 + 16 * j + c16;
-        const uint8_t *base = (G == MM_GATE_UP && j == 1 ? a.w2 : a.w) + expert * a.expert_bytes;
-        wrow[j] = base + (uint64_t)min(col, a.n - 1) * a.row_bytes;
-    }
-    const uint32_t nsb = a.k / 256;
-
-    // Activation staging: run f = tid + THREADS i (i < RUNS) is row f / 32,
-    // 16-byte run f % 32 (consecutive lanes, consecutive runs: coalesced
-    // loads, conflict-free LDS stores).
-    constexpr int RUNS = XV / 8;
-    uint32_t xsrc[RUNS], xrun[RUNS], xrow_[RUNS];
-    bool xlive[RUNS];
-    float gain[G == MM_DOWN ? RUNS : 1];
+        for (int i = 0; i < XL; i++) {
+            const uint32_t r = 2 * (wave + NW * i) + (lane >> 5), j = (lane & 31) ^ (r & 15);
+            const uint32_t src = G == MM_GATE_UP ? t_route[ti][r] / a.topk : sorted0 + min(r, rows - 1);
+            xoff[i] = (uint32_t)(src * xrow) + 16 * j;
+        }
 #pragma unroll
-    for (int i = 0; i < RUNS; i++) {
-        const uint32_t f = tid + THREADS * i, r = f / 32;
-        xrow_[i] = r;
-        xrun[i] = f % 32;
-        xlive[i] = r < rows;
-        xsrc[i] = !xlive[i] ? 0u : G == MM_GATE_UP ? tile_route[r] / a.topk : sorted0 + r;
-        if constexpr (G == MM_DOWN) gain[i] = xlive[i] ? q4_row_gain(a.rowmax[xsrc[i]]) : 1.0f;
-    }
-    uint4 xv[RUNS * (G == MM_DOWN ? 2 : 1)];
-    auto xload = [&](uint32_t sb) {
-        sb = min(sb, nsb - 1);
-#pragma unroll
-        for (int i = 0; i < RUNS; i++) {
-            const uint64_t off = (uint64_t)xsrc[i] * a.k + (uint64_t)sb * 256 + 8 * xrun[i];
-            if constexpr (G == MM_DOWN) {
-                const uint4 *src = reinterpret_cast<const uint4 *>(reinterpret_cast<const float *>(a.x) + off);
-                xv[2 * i] = xlive[i] ? src[0] : make_uint4(0, 0, 0, 0);
-                xv[2 * i + 1] = xlive[i] ? src[1] : make_uint4(0, 0, 0, 0);
-            } else {
-                xv[i] = xlive[i] ? *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(a.x) + off)
-                                 : make_uint4(0, 0, 0, 0);
-            }
+        for (int f = 0; f < 2; f++) {
+            const uint32_t col = ch * (NW * COLS) + wave * COLS + (G == MM_GATE_UP ? 0 : 16 * f) + c16;
+            const uint8_t *base = (G == MM_GATE_UP && f == 1 ? a.w2 : a.w) + (uint64_t)expert * a.expert_bytes;
+            wrow[f] = base + (uint64_t)min(col, a.n - 1) * a.row_bytes;
         }
     };
-    auto xstore = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < RUNS; i++) {
-            uint16_t *dst = &xs[buf][xrow_[i] * LD + 8 * xrun[i]];
-            uint4 o;
-            if constexpr (G == MM_DOWN) {
-                const uint4 u0 = xv[2 * i], u1 = xv[2 * i + 1];
-                const float g = gain[i];
-                o = make_uint4(f16_pair(__uint_as_float(u0.x) * g, __uint_as_float(u0.y) * g),
-                               f16_pair(__uint_as_float(u0.z) * g, __uint_as_float(u0.w) * g),
-                               f16_pair(__uint_as_float(u1.x) * g, __uint_as_float(u1.y) * g),
-                               f16_pair(__uint_as_float(u1.z) * g, __uint_as_float(u1.w) * g));
-            } else {  // gate/up: the caller hands f16 rows
-                o = xv[i];
-            }
-            *reinterpret_cast<uint4 *>(dst) = o;
+    // Refill of stage nst / register set wn for the cursor's step, as
+    // LOADS items: 0..5 the weight loads (fragment k / 3: header, then the
+    // two halves of the lane's qs bytes), 6.. the activation rows.  The
+    // items are spread over the eight MFMA chunks of a step: issued all at
+    // once, every wavefront's loads queued behind each other's at the
+    // address units.
+    auto load_item = [&](auto kk, int nst, Q4Raw *wn) __attribute__((always_inline)) {
+        constexpr int K = decltype(kk)::value;
+        if constexpr (K < 6) {
+            constexpr int f = K / 3, part = K % 3;
+            const uint8_t *blk = wrow[f] + psb * 144;
+            if constexpr (part == 0) wn[f].hdr = ld_u128(blk);
+            if constexpr (part == 1) wn[f].q0 = ld_u128(blk + 16 + 32 * q);
+            if constexpr (part == 2) wn[f].q1 = ld_u128(blk + 32 + 32 * q);
+        } else {
+            constexpr int i = K - 6;
+            uint8_t *stage = nst == 0 ? xs0 : nst == 1 ? xs1 : xs2;
+            q4_load_lds16(x8 + xoff[i] + psb * 512, stage + (wave + NW * i) * 1024);
         }
     };
-    Q4Raw wr[2][2];  // [register stage][fragment]
-    auto wload = [&](Q4Raw *r, uint32_t sb) {
-        sb = min(sb, nsb - 1);
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const uint8_t *blk = wrow[j] + (uint64_t)sb * 144;
-            r[j].hdr = ld_u128(blk);
-            r[j].q0 = ld_u128(blk + 16 + 32 * q);
-            r[j].q1 = ld_u128(blk + 32 + 32 * q);
+    auto advance = [&]() __attribute__((always_inline)) {
+        if (++psb == nsb) {  // uniform
+            psb = 0;
+            if (++pu < hi) set_unit(pu);
         }
     };
-
     q4f32x4 acc[MI][2];
 #pragma unroll
     for (int i = 0; i < MI; i++)
 #pragma unroll
         for (int j = 0; j < 2; j++) acc[i][j] = q4f32x4{0.f, 0.f, 0.f, 0.f};
 
-    auto step = [&](const Q4Raw *r, int buf) {
+    // One step: eight MFMA chunks of 32 k, each issuing its share of the
+    // refill for step t + 2.
+    auto compute = [&](int st, const Q4Raw *r, int nst, Q4Raw *wn) __attribute__((always_inline)) {
+        const uint8_t *xb = (st == 0 ? xs0 : st == 1 ? xs1 : xs2) + c16 * 512;
         const Q4Scales s0 = q4_scales(r[0].hdr, q), s1 = q4_scales(r[1].hdr, q);
-        const uint16_t *xb = xs[buf];
-        auto chunk = [&](auto cc) {
+        auto chunk = [&](auto cc) __attribute__((always_inline)) {
             constexpr int C = decltype(cc)::value;
+            q4_static_for<C * LOADS / 8, (C + 1) * LOADS / 8>([&](auto kk) { load_item(kk, nst, wn); });
+            q4f16x8 av[MI];
+#pragma unroll
+            for (int i = 0; i < MI; i++)
+                __builtin_memcpy(&av[i], xb + i * 16 * 512 + 16 * ((8 * q + C) ^ c16), 16);
             const q4f16x8 b0 = q4_chunk<C>(r[0], s0), b1 = q4_chunk<C>(r[1], s1);
 #pragma unroll
             for (int i = 0; i < MI; i++) {
-                q4f16x8 av;
-                __builtin_memcpy(&av, &xb[(i * 16 + c16) * LD + 64 * q + 8 * C], 16);
-                acc[i][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b0, acc[i][0], 0, 0, 0);
-                acc[i][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b1, acc[i][1], 0, 0, 0);
+                acc[i][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], b0, acc[i][0], 0, 0, 0);
+                acc[i][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], b1, acc[i][1], 0, 0, 0);
             }
         };
-        chunk(std::integral_constant<int, 0>{});
-        chunk(std::integral_constant<int, 1>{});
-        chunk(std::integral_constant<int, 2>{});
-        chunk(std::integral_constant<int, 3>{});
-        chunk(std::integral_constant<int, 4>{});
-        chunk(std::integral_constant<int, 5>{});
-        chunk(std::integral_constant<int, 6>{});
-        chunk(std::integral_constant<int, 7>{});
+        q4_static_for<0, 8>(chunk);
+        advance();
     };
 
-    // Super-block sb: activations in LDS buffer sb % 2, weights in register
-    // stage sb % 2; sb + 1's activations are in registers, sb + 2's loading.
-    xload(0);
-    wload(wr[0], 0);
-    xstore(0);
-    xload(1);
-    wload(wr[1], 1);
-    __syncthreads();
-    uint32_t sb = 0;
-    for (; sb + 2 <= nsb; sb += 2) {  // whole pairs: register stages by name
-        step(wr[0], 0);
-        xstore(1);
-        xload(sb + 2);
-        wload(wr[0], sb + 2);
-        __syncthreads();
-        step(wr[1], 1);
-        xstore(0);
-        xload(sb + 3);
-        wload(wr[1], sb + 3);
-        __syncthreads();
-    }
-    if (sb < nsb) step(wr[0], 0);
+    // Gate/up: per lane, max |activation| bits of its rows over the tile's
+    // units so far.
+    uint32_t rmax[G == MM_GATE_UP ? MI : 1][4] = {};
 
     // C fragment: lane l holds column l % 16, rows 4 (l / 16) .. + 4.
-    const int cr = q * 4;
-    if constexpr (G == MM_GATE_UP) {
-        const uint32_t col = col0 + c16;
-        const bool cok = col < a.n;
-        const uint64_t bi = (uint64_t)expert * a.n + (cok ? col : 0);
-        const float bg = a.bias && cok ? round_bf16(a.bias[bi]) : 0.f;
-        const float bu = a.bias2 && cok ? round_bf16(a.bias2[bi] + (a.up_one ? 1.0f : 0.0f)) : (a.up_one ? 1.0f : 0.0f);
-#pragma unroll
-        for (int i = 0; i < MI; i++)
-#pragma unroll
-            for (int v = 0; v < 4; v++) {
-                const uint32_t r = i * 16 + cr + v;
-                const float act = expert_activation(a.act, acc[i][0][v] + bg, acc[i][1][v] + bu);
-                if (cok && r < rows) reinterpret_cast<float *>(a.y)[(uint64_t)(sorted0 + r) * a.n + col] = act;
-                uint32_t m = cok ? __float_as_uint(act) & 0x7fffffffu : 0u;
-#pragma unroll
-                for (int o = 1; o < 16; o <<= 1) m = max(m, (uint32_t)__shfl_xor((int)m, o));
-                if (c16 == 0 && r < rows) atomicMax(&a.rowmax[sorted0 + r], m);
-            }
-    } else {
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const uint32_t col = col0 + 16 * j + c16;
-            if (col >= a.n) continue;
-            const float b = a.bias ? round_bf16(a.bias[(uint64_t)expert * a.n + col]) : 0.f;
+    auto epilogue = [&](uint32_t u) __attribute__((always_inline)) {
+        const uint32_t y = u / chunks, ch = u - y * chunks, ti = y - y0;
+        const float *ub = u_bias[u - lo];
+        const int cr = q * 4;
+        q4u32x4 info = q4_lds_b128(t_info[ti]);
+        if constexpr (G == MM_GATE_UP) {
+            uint32_t bgb = q4_lds_b32(ub + wave * 16 + c16), bub = q4_lds_b32(ub + 16 * NW + wave * 16 + c16);
+            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(info), "+v"(bgb), "+v"(bub));
+            const uint32_t rows = info.y, sorted0 = info.z;
+            const float bg = __uint_as_float(bgb), bu = __uint_as_float(bub);
+            const uint32_t col = ch * (NW * COLS) + wave * COLS + c16;
+            const bool cok = col < a.n;
 #pragma unroll
             for (int i = 0; i < MI; i++)
 #pragma unroll
                 for (int v = 0; v < 4; v++) {
                     const uint32_t r = i * 16 + cr + v;
-                    if (r >= rows) continue;
-                    const float val = acc[i][j][v] / q4_row_gain(a.rowmax[sorted0 + r]) + b;
-                    const uint64_t o = (uint64_t)tile_route[r] * a.n + col;
-                    if (a.y_bf16)
-                        reinterpret_cast<uint16_t *>(a.y)[o] = f32_to_bf16_bits(val);
-                    else
-                        reinterpret_cast<float *>(a.y)[o] = val;
+                    const float act = expert_activation(a.act, acc[i][0][v] + bg, acc[i][1][v] + bu);
+                    if (cok && r < rows) reinterpret_cast<float *>(a.y)[(uint64_t)(sorted0 + r) * a.n + col] = act;
+                    if (cok) rmax[i][v] = max(rmax[i][v], __float_as_uint(act) & 0x7fffffffu);
                 }
+            // Row maxima go out once per (workgroup, tile): after the tile's
+            // last unit in this range.
+            if (u + 1 == hi || (u + 1) / chunks != y) {
+#pragma unroll
+                for (int i = 0; i < MI; i++)
+#pragma unroll
+                    for (int v = 0; v < 4; v++) {
+                        const uint32_t r = i * 16 + cr + v, m = q4_row_max(rmax[i][v]);
+                        if (c16 == 0 && r < rows) atomicMax(&a.rowmax[sorted0 + r], m);
+                        rmax[i][v] = 0;
+                    }
+            }
+        } else {
+            // this lane's rows 16 i + 4 q .. + 3: routes and inverse gains
+            uint32_t bb[2];
+            q4u32x4 rt[MI], ig[MI];
+#pragma unroll
+            for (int f = 0; f < 2; f++) bb[f] = q4_lds_b32(ub + wave * COLS + 16 * f + c16);
+#pragma unroll
+            for (int i = 0; i < MI; i++) {
+                rt[i] = q4_lds_b128(&t_route[ti][i * 16 + cr]);
+                ig[i] = q4_lds_b128(&t_inv[ti][i * 16 + cr]);
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(info), "+v"(bb[0]), "+v"(bb[1]));
+#pragma unroll
+            for (int i = 0; i < MI; i++) asm volatile("" : "+v"(rt[i]), "+v"(ig[i]));
+            const uint32_t rows = info.y;
+#pragma unroll
+            for (int f = 0; f < 2; f++) {
+                const uint32_t col = ch * (NW * COLS) + wave * COLS + 16 * f + c16;
+                if (col >= a.n) continue;
+                const float b = __uint_as_float(bb[f]);
+#pragma unroll
+                for (int i = 0; i < MI; i++)
+#pragma unroll
+                    for (int v = 0; v < 4; v++) {
+                        const uint32_t r = i * 16 + cr + v;
+                        if (r >= rows) continue;
+                        // the inverse gain is a power of two: exact, as the division
+                        const float val = acc[i][f][v] * __uint_as_float(ig[i][v]) + b;
+                        const uint64_t o = (uint64_t)rt[i][v] * a.n + col;
+                        if (a.y_bf16)
+                            reinterpret_cast<uint16_t *>(a.y)[o] = f32_to_bf16_bits(val);
+                        else
+                            reinterpret_cast<float *>(a.y)[o] = val;
+                    }
+            }
         }
+#pragma unroll
+        for (int i = 0; i < MI; i++)
+#pragma unroll
+            for (int j = 0; j < 2; j++) acc[i][j] = q4f32x4{0.f, 0.f, 0.f, 0.f};
+    };
+
+    // Step t computes stage t % 3 with register set t % 3 and refills stage
+    // and set (t + 2) % 3, consumed at step t - 1; past the last step the
+    // refills repeat the last unit's first super-block, never consumed.
+    Q4Raw w0[2], w1[2], w2[2];
+    set_unit(lo);
+    // Steps 0 and 1's loads.
+    q4_static_for<0, LOADS>([&](auto kk) { load_item(kk, 0, w0); });
+    advance();
+    q4_static_for<0, LOADS>([&](auto kk) { load_item(kk, 1, w1); });
+    advance();
+    uint32_t cu = lo, csb = 0;
+    bool pend = false;  // unit cu - 1's results are in acc, not yet stored
+    // Start of step t (compute register set wc): its loads landed in every
+    // wavefront, a finished unit's stores go out, and wc is marked in use
+    // (the compiler's own wait for it then sits here, where it has landed).
+    auto start = [&](int t, const Q4Raw *wc) __attribute__((always_inline)) {
+        q4_vm_wait<LOADS>();                      // step t's loads (step t + 1's may be in flight)
+        asm volatile("s_barrier" ::: "memory");  // every wavefront's LDS loads landed; stage (t + 2) % 3 is free
+#pragma unroll
+        for (int f = 0; f < 2; f++) {
+            q4_touch(wc[f].hdr);
+            q4_touch(wc[f].q0);
+            q4_touch(wc[f].q1);
+        }
+        // A finished unit's stores go out before this step's loads, so that
+        // reusing their registers later waits only as far as those loads.
+        if (pend) {
+            epilogue(cu - 1);
+            pend = false;
+        }
+    };
+    auto body = [&](int st, int t, const Q4Raw *wc, Q4Raw *wn) __attribute__((always_inline)) {
+        compute(st, wc, (st + 2) % 3, wn);  // issues step t + 2's loads on the way
+        if (++csb == nsb) {
+            csb = 0;
+            cu++;
+            pend = true;
+        }
+    };
+    // The loop starts with step t's compute (its start is the previous
+    // iteration's last act, or the prologue's), so that its entry and its
+    // back edge hold the same loads in flight.
+    start(0, w0);
+    for (int t = 0;; t += 3) {
+        body(0, t, w0, w2);
+        if (t + 1 >= (int)T) break;
+        start(t + 1, w1);
+        body(1, t + 1, w1, w0);
+        if (t + 2 >= (int)T) break;
+        start(t + 2, w2);
+        body(2, t + 2, w2, w1);
+        if (t + 3 >= (int)T) break;
+        start(t + 3, w0);
     }
+    epilogue(cu - 1);  // the last unit ends on the last step
+    q4_vm_wait<0>();  // no LDS load may land after the workgroup exits
 }
 
-// Eight wavefronts (two per SIMD); rows per tile bm = 16 MI routes (32, 48 or 64).
+// Eight wavefronts (two per SIMD; the registers allow no more); rows per
+// tile bm = 16 MI routes (32, 48 or 64).
 constexpr int Q4_NW = 8;
 
-template <int MI>
-static void q4_launch(int mode, const MatmulArgs &a, dim3 grid, hipStream_t stream) {
-    if (mode == MM_GATE_UP)
-        hipLaunchKernelGGL((moe_q4k_kernel<MM_GATE_UP, MI, Q4_NW>), grid, dim3(64 * Q4_NW), 0, stream, a);
-    else
-        hipLaunchKernelGGL((moe_q4k_kernel<MM_DOWN, MI, Q4_NW>), grid, dim3(64 * Q4_NW), 0, stream, a);
+template <int G, int MI>
+static int q4_launch(const MatmulArgs &a, uint32_t bm, hipStream_t stream) {
+    static int per_cu = 0, cus = 0;
+    if (!per_cu) {
+        int dev = 0;
+        (void)hipGetDevice(&dev);
+        (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, moe_q4k_kernel<G, MI, Q4_NW>, 64 * Q4_NW, 0) != hipSuccess || per_cu <= 0)
+            per_cu = 1;
+        if (cus <= 0) cus = 256;
+    }
+    const uint32_t cols = (G == MM_GATE_UP ? 16 : 32) * Q4_NW;
+    const uint32_t chunks = (a.n + cols - 1) / cols;
+    const uint64_t max_units = (uint64_t)((a.routes + bm - 1) / bm + a.experts) * chunks;
+    // Enough workgroups that no range holds more than Q4_UNITS units or
+    // spans more than Q4_TILES tiles.
+    const uint64_t span = std::min<uint64_t>(Q4_UNITS, (uint64_t)(Q4_TILES - 1) * chunks + 1);
+    uint64_t grid = std::min<uint64_t>(max_units, (uint64_t)per_cu * cus);
+    grid = std::max<uint64_t>(grid, (max_units + span - 1) / span);
+    if (grid > 0x7fffffffu) return fail(OCO_ERR_INVALID, "experts: Q4_K grid of %llu units", (unsigned long long)max_units);
+    hipLaunchKernelGGL((moe_q4k_kernel<G, MI, Q4_NW>), dim3((unsigned)grid), dim3(64 * Q4_NW), 0, stream, a, chunks);
+    return OCO_OK;
 }
+
 
 int moe_q4k_launch(int mode, const MatmulArgs &a, uint32_t bm, hipStream_t stream) {
     if (a.k % 256) return fail(OCO_ERR_INVALID, "experts: Q4_K rows need k %% 256 == 0 (k=%u)", a.k);
     if (bm != 32 && bm != 48 && bm != 64) return fail(OCO_ERR_INVALID, "experts: Q4_K tile of %u rows", bm);
-    const uint32_t cols = (mode == MM_GATE_UP ? 16 : 32) * Q4_NW;
-    const dim3 grid((a.n + cols - 1) / cols, (a.routes + bm - 1) / bm + a.experts);
-    if (bm == 32) q4_launch<2>(mode, a, grid, stream);
-    if (bm == 48) q4_launch<3>(mode, a, grid, stream);
-    if (bm == 64) q4_launch<4>(mode, a, grid, stream);
+    // Activation rows are addressed with 32-bit byte offsets.
+    const uint64_t xrows = mode == MM_GATE_UP ? (uint64_t)a.routes / std::max(a.topk, 1u) : (uint64_t)a.routes;
+    if (xrows * a.k * 2 >= 0xffffffffull)
+        return fail(OCO_ERR_INVALID, "experts: Q4_K activations of %llu bytes exceed 4 GiB",
+                    (unsigned long long)(xrows * a.k * 2));
+    int rc = OCO_OK;
+    if (mode == MM_GATE_UP) {
+        if (bm == 32) rc = q4_launch<MM_GATE_UP, 2>(a, bm, stream);
+        if (bm == 48) rc = q4_launch<MM_GATE_UP, 3>(a, bm, stream);
+        if (bm == 64) rc = q4_launch<MM_GATE_UP, 4>(a, bm, stream);
+    } else {
+        if (bm == 32) rc = q4_launch<MM_DOWN, 2>(a, bm, stream);
+        if (bm == 48) rc = q4_launch<MM_DOWN, 3>(a, bm, stream);
+        if (bm == 64) rc = q4_launch<MM_DOWN, 4>(a, bm, stream);
+    }
+    OCO_TRY(rc);
     return launch_check("experts Q4_K grouped matmul");
 }
 
