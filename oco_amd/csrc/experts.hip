@@ -350,31 +350,6 @@ constexpr uint32_t MOE_MFMA_TOKENS = 32;
 // MXFP4 banks take the block-scaled MFMA path from this many tokens on.
 constexpr uint32_t MOE_MX_TOKENS = 8;  // measured: B=16 331 -> 237 us; B=4 is faster on the routed kernel
 
-// Activation rows to f16 (the reference's half(x)) from f32 or bf16, four
-// elements per thread; the same launch clears `nzero` words at `zero` (the
-// per-row activation maxima the gate/up tiles accumulate with atomics).
-template <typename XT>
-__global__ __launch_bounds__(256) void to_f16_kernel(const XT *x, uint16_t *y, uint64_t n, uint32_t *zero,
-                                                     uint32_t nzero) {
-    const uint64_t t = (uint64_t)blockIdx.x * 256 + threadIdx.x;
-    if (t < nzero) zero[t] = 0;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const uint64_t i = 4 * t + j;
-        if (i < n) {
-            float v;
-            if constexpr (sizeof(XT) == 4)
-                v = x[i];
-            else
-                v = __uint_as_float((uint32_t)x[i] << 16);
-            const _Float16 h = (_Float16)v;
-            uint16_t b;
-            __builtin_memcpy(&b, &h, 2);
-            y[i] = b;
-        }
-    }
-}
-
 // Gate/up activations to f16 rows for the Q4_K down tiles: each row scaled
 // by the power of two (row_gain) that brings its max |activation| into
 // [2^14, 2^15), which is exact, then rounded to f16; the down epilogue
@@ -493,17 +468,13 @@ int oco_experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype, co
         // Rows per tile: most experts in one tile (mean routes per expert,
         // plus room for the spread).
         const uint32_t mean = routes / w->experts;
-        const uint32_t bm = q4 ? (getenv("OCO_Q4_BM") ? (uint32_t)atoi(getenv("OCO_Q4_BM")) : mean <= 20 ? 32 : mean <= 36 ? 48 : 64) : (mean <= 40 ? 32 : 64);
-        OCO_TRY(oco_route_plan(ids, routes, w->experts, bm, 0, 0, plan, stream));
-        // The tiles take f16 rows (the reference's half(x)).
-        const uint64_t nx = (uint64_t)tokens * w->hidden;
-        const dim3 gx((unsigned)std::max<uint64_t>((nx + 1023) / 1024, (routes + 255) / 256));
-        if (x_dtype == OCO_DT_F32)
-            hipLaunchKernelGGL(to_f16_kernel<float>, gx, dim3(256), 0, s, (const float *)x, x16, nx, rowmax, routes);
-        else
-            hipLaunchKernelGGL(to_f16_kernel<uint16_t>, gx, dim3(256), 0, s, (const uint16_t *)x, x16, nx, rowmax,
-                               routes);
-        OCO_TRY(launch_check("experts f16 inputs"));
+        const uint32_t bm = q4 ? (getenv("OCO_Q4_BM") ? (uint32_t)atoi(getenv("OCO_Q4_BM"))  // env: tuning runs only
+                                                      : mean <= 20 ? 32 : mean <= 36 ? 48 : 64)
+                               : (mean <= 40 ? 32 : 64);
+        // The tiles take f16 rows (the reference's half(x)); the conversion
+        // and the clearing of the row maxima run beside the plan.
+        const PlanSide side = {x, x_dtype == OCO_DT_BF16 ? 1u : 0u, x16, (uint64_t)tokens * w->hidden, rowmax, routes};
+        OCO_TRY(route_plan_launch(ids, routes, w->experts, bm, 0, 0, plan, &side, s));
         const void *xin = x16;
         MatmulArgs g = {};
         g.w = (const uint8_t *)w->gate;

@@ -4,6 +4,22 @@
 
 namespace oco {
 
+// A job run beside the route plan, in the same launch (workgroups 1..):
+// activation rows to f16 (the reference's half(x)) from bf16 or f32, four
+// elements per thread, and `nzero` words of `zero` cleared.
+struct PlanSide {
+    const void *x;
+    uint32_t x_bf16;
+    uint16_t *y;
+    uint64_t n;
+    uint32_t *zero;
+    uint32_t nzero;
+};
+
+// oco_route_plan with an optional side job (null: none).
+int route_plan_launch(const uint32_t *ids, uint32_t routes, uint32_t experts, uint32_t tile_rows, uint32_t up_tiles,
+                      uint32_t down_tiles, uint32_t *plan, const PlanSide *side, hipStream_t stream);
+
 // Wave-wide max / min over 64 lanes with DPP and permlane swaps (all lanes
 // receive the result).
 template <int CTRL>

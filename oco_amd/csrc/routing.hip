@@ -53,7 +53,21 @@ constexpr uint32_t PLAN_HIST_EXPERTS = 256;  // per-wavefront histograms in LDS 
 __global__ __launch_bounds__(PLAN_THREADS) void route_plan_kernel(const uint32_t *ids, uint32_t routes,
                                                                   uint32_t experts, uint32_t tile_rows,
                                                                   uint32_t up_tiles, uint32_t down_tiles,
-                                                                  uint32_t *plan) {
+                                                                  uint32_t *plan, PlanSide side) {
+    if (blockIdx.x > 0) {  // the side job: four elements and one cleared word per thread
+        const uint64_t t = (uint64_t)(blockIdx.x - 1) * PLAN_THREADS + threadIdx.x;
+        if (t < side.nzero) side.zero[t] = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint64_t i = 4 * t + j;
+            if (i >= side.n) break;
+            const float v = side.x_bf16 ? __uint_as_float((uint32_t)reinterpret_cast<const uint16_t *>(side.x)[i] << 16)
+                                        : reinterpret_cast<const float *>(side.x)[i];
+            const _Float16 h = (_Float16)v;
+            __builtin_memcpy(&side.y[i], &h, 2);
+        }
+        return;
+    }
     // LDS: chunk ids [1024]; run, tile base, offset [experts]; per-wavefront
     // histograms [16][experts] (experts <= PLAN_HIST_EXPERTS)
     extern __shared__ __attribute__((aligned(16))) uint32_t sh[];
@@ -239,6 +253,27 @@ __global__ __launch_bounds__(256) void moe_sum8_kernel(const uint16_t *routes, c
 
 using namespace oco;
 
+namespace oco {
+
+int route_plan_launch(const uint32_t *ids, uint32_t routes, uint32_t experts, uint32_t tile_rows, uint32_t up_tiles,
+                      uint32_t down_tiles, uint32_t *plan, const PlanSide *side, hipStream_t stream) {
+    if (!ids || !plan) return fail(OCO_ERR_INVALID, "oco_route_plan: null pointer");
+    if (experts == 0 || experts > 4096 || tile_rows < 16)
+        return fail(OCO_ERR_INVALID,
+                    "oco_route_plan: need 0 < experts <= 4096 and tile_rows >= 16 (the plan holds ceil(routes/16) + "
+                    "experts tiles)");
+    PlanSide sj = side ? *side : PlanSide{};
+    const uint64_t side_blocks =
+        std::max<uint64_t>((sj.n + 4 * PLAN_THREADS - 1) / (4 * PLAN_THREADS), (sj.nzero + PLAN_THREADS - 1) / PLAN_THREADS);
+    if (side_blocks >= 0x7fffffffu) return fail(OCO_ERR_INVALID, "oco_route_plan: side job of %llu elements", (unsigned long long)sj.n);
+    hipLaunchKernelGGL(route_plan_kernel, dim3(1 + (unsigned)side_blocks), dim3(PLAN_THREADS),
+                       (size_t)(PLAN_THREADS + 3 * experts + (experts <= PLAN_HIST_EXPERTS ? 16 * experts : 0)) * 4,
+                       stream, ids, routes, experts, tile_rows, up_tiles, down_tiles, plan, sj);
+    return launch_check("oco_route_plan");
+}
+
+}  // namespace oco
+
 extern "C" {
 
 int oco_route_select(const float *logits, uint32_t tokens, uint32_t experts, uint32_t k, uint32_t *ids,
@@ -290,18 +325,13 @@ uint64_t oco_route_plan_words(uint32_t routes, uint32_t experts) {
            routes;
 }
 
+
 int oco_route_plan(const uint32_t *ids, uint32_t routes, uint32_t experts, uint32_t tile_rows,
                    uint32_t up_tiles, uint32_t down_tiles, uint32_t *plan, oco_stream stream) {
-    if (!ids || !plan) return fail(OCO_ERR_INVALID, "oco_route_plan: null pointer");
-    if (experts == 0 || experts > 4096 || tile_rows < 16)
-        return fail(OCO_ERR_INVALID,
-                    "oco_route_plan: need 0 < experts <= 4096 and tile_rows >= 16 (the plan holds ceil(routes/16) + "
-                    "experts tiles)");
-    hipLaunchKernelGGL(route_plan_kernel, dim3(1), dim3(PLAN_THREADS),
-                       (size_t)(PLAN_THREADS + 3 * experts + (experts <= PLAN_HIST_EXPERTS ? 16 * experts : 0)) * 4,
-                       (hipStream_t)stream, ids, routes, experts, tile_rows, up_tiles, down_tiles, plan);
-    return launch_check("oco_route_plan");
+    return route_plan_launch(ids, routes, experts, tile_rows, up_tiles, down_tiles, plan, nullptr,
+                             (hipStream_t)stream);
 }
+
 
 int oco_moe_sum(const void *routes, oco_dtype routes_dtype, const float *probs, uint16_t *out,
                 uint32_t hidden, uint32_t tokens, uint32_t k, oco_stream stream) {
