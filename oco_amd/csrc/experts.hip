@@ -260,27 +260,32 @@ __global__ __launch_bounds__(256) void moe_kernel(MoeArgs a) {
 }
 
 typedef void (*MoeFn)(MoeArgs);
-constexpr int MOE_T = 4;  // routes per tile
+constexpr int MOE_T = 4;  // routes per tile (plan tiles); one-route tiles without a plan use T = 1
 
-template <int FMT, bool GATED>
+template <int FMT, bool GATED, int T>
 static MoeFn moe_pick(int npl) {
     switch (npl) {
-    case 1: return moe_kernel<FMT, GATED, MOE_T, 1>;
-    case 2: return moe_kernel<FMT, GATED, MOE_T, 2>;
-    case 3: return moe_kernel<FMT, GATED, MOE_T, 3>;
-    case 4: return moe_kernel<FMT, GATED, MOE_T, 4>;
+    case 1: return moe_kernel<FMT, GATED, T, 1>;
+    case 2: return moe_kernel<FMT, GATED, T, 2>;
+    case 3: return moe_kernel<FMT, GATED, T, 3>;
+    case 4: return moe_kernel<FMT, GATED, T, 4>;
     }
     return nullptr;
 }
 
-static MoeFn moe_pick_format(uint32_t fmt, bool gated, int npl) {
+template <int T>
+static MoeFn moe_pick_t(uint32_t fmt, bool gated, int npl) {
     switch (fmt) {
-    case OCO_MXFP4: return gated ? moe_pick<OCO_MXFP4, true>(npl) : moe_pick<OCO_MXFP4, false>(npl);
-    case OCO_Q4_K: return gated ? moe_pick<OCO_Q4_K, true>(npl) : moe_pick<OCO_Q4_K, false>(npl);
-    case OCO_Q6_K: return gated ? moe_pick<OCO_Q6_K, true>(npl) : moe_pick<OCO_Q6_K, false>(npl);
-    case OCO_Q8_0: return gated ? moe_pick<OCO_Q8_0, true>(npl) : moe_pick<OCO_Q8_0, false>(npl);
+    case OCO_MXFP4: return gated ? moe_pick<OCO_MXFP4, true, T>(npl) : moe_pick<OCO_MXFP4, false, T>(npl);
+    case OCO_Q4_K: return gated ? moe_pick<OCO_Q4_K, true, T>(npl) : moe_pick<OCO_Q4_K, false, T>(npl);
+    case OCO_Q6_K: return gated ? moe_pick<OCO_Q6_K, true, T>(npl) : moe_pick<OCO_Q6_K, false, T>(npl);
+    case OCO_Q8_0: return gated ? moe_pick<OCO_Q8_0, true, T>(npl) : moe_pick<OCO_Q8_0, false, T>(npl);
     }
     return nullptr;
+}
+
+static MoeFn moe_pick_format(uint32_t fmt, bool gated, int npl, int t) {
+    return t == 1 ? moe_pick_t<1>(fmt, gated, npl) : moe_pick_t<MOE_T>(fmt, gated, npl);
 }
 
 static int device_cus() {
@@ -303,7 +308,10 @@ static int moe_launch(uint32_t fmt, bool gated, MoeArgs a, uint32_t tiles, uint3
     const uint32_t P = (fmt == OCO_Q4_K || fmt == OCO_Q6_K) ? 8 : 1;
     const uint32_t pieces = a.k / be * P;
     const int npl = (int)((pieces + 31) / 32);
-    MoeFn fn = npl <= 4 ? moe_pick_format(fmt, gated, npl) : nullptr;
+    // Without a plan every tile is one route: a one-route kernel, whose
+    // staged activations take a quarter of the LDS.
+    const int t = a.plan ? MOE_T : 1;
+    MoeFn fn = npl <= 4 ? moe_pick_format(fmt, gated, npl, t) : nullptr;
     if (!fn)
         return fail(OCO_ERR_UNSUPPORTED, "experts: format %u with k=%u has no routed kernel (rows over %u bytes)",
                     fmt, a.k, 4 * 32 * bb / P);
@@ -311,13 +319,14 @@ static int moe_launch(uint32_t fmt, bool gated, MoeArgs a, uint32_t tiles, uint3
     a.ngroups = (a.n + 7) / 8;
     const uint32_t nsum = fmt == OCO_Q8_0 ? 1 : fmt == OCO_Q4_K ? 2 : fmt == OCO_Q6_K ? 4 : 0;
     const int lpr = (npl * 32 * (int)bb / (int)P + 32 + 1023) / 1024;
-    const size_t lds = (size_t)MOE_T * a.k * 4 + (size_t)MOE_T * nsum * (a.k / 32) * 4 +
+    const size_t lds = (size_t)t * a.k * 4 + (size_t)t * nsum * (a.k / 32) * 4 +
                        4 * (size_t)(2 * (gated ? 2 : 1) * lpr * 1024);
     if (lds > 150 * 1024) return fail(OCO_ERR_UNSUPPORTED, "experts: k=%u needs %zu bytes of LDS", a.k, lds);
     if (lds > 64 * 1024)
         OCO_TRY(hip_check(hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
                           "hipFuncSetAttribute"));
-    const uint32_t target = 2 * device_cus();
+    static const uint32_t per_cu = getenv("OCO_MOE_WG") ? (uint32_t)atoi(getenv("OCO_MOE_WG")) : 2;  // tuning runs only
+    const uint32_t target = per_cu * device_cus();
     uint32_t gx = std::max<uint32_t>(1, target / std::max<uint32_t>(1, parallel_tiles));
     gx = std::min(gx, a.ngroups);
     hipLaunchKernelGGL(fn, dim3(gx, tiles), dim3(256), lds, stream, a);
