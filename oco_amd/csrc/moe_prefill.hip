@@ -54,20 +54,20 @@ __device__ __forceinline__ Q4Scales q4_scales(const uint4 &hdr, int q) {
     // scales[12] = hdr.y (bytes 0..3), hdr.z (4..7), hdr.w (8..11); sub-block
     // j < 4: sc = scales[j] & 63, mn = scales[j+4] & 63; j >= 4: sc =
     // (scales[j+4] & 15) | (scales[j-4] >> 6) << 4, mn = (scales[j+4] >> 4) |
-    // (scales[j] >> 6) << 4.  Pair q holds j = 2q, 2q + 1: bit offsets per
-    // lane, one select between the two forms.
-    uint32_t sc[2], mn[2];
-#pragma unroll
-    for (int h = 0; h < 2; h++) {
-        const uint32_t t = 8 * ((2 * q + h) & 3);
-        const uint32_t sc_lo = __builtin_amdgcn_ubfe(hdr.y, t, 6), mn_lo = __builtin_amdgcn_ubfe(hdr.z, t, 6);
-        const uint32_t sc_hi = __builtin_amdgcn_ubfe(hdr.w, t, 4) | (__builtin_amdgcn_ubfe(hdr.y, t + 6, 2) << 4);
-        const uint32_t mn_hi = __builtin_amdgcn_ubfe(hdr.w, t + 4, 4) | (__builtin_amdgcn_ubfe(hdr.z, t + 6, 2) << 4);
-        sc[h] = q < 2 ? sc_lo : sc_hi;
-        mn[h] = q < 2 ? mn_lo : mn_hi;
-    }
+    // (scales[j] >> 6) << 4.  Pair q holds j = 2q, 2q + 1; with b = 2 (q & 1)
+    // both forms read bytes b, b + 1 of hdr.y and hdr.z, and the second also
+    // bytes b, b + 1 of hdr.w, so two byte permutes gather the lane's
+    // [sc0, sc1, mn0, mn1].
+    const uint32_t b = 2u * (uint32_t)(q & 1);
+    const uint32_t sel = b | ((b + 1) << 8) | ((b + 4) << 16) | ((b + 5) << 24);
+    const uint32_t yz = __builtin_amdgcn_perm(hdr.z, hdr.y, sel);                                 // y_b, y_b1, z_b, z_b1
+    const uint32_t ww = __builtin_amdgcn_perm(hdr.w, hdr.w, (sel & 0x0000ffffu) | ((sel & 0xffffu) << 16));  // w_b, w_b1, w_b, w_b1
+    const uint32_t lo6 = yz & 0x3f3f3f3fu;
+    const uint32_t hi6 = (ww & 0x00000f0fu) | ((ww >> 4) & 0x0f0f0000u) | ((yz >> 2) & 0x30303030u);
+    const uint32_t v = q < 2 ? lo6 : hi6;
     const float d = half_bits_to_f32(hdr.x & 0xffffu), dmin = half_bits_to_f32(hdr.x >> 16);
-    return {d * (float)sc[0], dmin * (float)mn[0], d * (float)sc[1], dmin * (float)mn[1]};
+    return {d * (float)(v & 0xffu), dmin * (float)((v >> 16) & 0xffu), d * (float)((v >> 8) & 0xffu),
+            dmin * (float)(v >> 24)};
 }
 
 // Four weights from the nibbles of one dword (one per byte, high nibbles
