@@ -357,7 +357,7 @@ static uint64_t align256(uint64_t v) { return (v + 255) & ~255ull; }
 // GEMMs over the route plan's expert tiles.
 constexpr uint32_t MOE_MFMA_TOKENS = 32;
 // MXFP4 banks take the block-scaled MFMA path from this many tokens on.
-constexpr uint32_t MOE_MX_TOKENS = 8;  // measured: B=16 331 -> 237 us; B=4 is faster on the routed kernel
+constexpr uint32_t MOE_MX_TOKENS = 4;  // measured (gpt-oss): B=4 on these tiles beats the routed kernel, B=1 does not
 
 // Gate/up activations to f16 rows for the Q4_K down tiles: each row scaled
 // by the power of two (row_gain) that brings its max |activation| into
@@ -432,7 +432,9 @@ int oco_experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype, co
     if (tiled && w->format == OCO_MXFP4 && tokens >= mx_tokens) {
         // MXFP4 banks: block-scaled FP8 x FP4 MFMA on the GGUF bytes (no
         // weight decode); activations split per row into E4M3 terms.
-        OCO_TRY(oco_route_plan(ids, routes, w->experts, 32, 0, 0, plan, stream));
+        // Decode batches take 16-row tiles (half the staged activations).
+        const uint32_t tile_rows = tokens <= 16 ? 16 : 32;
+        OCO_TRY(oco_route_plan(ids, routes, w->experts, tile_rows, 0, 0, plan, stream));
         const int xterms = x_dtype == OCO_DT_BF16 ? 2 : 3;  // bf16 rows are exact in two terms
         OCO_TRY(mx_rows_split(x, x_dtype == OCO_DT_BF16, xrec, tokens, w->hidden, xterms, s));
         MatmulArgs g = {};
@@ -452,7 +454,7 @@ int oco_experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype, co
         g.topk = w->k;
         g.act = w->activation;
         g.up_one = w->up_bias_one;
-        OCO_TRY(mx_experts_launch(MM_GATE_UP, g, xrec, xterms, s));
+        OCO_TRY(mx_experts_launch(MM_GATE_UP, g, xrec, xterms, tile_rows, s));
         OCO_TRY(mx_rows_split(act, false, arec, routes, w->ffn, 3, s));
         MatmulArgs d = g;
         d.w = (const uint8_t *)w->down;
@@ -465,7 +467,7 @@ int oco_experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype, co
         d.k = w->ffn;
         d.row_bytes = oco_row_bytes(w->format, w->ffn);
         d.expert_bytes = d.row_bytes * w->hidden;
-        OCO_TRY(mx_experts_launch(MM_DOWN, d, arec, 3, s));
+        OCO_TRY(mx_experts_launch(MM_DOWN, d, arec, 3, tile_rows, s));
         return oco_moe_sum(down, routed ? OCO_DT_F32 : OCO_DT_BF16, probs, out, w->hidden, tokens, w->k, stream);
     }
 
