@@ -434,15 +434,22 @@ int oco_experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype, co
         // weight decode); activations split per row into E4M3 terms.
         // Decode batches take 16-row tiles (half the staged activations).
         const uint32_t tile_rows = tokens <= 16 ? 16 : 32;
-        OCO_TRY(oco_route_plan(ids, routes, w->experts, tile_rows, 0, 0, plan, stream));
+        // The input rows' split runs beside the plan; the activations are
+        // split by the gate/up tiles themselves.
         const int xterms = x_dtype == OCO_DT_BF16 ? 2 : 3;  // bf16 rows are exact in two terms
-        OCO_TRY(mx_rows_split(x, x_dtype == OCO_DT_BF16, xrec, tokens, w->hidden, xterms, s));
+        PlanSide side = {};
+        side.x = x;
+        side.x_bf16 = x_dtype == OCO_DT_BF16 ? 1u : 0u;
+        side.rec = xrec;
+        side.rows = tokens;
+        side.k = w->hidden;
+        OCO_TRY(route_plan_launch(ids, routes, w->experts, tile_rows, 0, 0, plan, &side, s));
         MatmulArgs g = {};
         g.w = (const uint8_t *)w->gate;
         g.w2 = (const uint8_t *)w->up;
         g.bias = w->gate_bias;
         g.bias2 = w->up_bias;
-        g.y = act;  // f32 [routes][ffn], expert-sorted rows
+        g.yrec = arec;  // split records [routes][ffn], expert-sorted rows
         g.m = routes;
         g.n = w->ffn;
         g.k = w->hidden;
@@ -455,8 +462,8 @@ int oco_experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype, co
         g.act = w->activation;
         g.up_one = w->up_bias_one;
         OCO_TRY(mx_experts_launch(MM_GATE_UP, g, xrec, xterms, tile_rows, s));
-        OCO_TRY(mx_rows_split(act, false, arec, routes, w->ffn, 3, s));
         MatmulArgs d = g;
+        d.yrec = nullptr;
         d.w = (const uint8_t *)w->down;
         d.w2 = nullptr;
         d.bias = w->down_bias;

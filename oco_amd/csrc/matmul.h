@@ -20,6 +20,7 @@ struct MatmulArgs {
     uint64_t expert_bytes; // bytes of one expert's matrix
     uint32_t routes, experts, topk, act, up_one;
     uint32_t *rowmax;      // [routes] max |activation| bits per expert-sorted row (gate/up writes, down reads)
+    uint8_t *yrec;         // MXFP4 gate/up: the activations' E4M3 split records in place of f32 rows (or null)
 };
 
 // Power of two that brings a row with max |value| `bits` (f32 bits) into
@@ -63,9 +64,10 @@ int grouped_matmul_launch(int mode, uint32_t fmt, const MatmulArgs &a, uint32_t 
 int moe_q4k_launch(int mode, const MatmulArgs &a, uint32_t bm, hipStream_t stream);
 
 // MXFP4 banks on the block-scaled MFMA: activations split per row into E4M3
-// records (mx_rows_bytes each matrix), route plan with tile_rows = 16 or 32.
+// records (mxsplit.h; mx_rows_bytes each matrix) -- the inputs beside the
+// route plan, the activations by the gate/up tiles -- route plan with
+// tile_rows = 16 or 32.
 uint64_t mx_rows_bytes(uint32_t rows, uint32_t k, int terms);
-int mx_rows_split(const void *x, bool bf16, uint8_t *rec, uint32_t rows, uint32_t k, int terms, hipStream_t stream);
 int mx_experts_launch(int mode, const MatmulArgs &a, const uint8_t *xrec, int terms, uint32_t tile_rows,
                       hipStream_t stream);
 

@@ -6,15 +6,9 @@
 // stored and its E8M0 byte the B scale (the operand layout is described in
 // mxmatmul.hip).
 //
-// Activations are split per row into TERMS E4M3 terms with E8M0 scales per
-// 32-block (the split of mxmatmul.hip), stored row-major so that tiles can
-// gather arbitrary rows: record (row, K step of 64) =
-//     data [term][part 2][block 2][16 B]   (lane part p reads 32 bytes)
-//     scales [block 2][4 bytes, byte t = term t] E8M0, padded to 16 bytes
-// Two terms hold bf16 inputs exactly; f32 inputs (and the f32 activations
-// between gate/up and down) take three: relL2 ~1.4e-5 of the product
-// against ~6e-4 with two (numpy model, N(0,1) and SwiGLU-shaped rows).
+// Activations come split per row into TERMS E4M3 terms (mxsplit.h).
 #include "matmul.h"
+#include "mxsplit.h"
 #include "stream.h"
 
 namespace oco {
@@ -22,105 +16,8 @@ namespace oco {
 typedef int mxe_i32x8 __attribute__((ext_vector_type(8)));
 typedef float mxe_f32x16 __attribute__((ext_vector_type(16)));
 
-__host__ __device__ constexpr uint32_t mxr_data(int terms) { return 64u * terms; }
-__host__ __device__ constexpr uint32_t mxr_rec(int terms) { return 64u * terms + 16u; }
-
 uint64_t mx_rows_bytes(uint32_t rows, uint32_t k, int terms) {
     return (uint64_t)rows * ((k + 63) / 64) * mxr_rec(terms);
-}
-
-// Smallest E with amax <= 448 * 2^E, as E (E8M0 byte E + 127); 128 (NaN byte)
-// for a non-finite block.
-__device__ __forceinline__ int mxe_scale_exp(float amax) {
-    if (!(amax <= 3.402823466e38f)) return 128;
-    if (amax == 0.f) return -127;
-    const uint32_t b = __float_as_uint(amax);
-    int e;
-    uint32_t mant;
-    if (b >> 23) {
-        e = (int)(b >> 23) - 127;
-        mant = b & 0x7fffffu;
-    } else {
-        const int lz = __builtin_clz(b) - 8;
-        e = -126 - lz;
-        mant = (b << lz) & 0x7fffffu;
-    }
-    const int E = mant <= 0x600000u ? e - 8 : e - 7;
-    return E < -127 ? -127 : E;
-}
-
-// One thread per (row, K step, block): the block's two E4M3 terms, written
-// in W's nibble order, and its two E8M0 scales.
-template <typename XT, int TERMS>
-__global__ __launch_bounds__(256) void mx_rows_split_kernel(const XT *x, uint8_t *rec, uint32_t rows, uint32_t k) {
-    const uint32_t ksteps = (k + 63) / 64;
-    const uint64_t item = (uint64_t)blockIdx.x * 256 + threadIdx.x;  // (row, step, block)
-    const uint32_t blk = (uint32_t)(item & 1);
-    const uint64_t rs = item >> 1;
-    if (rs >= (uint64_t)rows * ksteps) return;
-    const uint32_t row = (uint32_t)(rs / ksteps), s = (uint32_t)(rs % ksteps);
-    const uint32_t k0 = s * 64 + 32 * blk;
-    float v[32];
-    if (k0 < k) {
-        const XT *src = x + (uint64_t)row * k + k0;
-#pragma unroll
-        for (int i = 0; i < 32; i++) {
-            if constexpr (sizeof(XT) == 4)
-                v[i] = src[i];
-            else
-                v[i] = __uint_as_float((uint32_t)src[i] << 16);
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < 32; i++) v[i] = 0.f;
-    }
-    uint8_t *out = rec + ((uint64_t)row * ksteps + s) * mxr_rec(TERMS);
-    uint32_t scales = 0;
-#pragma unroll
-    for (int t = 0; t < TERMS; t++) {
-        float amax = 0.f;
-        bool nan = false;
-#pragma unroll
-        for (int i = 0; i < 32; i++) {
-            amax = fmaxf(amax, fabsf(v[i]));
-            nan |= v[i] != v[i];
-        }
-        if (nan) amax = __uint_as_float(0x7fc00000u);
-        const int E = mxe_scale_exp(amax);
-        scales |= (uint32_t)(E + 127) << (8 * t);
-        const float inv = E == 128 ? 0.f : __builtin_ldexpf(1.f, -E), sc = E == 128 ? 0.f : __builtin_ldexpf(1.f, E);
-        uint32_t codes[8];
-#pragma unroll
-        for (int i = 0; i < 32; i += 4) {
-            int p = __builtin_amdgcn_cvt_pk_fp8_f32(v[i] * inv, v[i + 1] * inv, 0, false);
-            p = __builtin_amdgcn_cvt_pk_fp8_f32(v[i + 2] * inv, v[i + 3] * inv, p, true);
-            codes[i / 4] = (uint32_t)p;
-        }
-#pragma unroll
-        for (int q = 0; q < 8; q++) {
-            v[4 * q] -= __builtin_amdgcn_cvt_f32_fp8((int)codes[q], 0) * sc;
-            v[4 * q + 1] -= __builtin_amdgcn_cvt_f32_fp8((int)codes[q], 1) * sc;
-            v[4 * q + 2] -= __builtin_amdgcn_cvt_f32_fp8((int)codes[q], 2) * sc;
-            v[4 * q + 3] -= __builtin_amdgcn_cvt_f32_fp8((int)codes[q], 3) * sc;
-        }
-        // part p, byte e of this block: value 8p + e / 2 + 16 (e & 1) (W's nibble order)
-#pragma unroll
-        for (int p = 0; p < 2; p++) {
-            uint32_t o[4];
-#pragma unroll
-            for (int d = 0; d < 4; d++) {
-                uint32_t word = 0;
-#pragma unroll
-                for (int bb = 0; bb < 4; bb++) {
-                    const int e = 4 * d + bb, idx = 8 * p + e / 2 + 16 * (e & 1);
-                    word |= ((codes[idx / 4] >> (8 * (idx & 3))) & 0xffu) << (8 * bb);
-                }
-                o[d] = word;
-            }
-            *reinterpret_cast<uint4 *>(out + ((t * 2 + p) * 2 + blk) * 16) = make_uint4(o[0], o[1], o[2], o[3]);
-        }
-    }
-    *reinterpret_cast<uint32_t *>(out + mxr_data(TERMS) + 4 * blk) = scales;
 }
 
 // Tile: one route-plan tile of up to TR routes (16 or 32: the plan's tile
@@ -306,16 +203,33 @@ __global__ __launch_bounds__(64 * NW) void mx_experts_kernel(MatmulArgs a, const
             for (int v = 0; v < 16; v++) hand[((wave - CT) * 16 + v) * 64 + lane] = acc[0][v];
         }
         __syncthreads();
-        if (upw || col >= a.n) return;
+        if (upw || col0 >= a.n) return;  // uniform per wavefront
         const float bg = a.bias ? round_bf16(a.bias[bi]) : 0.f;
         const float bu = a.bias2 ? round_bf16(a.bias2[bi] + (a.up_one ? 1.0f : 0.0f)) : (a.up_one ? 1.0f : 0.0f);
+        if (!a.yrec) {
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const uint32_t r = 8 * (v / 4) + 4 * part + (v % 4);
+                if (r < rows && col < a.n)
+                    reinterpret_cast<float *>(a.y)[(uint64_t)(sorted0 + r) * a.n + col] =
+                        expert_activation(a.act, acc[0][v] + bg, hand[(wave * 16 + v) * 64 + lane] + bu);
+            }
+            return;
+        }
+        // The 32 columns are one block of each activation row (n % 32 == 0):
+        // each half wavefront splits its rows' blocks into the down
+        // projection's records (and, for a lone last block, zeros the partner).
+        const uint32_t blk = col0 / 32, dsteps = (a.n + 63) / 64;
+        const bool lone = !(blk & 1) && blk + 1 == a.n / 32;
 #pragma unroll
         for (int v = 0; v < 16; v++) {
-            const uint32_t r = 8 * (v / 4) + 4 * part + (v % 4);
-            const float up = hand[(wave * 16 + v) * 64 + lane];
-            if (r < rows)
-                reinterpret_cast<float *>(a.y)[(uint64_t)(sorted0 + r) * a.n + col] =
-                    expert_activation(a.act, acc[0][v] + bg, up + bu);
+            const uint32_t r = 8 * (v / 4) + 4 * part + (v % 4);  // uniform per half wavefront
+            if (r < rows) {
+                uint8_t *rec = a.yrec + ((uint64_t)(sorted0 + r) * dsteps + blk / 2) * mxr_rec(3);
+                mx_split_lanes<3>(expert_activation(a.act, acc[0][v] + bg, hand[(wave * 16 + v) * 64 + lane] + bu), rec,
+                                  blk & 1);
+                if (lone) mx_split_lanes<3>(0.f, rec, 1);
+            }
         }
     } else {
         if (col >= a.n) return;
@@ -332,18 +246,6 @@ __global__ __launch_bounds__(64 * NW) void mx_experts_kernel(MatmulArgs a, const
                 reinterpret_cast<float *>(a.y)[o] = val;
         }
     }
-}
-
-int mx_rows_split(const void *x, bool bf16, uint8_t *rec, uint32_t rows, uint32_t k, int terms, hipStream_t stream) {
-    const uint64_t items = (uint64_t)rows * ((k + 63) / 64) * 2;
-    const dim3 grid((unsigned)((items + 255) / 256));
-    if (bf16 && terms == 2)
-        hipLaunchKernelGGL((mx_rows_split_kernel<uint16_t, 2>), grid, dim3(256), 0, stream, (const uint16_t *)x, rec, rows, k);
-    else if (!bf16 && terms == 3)
-        hipLaunchKernelGGL((mx_rows_split_kernel<float, 3>), grid, dim3(256), 0, stream, (const float *)x, rec, rows, k);
-    else
-        return fail(OCO_ERR_UNSUPPORTED, "experts: MXFP4 split of %s rows into %d terms", bf16 ? "bf16" : "f32", terms);
-    return launch_check("experts MXFP4 row split");
 }
 
 constexpr int MXE_NW = 4;

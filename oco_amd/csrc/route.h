@@ -6,7 +6,9 @@ namespace oco {
 
 // A job run beside the route plan, in the same launch (workgroups 1..):
 // activation rows to f16 (the reference's half(x)) from bf16 or f32, four
-// elements per thread, and `nzero` words of `zero` cleared.
+// elements per thread, and `nzero` words of `zero` cleared; or, with `rec`
+// set, the rows' E4M3 split records (mxsplit.h: bf16 rows in two terms, f32
+// rows in three) in place of the f16 copy.
 struct PlanSide {
     const void *x;
     uint32_t x_bf16;
@@ -14,6 +16,8 @@ struct PlanSide {
     uint64_t n;
     uint32_t *zero;
     uint32_t nzero;
+    uint8_t *rec;       // split records of rows x k (k % 32 == 0), or null
+    uint32_t rows, k;
 };
 
 // oco_route_plan with an optional side job (null: none).

@@ -5,6 +5,7 @@
 // nemotron.metal's route_plan_n (:238-273).
 #include <algorithm>
 
+#include "mxsplit.h"
 #include "route.h"
 
 namespace oco {
@@ -54,9 +55,19 @@ __global__ __launch_bounds__(PLAN_THREADS) void route_plan_kernel(const uint32_t
                                                                   uint32_t experts, uint32_t tile_rows,
                                                                   uint32_t up_tiles, uint32_t down_tiles,
                                                                   uint32_t *plan, PlanSide side) {
-    if (blockIdx.x > 0) {  // the side job: four elements and one cleared word per thread
+    if (blockIdx.x > 0) {  // the side job: four elements (or one split item) and one cleared word per thread
         const uint64_t t = (uint64_t)(blockIdx.x - 1) * PLAN_THREADS + threadIdx.x;
         if (t < side.nzero) side.zero[t] = 0;
+        if (side.rec) {  // one split item per 32 lanes (uniform per half wavefront)
+            const uint64_t item = t / 32;
+            if (item < (uint64_t)side.rows * ((side.k + 63) / 64) * 2) {
+                if (side.x_bf16)
+                    mx_split_item_lanes<uint16_t, 2>(reinterpret_cast<const uint16_t *>(side.x), side.rec, side.k, item);
+                else
+                    mx_split_item_lanes<float, 3>(reinterpret_cast<const float *>(side.x), side.rec, side.k, item);
+            }
+            return;
+        }
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const uint64_t i = 4 * t + j;
@@ -263,8 +274,10 @@ int route_plan_launch(const uint32_t *ids, uint32_t routes, uint32_t experts, ui
                     "oco_route_plan: need 0 < experts <= 4096 and tile_rows >= 16 (the plan holds ceil(routes/16) + "
                     "experts tiles)");
     PlanSide sj = side ? *side : PlanSide{};
+    if (sj.rec && sj.k % 32) return fail(OCO_ERR_INVALID, "oco_route_plan: split rows need k %% 32 == 0 (k=%u)", sj.k);
+    const uint64_t side_items = sj.rec ? (uint64_t)sj.rows * ((sj.k + 63) / 64) * 2 * 32 : (sj.n + 3) / 4;  // threads
     const uint64_t side_blocks =
-        std::max<uint64_t>((sj.n + 4 * PLAN_THREADS - 1) / (4 * PLAN_THREADS), (sj.nzero + PLAN_THREADS - 1) / PLAN_THREADS);
+        std::max<uint64_t>((side_items + PLAN_THREADS - 1) / PLAN_THREADS, (sj.nzero + PLAN_THREADS - 1) / PLAN_THREADS);
     if (side_blocks >= 0x7fffffffu) return fail(OCO_ERR_INVALID, "oco_route_plan: side job of %llu elements", (unsigned long long)sj.n);
     hipLaunchKernelGGL(route_plan_kernel, dim3(1 + (unsigned)side_blocks), dim3(PLAN_THREADS),
                        (size_t)(PLAN_THREADS + 3 * experts + (experts <= PLAN_HIST_EXPERTS ? 16 * experts : 0)) * 4,
