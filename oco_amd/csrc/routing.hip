@@ -50,6 +50,13 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const XT *x, const f
 // LDS reads of the whole chunk.  Ids >= experts are left out.
 constexpr uint32_t PLAN_THREADS = 1024;
 constexpr uint32_t PLAN_HIST_EXPERTS = 256;  // per-wavefront histograms in LDS up to this many experts
+constexpr uint32_t PLAN_ONEPASS_CHUNKS = 8;   // the one-pass plan: up to this many chunks of 1024 routes
+constexpr uint32_t PLAN_ONEPASS_WORDS = 12288;  // and per-(chunk, wavefront, expert) counts up to this many words (48 KB)
+
+__host__ __device__ inline bool plan_one_pass(uint32_t routes, uint32_t experts) {
+    const uint32_t nchunks = (routes + 1023) / 1024;
+    return experts <= PLAN_HIST_EXPERTS && nchunks <= PLAN_ONEPASS_CHUNKS && nchunks * 16 * experts <= PLAN_ONEPASS_WORDS;
+}
 
 __global__ __launch_bounds__(PLAN_THREADS) void route_plan_kernel(const uint32_t *ids, uint32_t routes,
                                                                   uint32_t experts, uint32_t tile_rows,
@@ -88,10 +95,72 @@ __global__ __launch_bounds__(PLAN_THREADS) void route_plan_kernel(const uint32_t
     const uint64_t grouped = 6 + 2 * ((uint64_t)(routes + 15) / 16 + experts);
     const uint64_t sorted = grouped + (uint64_t)experts * (routes + 1);
 
+    // One pass (experts <= PLAN_HIST_EXPERTS, up to PLAN_ONEPASS_CHUNKS chunks
+    // of 1024 routes whose per-wavefront histograms fit the LDS): every
+    // route's rank among its wavefront's peers by ballots, the counts per
+    // (chunk, wavefront, expert) in LDS, one exclusive scan per expert over
+    // those slots (which also gives the counts), then every placement at
+    // once -- a handful of barriers instead of four per chunk.
+    const uint32_t nchunks = (routes + PLAN_THREADS - 1) / PLAN_THREADS;
+    const bool one_pass = plan_one_pass(routes, experts);
+    uint32_t ev[PLAN_ONEPASS_CHUNKS], rk[PLAN_ONEPASS_CHUNKS];
+    if (one_pass) {
+        const uint32_t slots = nchunks * 16;
+        for (uint32_t t = tid; t < slots * experts; t += PLAN_THREADS) hist[t] = 0;
+        const uint32_t id_bits = experts > 1 ? 32u - (uint32_t)__builtin_clz(experts - 1) : 0u;
+#pragma unroll
+        for (uint32_t c = 0; c < PLAN_ONEPASS_CHUNKS; c++) {
+            ev[c] = 0xffffffffu;
+            rk[c] = 0;
+            if (c < nchunks) {
+                const uint32_t i = c * PLAN_THREADS + tid;
+                ev[c] = i < routes ? ids[i] : 0xffffffffu;
+            }
+        }
+        __syncthreads();  // hist cleared
+#pragma unroll
+        for (uint32_t c = 0; c < PLAN_ONEPASS_CHUNKS; c++) {
+            if (c >= nchunks) break;  // uniform
+            const uint32_t e = ev[c];
+            uint64_t peers = __ballot(e < experts);
+            if (e >= experts) peers = ~peers;
+            for (uint32_t bit = 0; bit < id_bits; bit++) {
+                const uint64_t b = __ballot((e >> bit) & 1u);
+                peers &= ((e >> bit) & 1u) ? b : ~b;
+            }
+            rk[c] = (uint32_t)__popcll(peers & ((1ull << lane) - 1ull));
+            if (e < experts && (peers >> lane) == 1ull) hist[(c * 16 + wave) * experts + e] = rk[c] + 1;
+        }
+        __syncthreads();
+        // exclusive scan per expert over the slots (chunk, wavefront) in
+        // route order: G consecutive threads per expert, each over a run of
+        // slots, joined by a shuffle scan within the group
+        uint32_t G = 1;
+        while (G * 2 * experts <= PLAN_THREADS && G < 64) G *= 2;
+        const uint32_t e = tid / G, j = tid % G, per = (slots + G - 1) / G;
+        uint32_t local = 0;
+        if (e < experts)
+            for (uint32_t q = j * per; q < min(slots, j * per + per); q++) local += hist[q * experts + e];
+        uint32_t incl = local;
+        for (uint32_t o = 1; o < G; o <<= 1) {
+            const uint32_t v = (uint32_t)__shfl_up((int)incl, o, (int)G);
+            if (j >= o) incl += v;
+        }
+        if (e < experts) {
+            uint32_t run_e = incl - local;
+            for (uint32_t q = j * per; q < min(slots, j * per + per); q++) {
+                const uint32_t v = hist[q * experts + e];
+                hist[q * experts + e] = run_e;
+                run_e += v;
+            }
+            if (j == G - 1) run[e] = incl;
+        }
+        __syncthreads();
+    }
     // 1. counts per expert (four ids in flight per thread)
-    for (uint32_t e = tid; e < experts; e += PLAN_THREADS) run[e] = 0;
+    for (uint32_t e = tid; e < experts && !one_pass; e += PLAN_THREADS) run[e] = 0;
     __syncthreads();
-    for (uint32_t base = tid; base < routes; base += 4 * PLAN_THREADS) {
+    for (uint32_t base = tid; base < routes && !one_pass; base += 4 * PLAN_THREADS) {
         uint32_t ev[4];
 #pragma unroll
         for (int u = 0; u < 4; u++) {
@@ -154,6 +223,20 @@ __global__ __launch_bounds__(PLAN_THREADS) void route_plan_kernel(const uint32_t
             plan[6 + 2 * (uint64_t)t] = e;
             plan[6 + 2 * (uint64_t)t + 1] = b;
         }
+    }
+    if (one_pass) {
+        __syncthreads();  // offs[] is complete
+#pragma unroll
+        for (uint32_t c = 0; c < PLAN_ONEPASS_CHUNKS; c++) {
+            if (c >= nchunks) break;  // uniform
+            const uint32_t e = ev[c], i = c * PLAN_THREADS + tid;
+            if (e < experts) {
+                const uint32_t pos = hist[(c * 16 + wave) * experts + e] + rk[c];
+                plan[grouped + (uint64_t)e * (routes + 1) + 1 + pos] = i;
+                plan[sorted + experts + i] = offs[e] + pos;
+            }
+        }
+        return;
     }
     __syncthreads();
     for (uint32_t e = tid; e < experts; e += PLAN_THREADS) run[e] = 0;  // reused as the running count of step 3
@@ -280,7 +363,10 @@ int route_plan_launch(const uint32_t *ids, uint32_t routes, uint32_t experts, ui
         std::max<uint64_t>((side_items + PLAN_THREADS - 1) / PLAN_THREADS, (sj.nzero + PLAN_THREADS - 1) / PLAN_THREADS);
     if (side_blocks >= 0x7fffffffu) return fail(OCO_ERR_INVALID, "oco_route_plan: side job of %llu elements", (unsigned long long)sj.n);
     hipLaunchKernelGGL(route_plan_kernel, dim3(1 + (unsigned)side_blocks), dim3(PLAN_THREADS),
-                       (size_t)(PLAN_THREADS + 3 * experts + (experts <= PLAN_HIST_EXPERTS ? 16 * experts : 0)) * 4,
+                       (size_t)(PLAN_THREADS + 3 * experts +
+                                (plan_one_pass(routes, experts) ? std::max(16 * experts, (routes + 1023) / 1024 * 16 * experts)
+                                 : experts <= PLAN_HIST_EXPERTS  ? 16 * experts
+                                                                 : 0)) * 4,
                        stream, ids, routes, experts, tile_rows, up_tiles, down_tiles, plan, sj);
     return launch_check("oco_route_plan");
 }
