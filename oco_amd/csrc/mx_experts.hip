@@ -35,18 +35,20 @@ uint64_t mx_rows_bytes(uint32_t rows, uint32_t k, int terms) {
 // Both are loaded one quad ahead into registers and written to LDS at the
 // top of the next quad, so one vmcnt(0) and two barriers per quad order
 // everything.
-template <int G, int NW, int TERMS, int TR>
+template <int G, int NW, int TERMS, int TR, int KS>
 __global__ __launch_bounds__(64 * NW) void mx_experts_kernel(MatmulArgs a, const uint8_t *xrec) {
     constexpr int NT = 1;                          // weight tiles per wavefront
     constexpr int WROWS = 32 * NT;                 // weight rows per wavefront
     constexpr int WLD = WROWS * 10 / 64;           // 16-byte loads per lane per quad (10 per row)
-    constexpr int CT = G == MM_GATE_UP ? NW / 2 : NW;  // column tiles per workgroup
+    constexpr int WPK = NW / KS;                   // wavefronts per K part (KS parts split the quads)
+    constexpr int CT = G == MM_GATE_UP ? WPK / 2 : WPK;  // column tiles per workgroup
     constexpr uint32_t WSLOT = 176;                // LDS bytes per staged row (11 x 16)
     constexpr uint32_t AREC = mxr_rec(TERMS);
     constexpr uint32_t AROW = 4 * AREC + 16;       // LDS bytes per tile row of A (four records + pad)
     constexpr uint32_t APR = 4 * AREC / 16;        // 16-byte pieces per tile row and quad
-    constexpr int ALD = (TR * APR + 64 * NW - 1) / (64 * NW);  // A loads per lane per quad (TR rows)
+    constexpr int ALD = (KS * TR * APR + 64 * NW - 1) / (64 * NW);  // A loads per lane per quad (TR rows per part)
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, c = lane & 31, part = lane >> 5;
+    const int kh = wave / WPK, wsub = wave % WPK;  // K part, wavefront within it
     const uint32_t used = gridDim.x * min(a.plan[1], gridDim.y);
     const uint32_t lin = xcd_order(blockIdx.x + gridDim.x * blockIdx.y, used);
     if (lin >= used) return;  // uniform: a surplus workgroup
@@ -59,34 +61,39 @@ __global__ __launch_bounds__(64 * NW) void mx_experts_kernel(MatmulArgs a, const
     const uint32_t sorted0 = a.plan[sorted + expert] + first;
     // Wavefronts past the last column still load (clamped rows) and join the
     // barriers; they store nothing.
-    const bool upw = G == MM_GATE_UP && wave >= CT;  // an up wavefront
-    const uint32_t col0 = (bx * CT + wave % CT) * 32;
+    const bool upw = G == MM_GATE_UP && wsub >= CT;  // an up wavefront
+    const uint32_t col0 = (bx * CT + wsub % CT) * 32;
     const uint32_t ksteps = (a.k + 63) / 64, nblk = a.k / 32, quads = (ksteps + 3) / 4;
+    // K part kh takes quads kh * qpart .. (an even count: both parts keep
+    // the parity of their local quad index)
+    const uint32_t qpart = KS == 1 ? quads : (quads + 2 * KS - 1) / (2 * KS) * 2, q0 = kh * qpart;
 
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    uint8_t *alds = lds;                                           // [TR][AROW]
-    uint8_t *wlds = lds + TR * AROW + wave * (WROWS * WSLOT);       // [WROWS][WSLOT]
+    uint8_t *alds = lds;                                           // [KS][TR][AROW]
+    uint8_t *wlds = lds + KS * TR * AROW + wave * (WROWS * WSLOT);  // [WROWS][WSLOT]
 
     // A: piece p (16 bytes) of the quad = tile row p / APR, byte 16 (p % APR)
     // of its four consecutive records.
     const uint32_t xrows = G == MM_GATE_UP ? a.routes / a.topk : a.routes;
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t *>(xrec), 0, (uint32_t)((uint64_t)xrows * ksteps * AREC), 0x00020000);
-    const uint32_t pieces = rows * APR;
+    // Piece p of the quad: K part p / (rows APR), then tile row and byte.
+    const uint32_t pieces = KS * rows * APR;
     uint32_t asrc[ALD], adst[ALD];
 #pragma unroll
     for (int i = 0; i < ALD; i++) {
-        const uint32_t p = threadIdx.x + 64 * NW * i, r = min(p / APR, TR - 1u), q16 = p % APR;
+        const uint32_t p = threadIdx.x + 64 * NW * i, kp = min(p / (rows * APR), KS - 1u), pr = p - kp * rows * APR;
+        const uint32_t r = min(pr / APR, TR - 1u), q16 = pr % APR;
         uint32_t xrow = 0;
         if (p < pieces) xrow = G == MM_GATE_UP ? a.plan[list + 1 + first + r] / a.topk : sorted0 + r;
-        asrc[i] = xrow * ksteps * AREC + 16 * q16;
-        adst[i] = r * AROW + 16 * q16;
+        asrc[i] = xrow * ksteps * AREC + kp * qpart * 4 * AREC + 16 * q16;
+        adst[i] = (kp * TR + r) * AROW + 16 * q16;
     }
     // A fragments: this lane's tile row (rows past the tile read row 0: a
     // row of C depends on its own row of A only, and those rows are never
     // stored).
     const uint32_t arow = (uint32_t)c < rows ? c : 0u;
-    const uint32_t afrag = arow * AROW + 32 * part, ascale = arow * AROW + mxr_data(TERMS) + 4 * part;
+    const uint32_t afrag = (kh * TR + arow) * AROW + 32 * part, ascale = (kh * TR + arow) * AROW + mxr_data(TERMS) + 4 * part;
 
     // B: load i of a lane covers staged row f / 10, chunk f % 10 (f = lane +
     // 64 i); quad q's span of a row at byte R starts at
@@ -125,7 +132,7 @@ __global__ __launch_bounds__(64 * NW) void mx_experts_kernel(MatmulArgs a, const
 
     u32x4 wreg[WLD], areg[ALD];
     auto issue = [&](uint32_t q, int par) __attribute__((always_inline)) {
-        const uint32_t sw = 136 * q - 8 * (q & 1), sa = 4 * q * AREC;
+        const uint32_t qg = q0 + q, sw = 136 * qg - 8 * (qg & 1), sa = 4 * q * AREC;  // q: this part's quad
 #pragma unroll
         for (int i = 0; i < WLD; i++)
             wreg[i] = __builtin_amdgcn_raw_buffer_load_b128(rw[(lane + 64 * i) / 10 / 32], boff[i][par], sw, 0);
@@ -144,11 +151,11 @@ __global__ __launch_bounds__(64 * NW) void mx_experts_kernel(MatmulArgs a, const
         for (int i = 0; i < ALD; i++)
             if (threadIdx.x + 64 * NW * i < pieces) *reinterpret_cast<u32x4 *>(alds + adst[i]) = areg[i];
         __syncthreads();  // this quad's A is in place
-        if (q + 1 < quads) issue(q + 1, par ^ 1);
+        if (q + 1 < qpart) issue(q + 1, par ^ 1);
 #pragma unroll
         for (int s = 0; s < 4; s++) {
-            const uint32_t step = 4 * q + s;
-            if (step >= ksteps) break;  // uniform
+            const uint32_t step = 4 * (q0 + q) + s;
+            if (step >= ksteps) break;  // uniform per wavefront
             // the lone last block's partner is zero with scale 1
             const bool live = 2 * step + part < nblk;
             u32x4 av[TERMS][2];
@@ -186,9 +193,24 @@ __global__ __launch_bounds__(64 * NW) void mx_experts_kernel(MatmulArgs a, const
         }
     };
     issue(0, 0);
-    for (uint32_t q = 0; q < quads; q += 2) {
+    for (uint32_t q = 0; q < qpart; q += 2) {
         quad(q, 0);
-        if (q + 1 < quads) quad(q + 1, 1);
+        if (q + 1 < qpart) quad(q + 1, 1);
+    }
+    if constexpr (KS > 1) {
+        // the other K parts' sums to part 0 (the A region is free now)
+        float *red = reinterpret_cast<float *>(lds);  // [KS - 1][WPK][16][64]
+        __syncthreads();
+        if (kh > 0) {
+#pragma unroll
+            for (int v = 0; v < 16; v++) red[(((kh - 1) * WPK + wsub) * 16 + v) * 64 + lane] = acc[0][v];
+        }
+        __syncthreads();
+        if (kh > 0) return;
+#pragma unroll
+        for (int k2 = 0; k2 < KS - 1; k2++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[0][v] += red[((k2 * WPK + wsub) * 16 + v) * 64 + lane];
     }
 
     // C: lane l holds column l % 32, rows 8 (v / 4) + 4 (l / 32) + v % 4.
@@ -200,7 +222,7 @@ __global__ __launch_bounds__(64 * NW) void mx_experts_kernel(MatmulArgs a, const
         __syncthreads();
         if (upw) {
 #pragma unroll
-            for (int v = 0; v < 16; v++) hand[((wave - CT) * 16 + v) * 64 + lane] = acc[0][v];
+            for (int v = 0; v < 16; v++) hand[((wsub - CT) * 16 + v) * 64 + lane] = acc[0][v];
         }
         __syncthreads();
         if (upw || col0 >= a.n) return;  // uniform per wavefront
@@ -212,7 +234,7 @@ __global__ __launch_bounds__(64 * NW) void mx_experts_kernel(MatmulArgs a, const
                 const uint32_t r = 8 * (v / 4) + 4 * part + (v % 4);
                 if (r < rows && col < a.n)
                     reinterpret_cast<float *>(a.y)[(uint64_t)(sorted0 + r) * a.n + col] =
-                        expert_activation(a.act, acc[0][v] + bg, hand[(wave * 16 + v) * 64 + lane] + bu);
+                        expert_activation(a.act, acc[0][v] + bg, hand[(wsub * 16 + v) * 64 + lane] + bu);
             }
             return;
         }
@@ -226,7 +248,7 @@ __global__ __launch_bounds__(64 * NW) void mx_experts_kernel(MatmulArgs a, const
             const uint32_t r = 8 * (v / 4) + 4 * part + (v % 4);  // uniform per half wavefront
             if (r < rows) {
                 uint8_t *rec = a.yrec + ((uint64_t)(sorted0 + r) * dsteps + blk / 2) * mxr_rec(3);
-                mx_split_lanes<3>(expert_activation(a.act, acc[0][v] + bg, hand[(wave * 16 + v) * 64 + lane] + bu), rec,
+                mx_split_lanes<3>(expert_activation(a.act, acc[0][v] + bg, hand[(wsub * 16 + v) * 64 + lane] + bu), rec,
                                   blk & 1);
                 if (lone) mx_split_lanes<3>(0.f, rec, 1);
             }
@@ -250,22 +272,42 @@ __global__ __launch_bounds__(64 * NW) void mx_experts_kernel(MatmulArgs a, const
 
 constexpr int MXE_NW = 4;
 
-template <int G, int TERMS, int TR>
+template <int G, int TERMS, int TR, int KS>
 static int mx_experts_go(const MatmulArgs &a, const uint8_t *xrec, hipStream_t stream) {
-    const size_t lds = TR * (4 * mxr_rec(TERMS) + 16) + (size_t)MXE_NW * 32 * 176;
+    const size_t lds = KS * TR * (4 * mxr_rec(TERMS) + 16) + (size_t)MXE_NW * 32 * 176;
     static_assert(TR * (4 * mxr_rec(2) + 16) >= MXE_NW / 2 * 16 * 64 * 4, "the up hand-over fits the A region");
-    auto fn = mx_experts_kernel<G, MXE_NW, TERMS, TR>;
+    auto fn = mx_experts_kernel<G, MXE_NW, TERMS, TR, KS>;
     OCO_TRY(hip_check(hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
                       "hipFuncSetAttribute"));
-    const uint32_t cols = 32 * (G == MM_GATE_UP ? MXE_NW / 2 : MXE_NW);
+    const uint32_t cols = 32 * (G == MM_GATE_UP ? MXE_NW / 2 : MXE_NW) / KS;
     const dim3 grid((a.n + cols - 1) / cols, (a.routes + TR - 1) / TR + a.experts);
     hipLaunchKernelGGL(fn, grid, dim3(64 * MXE_NW), lds, stream, a, xrec);
     return OCO_OK;
 }
 
+static uint32_t mx_device_cus() {
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+    }
+    return (uint32_t)cus;
+}
+
 template <int G, int TERMS>
 static int mx_experts_go_tr(const MatmulArgs &a, const uint8_t *xrec, uint32_t tile_rows, hipStream_t stream) {
-    return tile_rows == 16 ? mx_experts_go<G, TERMS, 16>(a, xrec, stream) : mx_experts_go<G, TERMS, 32>(a, xrec, stream);
+    if (tile_rows == 32) return mx_experts_go<G, TERMS, 32, 1>(a, xrec, stream);
+    if constexpr (G == MM_DOWN) {
+        // Few tiles (small decode batches): split each tile's K over two
+        // halves of the workgroup when twice the grid still fits one round
+        // of resident workgroups (three per CU), halving the serial quads.
+        const uint32_t tiles = std::min(a.routes, (a.routes + 15) / 16 + a.experts);
+        const uint32_t wgs = (a.n + 32 * MXE_NW - 1) / (32 * MXE_NW) * tiles;
+        if (2 * wgs <= 3 * mx_device_cus()) return mx_experts_go<G, TERMS, 16, 2>(a, xrec, stream);
+    }
+    return mx_experts_go<G, TERMS, 16, 1>(a, xrec, stream);
 }
 
 int mx_experts_launch(int mode, const MatmulArgs &a, const uint8_t *xrec, int terms, uint32_t tile_rows,
