@@ -203,6 +203,33 @@ def test_experts_apply_matches_oracle(lib, fmt, tokens):
     assert np.all(diff <= 2 ** -6 * np.abs(O.bf16_to_f32(ref["out"])) + 1e-2)
 
 
+@pytest.mark.parametrize("tokens", [6, 20])
+def test_experts_apply_mx_tiles_bf16_lone_blocks(lib, tokens):
+    """MXFP4 banks on the block-scaled MFMA tiles at decode batch sizes (16-
+    and 32-row plan tiles) with bf16 inputs (two-term split beside the route
+    plan) and block counts that leave a lone last block in both projections
+    (hidden = 96, ffn = 160: the gate/up tiles zero the activations' partner
+    block)."""
+    E, hidden, ffn, k = 16, 96, 160, 4
+    say("experts_apply mx tiles bf16", tokens)
+    host, devs = bank(lib, 39, E, hidden, ffn, seed=90 + tokens)
+    g, u, d, gb, ub, db = host
+    rng = np.random.default_rng(100 + tokens)
+    xb = O.f32_to_bf16(rng.normal(size=(tokens, hidden)).astype(np.float32))
+    ids, probs = O.select_experts(rng.normal(size=(tokens, E)).astype(np.float32), k)
+    resid = O.f32_to_bf16(rng.normal(size=(tokens, hidden)).astype(np.float32))
+    bk = lib.ExpertBank(39, hidden, ffn, E, k, *devs, activation=0, up_bias_one=True)
+    outb = dev(lib, resid)
+    routed = Guarded(lib, tokens * k * hidden * 4)
+    bk.apply(dev(lib, xb), lib.DType.BF16, dev(lib, ids), dev(lib, probs), tokens, outb, routed=routed.ptr)
+    lib.synchronize()
+    ref = O.experts_reference(39, hidden, ffn, g, u, d, O.bf16_to_f32(xb), ids, probs, resid, gb, ub, db,
+                              activation=0, up_one=True)
+    assert rel_l2(routed.read(np.float32).reshape(tokens * k, hidden), ref["down"]) < 1e-4
+    got = O.bf16_to_f32(outb.download(np.uint16).reshape(tokens, hidden)).astype(np.float64)
+    assert np.all(np.abs(got - O.bf16_to_f32(ref["out"])) <= 2 ** -6 * np.abs(O.bf16_to_f32(ref["out"])) + 1e-2)
+
+
 def test_experts_overfull_tiles(lib):
     """Batch 257 with ids [31, t%15, 15+t%8, 30]: experts 30/31 own 257 routes each,
     spanning many tiles (mxfp4.rs:309-482).  At 257 tokens the layer runs as
