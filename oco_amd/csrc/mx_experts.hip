@@ -47,6 +47,8 @@ __global__ __launch_bounds__(64 * NW) void mx_experts_kernel(MatmulArgs a, const
     constexpr uint32_t AROW = 4 * AREC + 16;       // LDS bytes per tile row of A (four records + pad)
     constexpr uint32_t APR = 4 * AREC / 16;        // 16-byte pieces per tile row and quad
     constexpr int ALD = (KS * TR * APR + 64 * NW - 1) / (64 * NW);  // A loads per lane per quad (TR rows per part)
+    static_assert(NW % KS == 0 && (G == MM_DOWN || (NW / KS) % 2 == 0), "wavefronts split evenly into parts and tiles");
+    static_assert((KS - 1) * (NW / KS) * 16 * 64 * 4 <= KS * TR * AROW, "the K-part sums fit the record region");
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, c = lane & 31, part = lane >> 5;
     const int kh = wave / WPK, wsub = wave % WPK;  // K part, wavefront within it
     const uint32_t used = gridDim.x * min(a.plan[1], gridDim.y);
