@@ -84,6 +84,28 @@ typedef void *oco_event;  /* hipEvent_t */
 /* Thread-local message of the last failed call on this thread ("" if none). */
 const char *oco_last_error(void);
 
+/* Kernel-choice overrides.  No counterpart in the reference, whose kernel
+ * choice tables are fixed at pipeline build time (src/weights/pipelines.rs:
+ * 227-355, compute/matrix.rs:130-379); here the same tables run unless a
+ * knob is set, so that parity tests can reach every kernel variant and
+ * tuning runs can compare them.  count == 0 clears the knob.  Not
+ * synchronised with launches on other threads: set knobs before launching. */
+typedef enum oco_knob {
+    OCO_KNOB_STREAM_PLAN = 0,     /* streaming matvec: rows per half-wave (1|2), K split (1|2|4), WGs per CU */
+    OCO_KNOB_MATVEC_PLAN = 1,     /* plain matvec (F32/F16/BF16): rows per wave, K split */
+    OCO_KNOB_MATVEC_PLAIN = 2,    /* value 1: quantized formats take the plain matvec, not the streaming one */
+    OCO_KNOB_MX_TILE = 3,         /* MXFP4 prefill tile: wavefronts along rows, 32-column tiles per wave */
+    OCO_KNOB_MX_PREFILL_OFF = 4,  /* value 1: MXFP4 prefill takes the f16 MFMA tiles instead of the FP4 ones */
+    OCO_KNOB_MATMUL_TILE = 5,     /* f16 MFMA prefill tile choice index */
+    OCO_KNOB_MOE_MX_TOKENS = 6,   /* MXFP4 banks take the block-scaled MFMA tiles from this many tokens */
+    OCO_KNOB_MOE_MFMA_TOKENS = 7, /* other banks take the grouped MFMA tiles from this many tokens */
+    OCO_KNOB_MOE_Q4_ROWS = 8,     /* Q4_K grouped tiles: rows per tile (32|48|64), value 0: the f16 LDS tiles */
+    OCO_KNOB_MOE_WG = 9,          /* routed decode kernel: workgroups per CU */
+    OCO_KNOB_MX_EXPERTS_KS = 10,  /* MXFP4 expert down tiles of 16 rows: K split (1|2) */
+    OCO_KNOB_COUNT = 11
+} oco_knob;
+int oco_plan_override(uint32_t knob, const int32_t *values, uint32_t count);
+
 /* (elements, bytes) per GGUF block: src/tensor.rs:24-38 (block_layout). */
 int oco_block_layout(uint32_t format, uint32_t *elements, uint32_t *bytes);
 
@@ -256,6 +278,20 @@ uint64_t oco_experts_workspace(const oco_experts *w, uint32_t tokens);
 int oco_experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype,
                       const uint32_t *ids, const float *probs, uint32_t tokens, uint16_t *out,
                       float *routed, void *workspace, uint64_t workspace_bytes, oco_stream stream);
+
+/* The whole routed layer from the router on, as Bindings::experts runs it
+ * (src/weights/compute/feed_forward.rs:107-275): router logits =
+ * bf16(x) . bf16(router_w) + bf16(router_bias) over `experts` f32 rows
+ * [experts, hidden] (router_logits / router, routing.metal:96-146), top-k
+ * selection with softmax over the chosen (select_expert_values, :71-94) --
+ * at one token inside the gate/up kernel as expert_expand does
+ * (projections.metal:78-137), else by its own launch -- then everything
+ * oco_experts_apply does.  ids/probs [tokens, k] receive the selection
+ * (routing.ids / routing.prob of the reference); workspace:
+ * oco_experts_workspace bytes (the logits live at its end). */
+int oco_experts_forward(const oco_experts *w, const float *router_w, const float *router_bias, const void *x,
+                        oco_dtype x_dtype, uint32_t tokens, uint16_t *out, uint32_t *ids, float *probs,
+                        float *routed, void *workspace, uint64_t workspace_bytes, oco_stream stream);
 
 /* Single-token fused expansion: select the top-k experts from `logits`
  * [experts], then gate and up projections of the selected experts with the

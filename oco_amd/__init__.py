@@ -39,6 +39,21 @@ class WeightFormat(enum.IntEnum):
     Mxfp4 = 39
 
 
+class Knob(enum.IntEnum):
+    """oco_knob: kernel-choice overrides (tests and tuning runs)."""
+    STREAM_PLAN = 0
+    MATVEC_PLAN = 1
+    MATVEC_PLAIN = 2
+    MX_TILE = 3
+    MX_PREFILL_OFF = 4
+    MATMUL_TILE = 5
+    MOE_MX_TOKENS = 6
+    MOE_MFMA_TOKENS = 7
+    MOE_Q4_ROWS = 8
+    MOE_WG = 9
+    MX_EXPERTS_KS = 10
+
+
 class DType(enum.IntEnum):
     F32 = 0
     BF16 = 1
@@ -115,6 +130,7 @@ _MP = ctypes.POINTER(Matrix)
 _EP = ctypes.POINTER(ExpertsDesc)
 SIGNATURES = {
     "oco_last_error": (ctypes.c_char_p, []),
+    "oco_plan_override": (_i32, [_u32, ctypes.POINTER(ctypes.c_int32), _u32]),
     "oco_block_layout": (_i32, [_u32, ctypes.POINTER(_u32), ctypes.POINTER(_u32)]),
     "oco_row_bytes": (_u64, [_u32, _u32]),
     "oco_device_open": (_i32, [_i32, ctypes.POINTER(_i32)]),
@@ -146,6 +162,7 @@ SIGNATURES = {
     "oco_route_plan": (_i32, [_vp, _u32, _u32, _u32, _u32, _u32, _vp, _vp]),
     "oco_experts_workspace": (_u64, [_EP, _u32]),
     "oco_experts_apply": (_i32, [_EP, _vp, _i32, _vp, _vp, _u32, _vp, _vp, _vp, _u64, _vp]),
+    "oco_experts_forward": (_i32, [_EP, _vp, _vp, _vp, _i32, _u32, _vp, _vp, _vp, _vp, _vp, _u64, _vp]),
     "oco_expert_expand": (_i32, [_EP, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
     "oco_moe_sum": (_i32, [_vp, _i32, _vp, _vp, _u32, _u32, _u32, _vp]),
     "oco_norm": (_i32, [_vp, _vp, _vp, _u32, _u32, ctypes.c_float, _i32, _vp]),
@@ -213,6 +230,26 @@ def open_device(ordinal: int = 0) -> int:
 def _ensure_device():
     if not _device_open:
         open_device(0)
+
+
+def plan_override(knob: int, values=()):
+    """Override one kernel-choice table entry (empty `values` clears it)."""
+    vals = (ctypes.c_int32 * max(len(values), 1))(*[int(v) for v in values])
+    _check(load_library().oco_plan_override(int(knob), vals, len(values)))
+
+
+class overridden:
+    """Context manager: `with overridden(Knob.X, (a, b)):` ... then cleared."""
+
+    def __init__(self, knob: int, values):
+        self.knob, self.values = knob, tuple(values)
+
+    def __enter__(self):
+        plan_override(self.knob, self.values)
+        return self
+
+    def __exit__(self, *a):
+        plan_override(self.knob, ())
 
 
 class Stream:
@@ -608,6 +645,21 @@ class ExpertBank:
                                                 _addr(ids), _addr(probs), tokens, _addr(out),
                                                 _addr(routed), _addr(workspace), ws_bytes,
                                                 _stream(stream)))
+
+    def forward(self, router_w, router_bias, x, x_dtype, tokens: int, out, ids, probs, routed=None,
+                workspace=None, stream=None):
+        """Bindings::experts (feed_forward.rs:107-275) from the router logits on:
+        ids/probs [tokens, k] receive the device's expert selection."""
+        need = self.workspace_bytes(tokens)
+        if workspace is None:
+            if self._workspace is None or self._workspace.nbytes < need:
+                self._workspace = DeviceBuffer(max(need, 256))
+            workspace = self._workspace
+        ws_bytes = workspace.nbytes if isinstance(workspace, DeviceBuffer) else need
+        _check(load_library().oco_experts_forward(ctypes.byref(self.desc), _addr(router_w), _addr(router_bias),
+                                                  _addr(x), int(x_dtype), tokens, _addr(out), _addr(ids),
+                                                  _addr(probs), _addr(routed), _addr(workspace), ws_bytes,
+                                                  _stream(stream)))
 
     def expand(self, x, x_dtype, logits, ids, probs, up_out, act_out, stream=None):
         """expert_expand (projections.metal:78-137) for one token."""

@@ -11,6 +11,10 @@ namespace oco {
 int fail(int code, const char *fmt, ...);   // records the message, returns code
 int hip_check(hipError_t e, const char *what);
 int launch_check(const char *what);        // hipGetLastError after a launch
+// Kernel-choice override set through oco_plan_override (tests and tuning
+// runs); copies up to 4 values into vals and returns their count, 0 when the
+// knob is not overridden (the built-in choice table applies).
+int plan_override(uint32_t knob, int32_t *vals);
 }  // namespace oco
 
 #define OCO_TRY(expr)              \

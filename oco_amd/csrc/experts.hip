@@ -325,7 +325,8 @@ static int moe_launch(uint32_t fmt, bool gated, MoeArgs a, uint32_t tiles, uint3
     if (lds > 64 * 1024)
         OCO_TRY(hip_check(hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
                           "hipFuncSetAttribute"));
-    static const uint32_t per_cu = getenv("OCO_MOE_WG") ? (uint32_t)atoi(getenv("OCO_MOE_WG")) : 2;  // tuning runs only
+    int32_t ov[4];
+    const uint32_t per_cu = plan_override(OCO_KNOB_MOE_WG, ov) && ov[0] > 0 ? (uint32_t)ov[0] : 2u;
     const uint32_t target = per_cu * device_cus();
     uint32_t gx = std::max<uint32_t>(1, target / std::max<uint32_t>(1, parallel_tiles));
     gx = std::min(gx, a.ngroups);
@@ -397,21 +398,30 @@ uint64_t oco_experts_workspace(const oco_experts *w, uint32_t tokens) {
     if (w->format == OCO_Q4_K) bytes += align256(routes * w->ffn * 2);
     if (w->format == OCO_MXFP4)
         bytes += align256(mx_rows_bytes(tokens, w->hidden, 3)) + align256(mx_rows_bytes((uint32_t)routes, w->ffn, 3));
-    return bytes;
+    // router logits of oco_experts_forward, last
+    return bytes + align256((uint64_t)tokens * w->experts * 4);
 }
 
-int oco_experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype, const uint32_t *ids,
-                      const float *probs, uint32_t tokens, uint16_t *out, float *routed, void *workspace,
-                      uint64_t workspace_bytes, oco_stream stream) {
+}  // extern "C"
+
+// The layer after the router logits.  With `logits`, the experts are
+// selected on the device (ids/probs are written): at one token inside the
+// routed gate/up kernel (expert_expand's selection), else by route_select.
+static int experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype, uint32_t *ids, float *probs,
+                         const float *logits, uint32_t tokens, uint16_t *out, float *routed, void *workspace,
+                         uint64_t workspace_bytes, hipStream_t s, const char *who) {
     OCO_TRY(check_bank(w, true));
     if (!tokens) return OCO_OK;
-    if (!x || !ids || !probs || !out || !workspace) return fail(OCO_ERR_INVALID, "oco_experts_apply: null pointer");
+    if (!x || !ids || !probs || !out || !workspace) return fail(OCO_ERR_INVALID, "%s: null pointer", who);
     if (x_dtype != OCO_DT_F32 && x_dtype != OCO_DT_BF16)
-        return fail(OCO_ERR_UNSUPPORTED, "oco_experts_apply: activations must be f32 or bf16");
+        return fail(OCO_ERR_UNSUPPORTED, "%s: activations must be f32 or bf16", who);
     if (workspace_bytes < oco_experts_workspace(w, tokens))
-        return fail(OCO_ERR_INVALID, "oco_experts_apply: workspace of %llu bytes, need %llu",
+        return fail(OCO_ERR_INVALID, "%s: workspace of %llu bytes, need %llu", who,
                     (unsigned long long)workspace_bytes, (unsigned long long)oco_experts_workspace(w, tokens));
-    hipStream_t s = (hipStream_t)stream;
+    oco_stream stream = (oco_stream)s;
+    // Selection inside the gate/up kernel covers one token over <= 64 experts.
+    const bool fused_select = logits && tokens == 1 && w->experts <= 64;
+    if (logits && !fused_select) OCO_TRY(oco_route_select(logits, tokens, w->experts, w->k, ids, probs, stream));
     const uint32_t routes = tokens * w->k;
     uint8_t *ws = (uint8_t *)workspace;
     uint32_t *plan = (uint32_t *)ws;
@@ -424,8 +434,8 @@ int oco_experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype, co
     uint8_t *arec = xrec + align256(mx_rows_bytes(tokens, w->hidden, 3));
     uint16_t *act16 = (uint16_t *)xrec;  // Q4_K only (in place of the MXFP4 splits)
 
-    static const uint32_t mx_tokens =
-        getenv("OCO_MOE_MX_TOKENS") ? (uint32_t)atoi(getenv("OCO_MOE_MX_TOKENS")) : MOE_MX_TOKENS;  // tuning runs only
+    int32_t ov[4];
+    const uint32_t mx_tokens = plan_override(OCO_KNOB_MOE_MX_TOKENS, ov) ? (uint32_t)ov[0] : MOE_MX_TOKENS;
     // The MFMA tiles and the E4M3 row split read whole 32-element k groups
     // and n tiles; other geometries take the routed matvec path below.
     const bool tiled = w->hidden % 32 == 0 && w->ffn % 32 == 0;
@@ -478,16 +488,17 @@ int oco_experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype, co
         return oco_moe_sum(down, routed ? OCO_DT_F32 : OCO_DT_BF16, probs, out, w->hidden, tokens, w->k, stream);
     }
 
-    static const uint32_t mfma_tokens = getenv("OCO_MOE_MFMA_TOKENS") ? (uint32_t)atoi(getenv("OCO_MOE_MFMA_TOKENS")) : MOE_MFMA_TOKENS;  // tuning runs only
+    const uint32_t mfma_tokens = plan_override(OCO_KNOB_MOE_MFMA_TOKENS, ov) ? (uint32_t)ov[0] : MOE_MFMA_TOKENS;
     if (tiled && tokens >= mfma_tokens) {
         // Prefill: grouped MFMA GEMMs (expert_up_tensor / moe_activate /
         // expert_down_tensor, projections.metal:192-376, routing.metal:44-64).
-        const bool q4 = w->format == OCO_Q4_K && !getenv("OCO_MOE_LDS");  // OCO_MOE_LDS: tuning comparisons
         // Rows per tile: most experts in one tile (mean routes per expert,
-        // plus room for the spread).
+        // plus room for the spread).  An OCO_KNOB_MOE_Q4_ROWS override of 0
+        // sends Q4_K to the f16 LDS tiles of the other formats.
+        const int q4_rows = plan_override(OCO_KNOB_MOE_Q4_ROWS, ov) ? ov[0] : -1;
+        const bool q4 = w->format == OCO_Q4_K && q4_rows != 0;
         const uint32_t mean = routes / w->experts;
-        const uint32_t bm = q4 ? (getenv("OCO_Q4_BM") ? (uint32_t)atoi(getenv("OCO_Q4_BM"))  // env: tuning runs only
-                                                      : mean <= 20 ? 32 : mean <= 36 ? 48 : 64)
+        const uint32_t bm = q4 ? (q4_rows > 0 ? (uint32_t)q4_rows : mean <= 20 ? 32 : mean <= 36 ? 48 : 64)
                                : (mean <= 40 ? 32 : 64);
         // The tiles take f16 rows (the reference's half(x)); the conversion
         // and the clearing of the row maxima run beside the plan.
@@ -543,6 +554,47 @@ int oco_experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype, co
 
     uint32_t tiles = routes, parallel = routes;
     const uint32_t *use_plan = nullptr;
+    if (fused_select) {
+        // expert_expand (projections.metal:78-137): every gate/up workgroup
+        // selects the token's experts from the logits; workgroup (0, 0)
+        // records ids and probabilities for the down pass and the combine.
+        MoeArgs a = {};
+        a.w[0] = (const uint8_t *)w->gate;
+        a.w[1] = (const uint8_t *)w->up;
+        a.bias[0] = w->gate_bias;
+        a.bias[1] = w->up_bias;
+        a.x = x;
+        a.x_bf16 = x_dtype == OCO_DT_BF16;
+        a.input_div = w->k;
+        a.out0 = act;
+        a.logits = logits;
+        a.ids_out = ids;
+        a.probs_out = probs;
+        a.k = w->hidden;
+        a.n = w->ffn;
+        a.experts = w->experts;
+        a.topk = w->k;
+        a.routes = routes;
+        a.act = w->activation;
+        a.up_one = w->up_bias_one;
+        OCO_TRY(moe_launch(w->format, true, a, routes, routes, s));
+        MoeArgs d = {};
+        d.w[0] = (const uint8_t *)w->down;
+        d.bias[0] = w->down_bias;
+        d.x = act;
+        d.input_div = 1;
+        d.out0 = down;
+        d.ids = ids;
+        d.k = w->ffn;
+        d.n = w->hidden;
+        d.experts = w->experts;
+        d.topk = w->k;
+        d.routes = routes;
+        d.act = w->activation;
+        d.up_one = w->up_bias_one;
+        OCO_TRY(moe_launch(w->format, false, d, routes, routes, s));
+        return oco_moe_sum(down, OCO_DT_F32, probs, out, w->hidden, tokens, w->k, stream);
+    }
     if (tokens > 1) {
         OCO_TRY(oco_route_plan(ids, routes, w->experts, PLAN_TILE, 0, 0, plan, stream));
         use_plan = plan;
@@ -583,6 +635,32 @@ int oco_experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype, co
     d.n = w->hidden;
     OCO_TRY(moe_launch(w->format, false, d, tiles, parallel, s));
     return oco_moe_sum(down, OCO_DT_F32, probs, out, w->hidden, tokens, w->k, stream);
+}
+
+extern "C" {
+
+int oco_experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype, const uint32_t *ids,
+                      const float *probs, uint32_t tokens, uint16_t *out, float *routed, void *workspace,
+                      uint64_t workspace_bytes, oco_stream stream) {
+    return experts_apply(w, x, x_dtype, const_cast<uint32_t *>(ids), const_cast<float *>(probs), nullptr, tokens,
+                         out, routed, workspace, workspace_bytes, (hipStream_t)stream, "oco_experts_apply");
+}
+
+int oco_experts_forward(const oco_experts *w, const float *router_w, const float *router_bias, const void *x,
+                        oco_dtype x_dtype, uint32_t tokens, uint16_t *out, uint32_t *ids, float *probs,
+                        float *routed, void *workspace, uint64_t workspace_bytes, oco_stream stream) {
+    OCO_TRY(check_bank(w, true));
+    if (!tokens) return OCO_OK;
+    if (!router_w || !x || !workspace) return fail(OCO_ERR_INVALID, "oco_experts_forward: null pointer");
+    if (workspace_bytes < oco_experts_workspace(w, tokens))
+        return fail(OCO_ERR_INVALID, "oco_experts_forward: workspace of %llu bytes, need %llu",
+                    (unsigned long long)workspace_bytes, (unsigned long long)oco_experts_workspace(w, tokens));
+    hipStream_t s = (hipStream_t)stream;
+    float *logits = (float *)((uint8_t *)workspace + oco_experts_workspace(w, tokens) -
+                              align256((uint64_t)tokens * w->experts * 4));
+    OCO_TRY(router_logits_launch(x, x_dtype, router_w, router_bias, tokens, w->hidden, w->experts, logits, s));
+    return experts_apply(w, x, x_dtype, ids, probs, logits, tokens, out, routed, workspace, workspace_bytes, s,
+                         "oco_experts_forward");
 }
 
 int oco_expert_expand(const oco_experts *w, const void *x, oco_dtype x_dtype, const float *logits, uint32_t *ids,

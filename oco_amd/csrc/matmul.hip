@@ -498,8 +498,8 @@ static MatmulFn matmul_pick_tile(uint32_t fmt) {
 // Tile choice (the prefill half of Builder::dense, pipelines.rs:267-355):
 // the largest tile that still gives every CU work.
 static MatmulFn matmul_pick(uint32_t fmt, uint32_t m, uint32_t n, int &bm, int &bn) {
-    int choice = -1;
-    if (const char *env = getenv("OCO_MATMUL_TILE")) choice = atoi(env);  // tuning runs only
+    int32_t ov[4];
+    int choice = plan_override(OCO_KNOB_MATMUL_TILE, ov) ? ov[0] : -1;
     auto tiles = [&](int tm, int tn) { return (uint64_t)((m + tm - 1) / tm) * ((n + tn - 1) / tn); };
     if (choice < 0) choice = tiles(128, 128) >= 160 ? 3 : 1;  // measured: 128x128 once it fills the chip
     switch (choice) {
@@ -545,11 +545,12 @@ uint64_t mx_workspace_bytes(uint32_t m, uint32_t n, uint32_t k);
 int mx_matmul_launch(const void *w, const void *x, void *y, bool y_bf16, const float *bias, uint32_t m, uint32_t n,
                      uint32_t k, void *workspace, hipStream_t stream);
 
-// MXFP4 goes to the block-scaled FP8 x FP4 MFMA unless OCO_MX_OFF is set
-// (tuning comparisons against the bf16 decode path).
+// MXFP4 goes to the block-scaled FP8 x FP4 MFMA unless the
+// OCO_KNOB_MX_PREFILL_OFF override says otherwise (comparisons against the
+// f16 decode path).
 static bool use_mx(uint32_t format) {
-    static const bool off = getenv("OCO_MX_OFF") != nullptr;
-    return format == OCO_MXFP4 && !off;
+    int32_t ov[4];
+    return format == OCO_MXFP4 && !(plan_override(OCO_KNOB_MX_PREFILL_OFF, ov) && ov[0]);
 }
 
 static int matmul_check(uint32_t format, const void *w, const void *x, oco_dtype x_dtype, const void *y,

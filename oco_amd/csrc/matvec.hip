@@ -407,10 +407,8 @@ struct StreamPlan {
 // wavefronts per K range, workgroups per CU (the analogue of
 // Builder::vector_kernel's table, pipelines.rs:227-265).
 static StreamPlan stream_plan(uint32_t fmt, uint32_t k, uint32_t n, uint32_t m) {
-    if (const char *env = getenv("OCO_STREAM_PLAN")) {  // "r,ks,wg_per_cu" (tuning runs only)
-        int r = 0, ks = 0, w = 0;
-        if (sscanf(env, "%d,%d,%d", &r, &ks, &w) == 3 && r > 0) return {r, ks, w};
-    }
+    int32_t ov[4];
+    if (plan_override(OCO_KNOB_STREAM_PLAN, ov) == 3 && ov[0] > 0) return {ov[0], ov[1], ov[2]};
     uint64_t row_bytes = oco_row_bytes(fmt, k);
     int ks = row_bytes > 6144 ? 4 : row_bytes > 3072 ? 2 : 1;
     (void)m;
@@ -459,11 +457,8 @@ struct MatvecPlan {
 };
 
 MatvecPlan matvec_plan(uint32_t fmt, uint32_t k, uint32_t n, uint32_t m) {
-    // OCO_MATVEC_PLAN="r,ks" overrides the table (tuning runs only).
-    if (const char *env = getenv("OCO_MATVEC_PLAN")) {
-        int r = 0, ks = 0;
-        if (sscanf(env, "%d,%d", &r, &ks) == 2 && r > 0) return {r, ks};
-    }
+    int32_t ov[4];
+    if (plan_override(OCO_KNOB_MATVEC_PLAN, ov) == 2 && ov[0] > 0) return {ov[0], ov[1]};
     uint32_t e, bb;
     oco_block_layout(fmt, &e, &bb);
     uint64_t rows = (uint64_t)n * m;
@@ -514,7 +509,8 @@ static int matvec_impl(uint32_t format, const void *w, const void *x, oco_dtype 
     if (y_dtype != OCO_DT_F32 && y_dtype != OCO_DT_BF16)
         return fail(OCO_ERR_UNSUPPORTED, "oco_matvec: output must be f32 or bf16");
     const int routed_f32 = p->experts > 1 && !p->route_major;
-    if (streamable(format) && !getenv("OCO_MATVEC_V1")) {
+    int32_t plain[4];
+    if (streamable(format) && !(plan_override(OCO_KNOB_MATVEC_PLAIN, plain) && plain[0])) {
         static int cus = 0;
         if (!cus) {
             int dev = 0;

@@ -287,16 +287,7 @@ static int mx_experts_go(const MatmulArgs &a, const uint8_t *xrec, hipStream_t s
     return OCO_OK;
 }
 
-static uint32_t mx_device_cus() {
-    static int cus = 0;
-    if (!cus) {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-            cus = 256;
-    }
-    return (uint32_t)cus;
-}
+constexpr uint32_t MXE_CUS = 256;
 
 template <int G, int TERMS>
 static int mx_experts_go_tr(const MatmulArgs &a, const uint8_t *xrec, uint32_t tile_rows, hipStream_t stream) {
@@ -305,9 +296,16 @@ static int mx_experts_go_tr(const MatmulArgs &a, const uint8_t *xrec, uint32_t t
         // Few tiles (small decode batches): split each tile's K over two
         // halves of the workgroup when twice the grid still fits one round
         // of resident workgroups (three per CU), halving the serial quads.
+        // The threshold is a constant (MI355X: 256 CUs), not the device's
+        // count, so the kernel and its summation order are a function of the
+        // shape alone.
         const uint32_t tiles = std::min(a.routes, (a.routes + 15) / 16 + a.experts);
         const uint32_t wgs = (a.n + 32 * MXE_NW - 1) / (32 * MXE_NW) * tiles;
-        if (2 * wgs <= 3 * mx_device_cus()) return mx_experts_go<G, TERMS, 16, 2>(a, xrec, stream);
+        int32_t ov[4];
+        // Under four quads the second part would hold little or no real work.
+        const uint32_t quads = ((a.k + 63) / 64 + 3) / 4;
+        const int ks = plan_override(OCO_KNOB_MX_EXPERTS_KS, ov) ? ov[0] : 2 * wgs <= 3 * MXE_CUS && quads >= 4 ? 2 : 1;
+        if (ks == 2) return mx_experts_go<G, TERMS, 16, 2>(a, xrec, stream);
     }
     return mx_experts_go<G, TERMS, 16, 1>(a, xrec, stream);
 }

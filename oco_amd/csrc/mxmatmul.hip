@@ -382,9 +382,10 @@ struct MxTilePlan {
 };
 static MxTilePlan mx_plan(uint32_t m, uint32_t n) {
     int wm = 4, ctw = 3;  // 128 x 96: measured fastest at 512 x 5760 x 2880
-    if (const char *env = getenv("OCO_MX_TILE")) {  // "wm,ctw" (tuning runs only)
-        int w2 = 0, c2 = 0;
-        if (sscanf(env, "%d,%d", &w2, &c2) == 2 && (w2 == 2 || w2 == 4) && (c2 == 3 || c2 == 6)) {
+    int32_t ov[4];
+    if (plan_override(OCO_KNOB_MX_TILE, ov) == 2) {
+        const int w2 = ov[0], c2 = ov[1];
+        if ((w2 == 2 || w2 == 4) && (c2 == 3 || c2 == 6)) {
             wm = w2;
             ctw = c2;
         }

@@ -21,6 +21,9 @@ struct PlanSide {
 };
 
 // oco_route_plan with an optional side job (null: none).
+// Router logits [tokens, experts] (routing.metal:96-146) into `logits`.
+int router_logits_launch(const void *x, oco_dtype x_dtype, const float *w, const float *bias, uint32_t tokens,
+                         uint32_t hidden, uint32_t experts, float *logits, hipStream_t stream);
 int route_plan_launch(const uint32_t *ids, uint32_t routes, uint32_t experts, uint32_t tile_rows, uint32_t up_tiles,
                       uint32_t down_tiles, uint32_t *plan, const PlanSide *side, hipStream_t stream);
 

@@ -39,6 +39,70 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const XT *x, const f
     if (lane == 0) logits[(uint64_t)t * experts + e] = acc + (bias ? round_bf16(bias[e]) : 0.f);
 }
 
+// The same logits with the reduction spread over a workgroup: workgroup
+// (e, g) takes expert e and tokens 4g .. 4g + 3, each thread four columns per
+// 1024-column chunk (16-byte weight loads, all of a thread's loads issued
+// before its first FMA), partial sums over DPP and then LDS.  Needs hidden %
+// 4 == 0 and 16-byte (f32) or 8-byte (bf16) aligned rows.
+constexpr int ROUTER_TOKENS = 4;
+template <typename XT>
+__global__ __launch_bounds__(256) void router_logits_wide_kernel(const XT *x, const float *w, const float *bias,
+                                                                 uint32_t tokens, uint32_t hidden,
+                                                                 uint32_t experts, float *logits) {
+    constexpr int TT = ROUTER_TOKENS, U = 4;  // tokens per workgroup, chunks in flight per thread
+    __shared__ float part[4][TT];
+    const uint32_t e = blockIdx.x, t0 = blockIdx.y * TT, wave = threadIdx.x >> 6;
+    const uint32_t nt = min((uint32_t)TT, tokens - t0), quads = hidden / 4;
+    const float4 *wr = reinterpret_cast<const float4 *>(w + (uint64_t)e * hidden);
+    float acc[TT];
+#pragma unroll
+    for (int t = 0; t < TT; t++) acc[t] = 0.f;
+    for (uint32_t f0 = threadIdx.x; f0 < quads; f0 += 256 * U) {
+        float4 wv[U];
+        float xv[TT][U][4];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const uint32_t f = f0 + 256 * u;
+            wv[u] = f < quads ? wr[f] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int t = 0; t < TT; t++) {
+                const uint32_t tt = t0 + min((uint32_t)t, nt - 1);
+                if (f < quads) {
+                    if constexpr (sizeof(XT) == 4) {
+                        const float4 v = reinterpret_cast<const float4 *>(x + (uint64_t)tt * hidden)[f];
+                        xv[t][u][0] = v.x; xv[t][u][1] = v.y; xv[t][u][2] = v.z; xv[t][u][3] = v.w;
+                    } else {
+                        const uint2 v = reinterpret_cast<const uint2 *>(x + (uint64_t)tt * hidden)[f];
+                        xv[t][u][0] = __uint_as_float(v.x << 16); xv[t][u][1] = __uint_as_float(v.x & 0xffff0000u);
+                        xv[t][u][2] = __uint_as_float(v.y << 16); xv[t][u][3] = __uint_as_float(v.y & 0xffff0000u);
+                    }
+                } else {
+                    xv[t][u][0] = xv[t][u][1] = xv[t][u][2] = xv[t][u][3] = 0.f;
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const float wq[4] = {round_bf16(wv[u].x), round_bf16(wv[u].y), round_bf16(wv[u].z), round_bf16(wv[u].w)};
+#pragma unroll
+            for (int t = 0; t < TT; t++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[t] = fmaf(sizeof(XT) == 4 ? round_bf16(xv[t][u][j]) : xv[t][u][j], wq[j], acc[t]);
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < TT; t++) {
+        const float v = wave_sum(acc[t]);
+        if ((threadIdx.x & 63) == 0) part[wave][t] = v;
+    }
+    __syncthreads();
+    if (threadIdx.x < nt) {
+        const uint32_t t = threadIdx.x;
+        const float v = (part[0][t] + part[1][t]) + (part[2][t] + part[3][t]);
+        logits[(uint64_t)(t0 + t) * experts + e] = v + (bias ? round_bf16(bias[e]) : 0.f);
+    }
+}
+
 // Route plan (routing.metal:4-39, nemotron.metal:238-273) by one workgroup:
 // per-expert route lists in route order, expert-sorted first rows, each
 // route's sorted row, (expert, first list row) tiles of `tile_rows`, and the
@@ -404,20 +468,43 @@ int oco_router(const void *x, oco_dtype x_dtype, const float *w, const float *bi
         // Caller did not ask for the logits: keep them in a per-call allocation.
         OCO_TRY(hip_check(hipMallocAsync((void **)&l, (size_t)tokens * experts * 4, s), "hipMallocAsync"));
     }
-    uint32_t waves = tokens * experts;
-    if (x_dtype == OCO_DT_F32)
-        hipLaunchKernelGGL(router_logits_kernel<float>, dim3((waves + 3) / 4), dim3(256), 0, s,
-                           (const float *)x, w, bias, tokens, hidden, experts, l);
-    else if (x_dtype == OCO_DT_BF16)
-        hipLaunchKernelGGL(router_logits_kernel<bf16_t>, dim3((waves + 3) / 4), dim3(256), 0, s,
-                           (const bf16_t *)x, w, bias, tokens, hidden, experts, l);
-    else
-        return fail(OCO_ERR_UNSUPPORTED, "oco_router: activations must be f32 or bf16");
-    OCO_TRY(launch_check("oco_router logits"));
-    int rc = oco_route_select(l, tokens, experts, k, ids, probs, stream);
+    int rc = router_logits_launch(x, x_dtype, w, bias, tokens, hidden, experts, l, s);
+    if (rc == OCO_OK) rc = oco_route_select(l, tokens, experts, k, ids, probs, stream);
     if (!logits) hipFreeAsync(l, s);
     return rc;
 }
+
+}  // extern "C"
+
+namespace oco {
+int router_logits_launch(const void *x, oco_dtype x_dtype, const float *w, const float *bias, uint32_t tokens,
+                         uint32_t hidden, uint32_t experts, float *logits, hipStream_t s) {
+    const uint32_t waves = tokens * experts;
+    const uint32_t xal = x_dtype == OCO_DT_F32 ? 16 : 8;
+    if (hidden % 4 == 0 && ((uintptr_t)w & 15) == 0 && ((uintptr_t)x & (xal - 1)) == 0 &&
+        (x_dtype == OCO_DT_F32 || x_dtype == OCO_DT_BF16)) {
+        const dim3 grid(experts, (tokens + ROUTER_TOKENS - 1) / ROUTER_TOKENS);
+        if (x_dtype == OCO_DT_F32)
+            hipLaunchKernelGGL(router_logits_wide_kernel<float>, grid, dim3(256), 0, s, (const float *)x, w, bias,
+                               tokens, hidden, experts, logits);
+        else
+            hipLaunchKernelGGL(router_logits_wide_kernel<bf16_t>, grid, dim3(256), 0, s, (const bf16_t *)x, w, bias,
+                               tokens, hidden, experts, logits);
+        return launch_check("router logits");
+    }
+    if (x_dtype == OCO_DT_F32)
+        hipLaunchKernelGGL(router_logits_kernel<float>, dim3((waves + 3) / 4), dim3(256), 0, s,
+                           (const float *)x, w, bias, tokens, hidden, experts, logits);
+    else if (x_dtype == OCO_DT_BF16)
+        hipLaunchKernelGGL(router_logits_kernel<bf16_t>, dim3((waves + 3) / 4), dim3(256), 0, s,
+                           (const bf16_t *)x, w, bias, tokens, hidden, experts, logits);
+    else
+        return fail(OCO_ERR_UNSUPPORTED, "router: activations must be f32 or bf16");
+    return launch_check("router logits");
+}
+}  // namespace oco
+
+extern "C" {
 
 uint64_t oco_route_plan_words(uint32_t routes, uint32_t experts) {
     return 6 + 2 * ((uint64_t)(routes + 15) / 16 + experts) + (uint64_t)experts * (routes + 1) + experts +

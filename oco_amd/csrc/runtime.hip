@@ -26,6 +26,17 @@ int hip_check(hipError_t e, const char *what) {
 
 int launch_check(const char *what) { return hip_check(hipGetLastError(), what); }
 
+// Override table of oco_plan_override: a count of 0 means "not set".
+static int32_t g_knob_vals[OCO_KNOB_COUNT][4];
+static uint32_t g_knob_count[OCO_KNOB_COUNT];
+
+int plan_override(uint32_t knob, int32_t *vals) {
+    if (knob >= OCO_KNOB_COUNT) return 0;
+    const uint32_t n = __atomic_load_n(&g_knob_count[knob], __ATOMIC_ACQUIRE);
+    for (uint32_t i = 0; i < n; i++) vals[i] = g_knob_vals[knob][i];
+    return (int)n;
+}
+
 __global__ void fill32_kernel(uint32_t *dst, uint32_t pattern, size_t words) {
     size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     size_t stride = (size_t)gridDim.x * blockDim.x;
@@ -39,6 +50,15 @@ using namespace oco;
 extern "C" {
 
 const char *oco_last_error(void) { return g_error; }
+
+int oco_plan_override(uint32_t knob, const int32_t *values, uint32_t count) {
+    if (knob >= OCO_KNOB_COUNT) return fail(OCO_ERR_INVALID, "oco_plan_override: unknown knob %u", knob);
+    if (count > 4 || (count && !values)) return fail(OCO_ERR_INVALID, "oco_plan_override: 0..4 values");
+    __atomic_store_n(&g_knob_count[knob], 0u, __ATOMIC_RELEASE);
+    for (uint32_t i = 0; i < count; i++) g_knob_vals[knob][i] = values[i];
+    __atomic_store_n(&g_knob_count[knob], count, __ATOMIC_RELEASE);
+    return OCO_OK;
+}
 
 int oco_block_layout(uint32_t format, uint32_t *elements, uint32_t *bytes) {
     uint32_t e, b;

@@ -162,17 +162,17 @@ def test_matmul_mxfp4_nan_scale_and_nan_activation(lib):
 
 
 @pytest.mark.parametrize("plan", ["2,3", "2,6", "4,3", "4,6"])
-def test_matmul_mxfp4_tile_plans(lib, plan, monkeypatch):
+def test_matmul_mxfp4_tile_plans(lib, plan):
     """Every tile plan (wavefronts along the rows, 32-column tiles per
     wavefront) on tails: lone last block (k % 64 == 32), odd and even K-step
     counts, row and column tails; reruns are bit-identical."""
-    monkeypatch.setenv("OCO_MX_TILE", plan)
-    for m, n, k in [(45, 70, 160), (130, 200, 2880), (257, 400, 576), (512, 193, 1056)]:
-        say("matmul mxfp4 plan", plan, m, n, k)
-        w, x = _mx_case(m, n, k, 51)
-        exact, _ = O.matmul_reference(39, w, x, n, k, half_operands=False)
-        first = run(lib, 39, w, x, m, n, k)
-        assert rel_l2(first, exact) <= 1e-5
-        for _ in range(2):
-            again = run(lib, 39, w, x, m, n, k)
-            assert np.array_equal(again.view(np.uint32), first.view(np.uint32))
+    with lib.overridden(lib.Knob.MX_TILE, [int(v) for v in plan.split(",")]):
+        for m, n, k in [(45, 70, 160), (130, 200, 2880), (257, 400, 576), (512, 193, 1056)]:
+            say("matmul mxfp4 plan", plan, m, n, k)
+            w, x = _mx_case(m, n, k, 51)
+            exact, _ = O.matmul_reference(39, w, x, n, k, half_operands=False)
+            first = run(lib, 39, w, x, m, n, k)
+            assert rel_l2(first, exact) <= 1e-5
+            for _ in range(2):
+                again = run(lib, 39, w, x, m, n, k)
+                assert np.array_equal(again.view(np.uint32), first.view(np.uint32))

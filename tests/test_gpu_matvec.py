@@ -200,12 +200,16 @@ STREAM_PLANS = ["1,1,1", "2,1,2", "1,2,2", "2,2,1", "2,4,1", "1,4,3"]
 
 
 @pytest.mark.parametrize("plan", STREAM_PLANS)
-def test_matvec_stream_plans(lib, plan, monkeypatch):
+def test_matvec_stream_plans(lib, plan):
     """Every streaming-kernel geometry (rows per half-wavefront, K split,
     workgroups per CU) on ragged row counts, f32 and
     bf16 activations, routed rows with bias."""
+    with lib.overridden(lib.Knob.STREAM_PLAN, [int(v) for v in plan.split(",")]):
+        _stream_plan_cases(lib, plan)
+
+
+def _stream_plan_cases(lib, plan):
     from oco_amd import synth
-    monkeypatch.setenv("OCO_STREAM_PLAN", plan)
     for fmt, n, k in [(O.MXFP4, 131, 2880), (P.Q8_0, 77, 4096), (P.Q4_K, 257, 2048), (P.Q6_K, 300, 4096),
                       (P.Q4_0, 90, 4096), (P.Q4_1, 65, 2048), (P.Q5_K, 130, 4096)]:
         say("matvec plan", plan, fmt, n, k)
