@@ -293,6 +293,23 @@ int oco_experts_forward(const oco_experts *w, const float *router_w, const float
                         oco_dtype x_dtype, uint32_t tokens, uint16_t *out, uint32_t *ids, float *probs,
                         float *routed, void *workspace, uint64_t workspace_bytes, oco_stream stream);
 
+/* oco_experts_forward without a workspace argument and without any
+ * allocation: no counterpart in the reference.  It is for callers that
+ * cannot allocate device memory -- code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc.  Its workspace is a
+ * static device array of OCO_EXPERTS_SCRATCH_BYTES per GPU (held until the
+ * process ends; gpt-oss at 16 tokens needs about 2.4 MB of it); calls whose
+ * oco_experts_workspace(w, tokens) exceeds it fail with OCO_ERR_INVALID.
+ * Every call on one GPU shares that GPU's array: calls that overlap on one
+ * GPU (two streams, two threads) race and must be ordered by the caller.
+ * Nothing in it needs to start at zero; it keeps the last call's contents.
+ * Its device address is resolved by oco_device_open, or on the first call
+ * on a device. */
+#define OCO_EXPERTS_SCRATCH_BYTES (8ull << 20)
+int oco_experts_forward_static(const oco_experts *w, const float *router_w, const float *router_bias, const void *x,
+                               oco_dtype x_dtype, uint32_t tokens, uint16_t *out, uint32_t *ids, float *probs,
+                               float *routed, oco_stream stream);
+
 /* Single-token fused expansion: select the top-k experts from `logits`
  * [experts], then gate and up projections of the selected experts with the
  * activation applied; up_out/act_out [k, ffn] f32; ids/probs [k].

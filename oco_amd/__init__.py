@@ -163,6 +163,7 @@ SIGNATURES = {
     "oco_experts_workspace": (_u64, [_EP, _u32]),
     "oco_experts_apply": (_i32, [_EP, _vp, _i32, _vp, _vp, _u32, _vp, _vp, _vp, _u64, _vp]),
     "oco_experts_forward": (_i32, [_EP, _vp, _vp, _vp, _i32, _u32, _vp, _vp, _vp, _vp, _vp, _u64, _vp]),
+    "oco_experts_forward_static": (_i32, [_EP, _vp, _vp, _vp, _i32, _u32, _vp, _vp, _vp, _vp, _vp]),
     "oco_expert_expand": (_i32, [_EP, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
     "oco_moe_sum": (_i32, [_vp, _i32, _vp, _vp, _u32, _u32, _u32, _vp]),
     "oco_norm": (_i32, [_vp, _vp, _vp, _u32, _u32, ctypes.c_float, _i32, _vp]),

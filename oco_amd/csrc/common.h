@@ -15,6 +15,9 @@ int launch_check(const char *what);        // hipGetLastError after a launch
 // runs); copies up to 4 values into vals and returns their count, 0 when the
 // knob is not overridden (the built-in choice table applies).
 int plan_override(uint32_t knob, int32_t *vals);
+// Resolve the device address of the experts' static scratch array on
+// `device` (the current device), once per device.
+int experts_scratch_init(int device);
 }  // namespace oco
 
 #define OCO_TRY(expr)              \

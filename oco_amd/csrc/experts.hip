@@ -19,6 +19,8 @@
 #include "route.h"
 #include "stream.h"
 
+#include <mutex>
+
 namespace oco {
 
 struct MoeArgs {
@@ -661,6 +663,52 @@ int oco_experts_forward(const oco_experts *w, const float *router_w, const float
     OCO_TRY(router_logits_launch(x, x_dtype, router_w, router_bias, tokens, w->hidden, w->experts, logits, s));
     return experts_apply(w, x, x_dtype, ids, probs, logits, tokens, out, routed, workspace, workspace_bytes, s,
                          "oco_experts_forward");
+}
+
+}  // extern "C"
+
+// ---- the layer without allocation -------------------------------------------
+// A file-scope device array stands in for the caller's workspace.  In host
+// code `scratch` names a host-side stand-in, never its device memory: its
+// address on each device comes from hipGetSymbolAddress, once per device,
+// and only that address is handed to kernels.
+static __device__ __align__(256) uint8_t scratch[OCO_EXPERTS_SCRATCH_BYTES];
+constexpr int SCRATCH_DEVICES = 64;
+static void *g_scratch[SCRATCH_DEVICES];
+static std::mutex g_scratch_lock;
+
+namespace oco {
+int experts_scratch_init(int device) {
+    if (device < 0 || device >= SCRATCH_DEVICES)
+        return fail(OCO_ERR_UNSUPPORTED, "experts scratch: device %d beyond %d", device, SCRATCH_DEVICES);
+    std::lock_guard<std::mutex> hold(g_scratch_lock);
+    if (g_scratch[device]) return OCO_OK;
+    void *p = nullptr;
+    OCO_TRY(hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)"));
+    if (!p) return fail(OCO_ERR_HIP, "hipGetSymbolAddress(scratch): null address");
+    g_scratch[device] = p;
+    return OCO_OK;
+}
+}  // namespace oco
+
+extern "C" {
+
+int oco_experts_forward_static(const oco_experts *w, const float *router_w, const float *router_bias, const void *x,
+                               oco_dtype x_dtype, uint32_t tokens, uint16_t *out, uint32_t *ids, float *probs,
+                               float *routed, oco_stream stream) {
+    OCO_TRY(check_bank(w, true));
+    if (!tokens) return OCO_OK;
+    const uint64_t need = oco_experts_workspace(w, tokens);
+    if (need > OCO_EXPERTS_SCRATCH_BYTES)
+        return fail(OCO_ERR_INVALID,
+                    "oco_experts_forward_static: %u tokens need %llu bytes of scratch, over its %llu (use "
+                    "oco_experts_forward with a workspace)",
+                    tokens, (unsigned long long)need, (unsigned long long)OCO_EXPERTS_SCRATCH_BYTES);
+    int dev = 0;
+    OCO_TRY(hip_check(hipGetDevice(&dev), "hipGetDevice"));
+    if (dev < 0 || dev >= SCRATCH_DEVICES || !g_scratch[dev]) OCO_TRY(experts_scratch_init(dev));
+    return oco_experts_forward(w, router_w, router_bias, x, x_dtype, tokens, out, ids, probs, routed, g_scratch[dev],
+                               need, stream);
 }
 
 int oco_expert_expand(const oco_experts *w, const void *x, oco_dtype x_dtype, const float *logits, uint32_t *ids,

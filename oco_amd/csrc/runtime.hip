@@ -92,6 +92,7 @@ int oco_device_open(int ordinal, int *compute_units) {
     if (ordinal < 0 || ordinal >= count)
         return fail(OCO_ERR_INVALID, "device %d out of range (%d devices)", ordinal, count);
     OCO_TRY(hip_check(hipSetDevice(ordinal), "hipSetDevice"));
+    OCO_TRY(experts_scratch_init(ordinal));
     if (compute_units) {
         int cu = 0;
         OCO_TRY(hip_check(hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, ordinal),
