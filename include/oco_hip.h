@@ -91,7 +91,7 @@ const char *oco_last_error(void);
  * tuning runs can compare them.  count == 0 clears the knob.  Not
  * synchronised with launches on other threads: set knobs before launching. */
 typedef enum oco_knob {
-    OCO_KNOB_STREAM_PLAN = 0,     /* streaming matvec: rows per half-wave (1|2), K split (1|2|4), WGs per CU */
+    OCO_KNOB_STREAM_PLAN = 0,     /* streaming matvec: 1 (reserved), K split (1|2|4), WGs per CU */
     OCO_KNOB_MATVEC_PLAN = 1,     /* plain matvec (F32/F16/BF16): rows per wave, K split */
     OCO_KNOB_MATVEC_PLAIN = 2,    /* value 1: quantized formats take the plain matvec, not the streaming one */
     OCO_KNOB_MX_TILE = 3,         /* MXFP4 prefill tile: wavefronts along rows, 32-column tiles per wave */
@@ -102,7 +102,8 @@ typedef enum oco_knob {
     OCO_KNOB_MOE_Q4_ROWS = 8,     /* Q4_K grouped tiles: rows per tile (32|48|64), value 0: the f16 LDS tiles */
     OCO_KNOB_MOE_WG = 9,          /* routed decode kernel: workgroups per CU */
     OCO_KNOB_MX_EXPERTS_KS = 10,  /* MXFP4 expert down tiles of 16 rows: K split (1|2) */
-    OCO_KNOB_COUNT = 11
+    OCO_KNOB_STREAM_DIRECT = 11,  /* value 0: Q4_K/Q5_K streaming matvec through the LDS tile even when aligned */
+    OCO_KNOB_COUNT = 12
 } oco_knob;
 int oco_plan_override(uint32_t knob, const int32_t *values, uint32_t count);
 

@@ -52,6 +52,7 @@ class Knob(enum.IntEnum):
     MOE_Q4_ROWS = 8
     MOE_WG = 9
     MX_EXPERTS_KS = 10
+    STREAM_DIRECT = 11
 
 
 class DType(enum.IntEnum):

@@ -26,6 +26,9 @@ FLAGS = [
     # the feature, which is harmless.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-fno-gpu-rdc", "-Wno-unused-command-line-argument",
+    # Leading scalar kernel arguments arrive preloaded in SGPRs instead of
+    # being fetched from the kernarg segment at wave start.
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     f"-I{os.path.join(HERE, '..', 'include')}",
 ]
 

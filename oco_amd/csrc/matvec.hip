@@ -20,6 +20,21 @@
 #include "stream.h"
 #include "norm.h"
 
+// Timeline probes for tuning builds only (-DOCO_TIMELINE): per workgroup,
+// wave 0 stamps s_memrealtime at entry and s_memtime at each marked point.
+#ifdef OCO_TIMELINE
+__device__ unsigned long long g_tl[8192 * 8];
+#define TL_STAMP(i)                                                                                      \
+    do {                                                                                                 \
+        if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < 8192)                                    \
+            g_tl[blockIdx.x * 8 + (i)] = (i) == 0 ? __builtin_amdgcn_s_memrealtime() : __builtin_amdgcn_s_memtime(); \
+    } while (0)
+#else
+#define TL_STAMP(i) \
+    do {            \
+    } while (0)
+#endif
+
 namespace oco {
 
 struct MatvecArgs {
@@ -151,12 +166,53 @@ struct StreamShape {
     static constexpr int LPR = (BYTES_MAX + 1023) / 1024;
 };
 
-template <int FMT, typename XT, int R, int NPL>
-__global__ __launch_bounds__(256) void stream_kernel(StreamArgs a) {
+// The values the first loads depend on come first, as scalars: the command
+// processor preloads leading scalar kernel arguments into SGPRs (built with
+// -amdgpu-kernarg-preload-count), so the weight and activation loads issue
+// without waiting for a kernarg fetch; the rest of StreamArgs is read behind
+// them.
+template <int FMT>
+struct DirectOk {
+    static constexpr bool value = false;
+};
+template <>
+struct DirectOk<OCO_Q4_K> {
+    static constexpr bool value = true;
+};
+template <>
+struct DirectOk<OCO_Q5_K> {
+    static constexpr bool value = true;
+};
+
+// DIRECT (Q4_K / Q5_K on a 16-byte aligned base, whose blocks are then all
+// 16-byte aligned): each lane loads its pieces' 16-byte chunks straight into
+// registers, with no LDS tile and no realignment.
+template <int FMT, typename XT, int NPL, int NORM, bool DIRECT>
+__global__ __launch_bounds__(256) void stream_kernel(const uint8_t *w_, const void *x_, uint32_t row_bytes_,
+                                                     uint32_t n_, uint32_t k_, uint32_t mode_, uint32_t slice_,
+                                                     uint32_t ngroups_, uint32_t experts_, uint32_t routes_,
+                                                     StreamArgs a) {
+    a.w = w_;
+    a.x = x_;
+    a.row_bytes = row_bytes_;
+    a.p.n = n_;
+    a.p.k = k_;
+    // mode_: bits 0-1 log2 of the K split
+    const uint32_t ks_log2 = mode_ & 3u;
+    a.ks = 1u << ks_log2;
+    a.slice_blocks = slice_;
+    a.ngroups = ngroups_;
+    // routes_ carries route_major in its top bit
+    a.p.experts = experts_;
+    a.p.routes = routes_ & 0x7fffffffu;
+    a.p.route_major = routes_ >> 31;
+    TL_STAMP(0);
+    TL_STAMP(1);
     using T = Tile<FMT>;
     constexpr int LPR = StreamShape<FMT, NPL>::LPR;
-    constexpr int ROWS = 2 * R;                 // tile rows per wavefront
-    constexpr int TILE = ROWS * LPR * 1024;     // LDS bytes per wavefront tile
+    constexpr int ROWS = 2;                     // tile rows per wavefront (one per half-wavefront)
+    constexpr int TILE = DIRECT ? 0 : ROWS * LPR * 1024;  // LDS bytes per wavefront tile
+    constexpr int NS = T::NSUM > 0 ? T::NSUM : 1;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const oco_matrix &p = a.p;
     const uint32_t PT = p.k / T::BLOCK * T::P;  // pieces per full row
@@ -165,24 +221,20 @@ __global__ __launch_bounds__(256) void stream_kernel(StreamArgs a) {
     uint8_t *tiles = smem + (size_t)p.k * 4 + (size_t)T::NSUM * PT * 4;
     float *part = reinterpret_cast<float *>(tiles + 4 * TILE);
 
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, half = lane >> 5, c = lane & 31;
-    const uint32_t ks = a.ks, sets = 4 / ks, set = wave / ks, sl = wave % ks;
+    // The wavefront index is uniform: as a scalar, every row and group offset
+    // below is SALU work.
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63, half = lane >> 5, c = lane & 31;
+    const uint32_t ks = a.ks, sets = 4 >> ks_log2, set = wave >> ks_log2, sl = wave & (ks - 1);
     const uint32_t route = blockIdx.y;
     const uint32_t expert = p.experts > 1 ? a.ids[route] : 0;
     const uint32_t input = (p.experts > 1 && !p.route_major) ? route / p.routes : route;
     const uint32_t rows_per_group = sets * ROWS;
 
-    // One buffer resource over this expert's rows, based 16-byte aligned.
-    // Buffer loads zero any access that straddles num_records, so the range
-    // extends to the 16-byte boundary after the last byte: that chunk lies in
-    // the same page as the tensor's last byte, and bytes past the end of the
-    // last row are never decoded.
+    // This expert's rows, from the 16-byte boundary at or below their start.
     const uint8_t *ebase = a.w + (uint64_t)expert * p.n * a.row_bytes;
     const uintptr_t base_al = (uintptr_t)ebase & ~(uintptr_t)15;
     const uint32_t shift = (uint32_t)((uintptr_t)ebase & 15);
-    const uint64_t span = ((uint64_t)p.n * a.row_bytes + shift + 15) & ~15ull;
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)base_al, 0, (uint32_t)(span > 0xffffffffull ? 0xffffffffull : span), 0x00020000);
 
     // This wavefront's K slice.
     const uint32_t nblocks = p.k / T::BLOCK;
@@ -191,28 +243,85 @@ __global__ __launch_bounds__(256) void stream_kernel(StreamArgs a) {
     const uint32_t slice_bytes = (b1 - b0) * T::BYTES;
     const uint32_t pieces = (b1 - b0) * T::P;
 
-    u32x4 regs[ROWS * LPR];
+    // Two groups' loads in flight per wavefront: a ring of two register sets.
+    u32x4 ra[DIRECT ? 1 : ROWS * LPR], rb[DIRECT ? 1 : ROWS * LPR];
+    typename T::Raw da[DIRECT ? NPL : 1], db[DIRECT ? NPL : 1];
+    __amdgpu_buffer_rsrc_t rall;
+    if constexpr (DIRECT) {
+        const uint64_t bytes = (uint64_t)p.n * a.row_bytes;
+        rall = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(ebase), 0,
+                                                 (uint32_t)(bytes > 0xffffffffull ? 0xffffffffull : bytes), 0x00020000);
+    }
+    // DIRECT: this half-wavefront's row of group g (rows past n read row n - 1
+    // and are never stored), pieces past the slice read the last piece.
+    auto issue_direct = [&](uint32_t g, typename T::Raw *dst) __attribute__((always_inline)) {
+        if constexpr (DIRECT) {
+            const uint32_t row = min(g * rows_per_group + set * ROWS + half, p.n - 1);
+            const uint32_t roff = row * (uint32_t)a.row_bytes;
+#pragma unroll
+            for (int s = 0; s < NPL; s++) {
+                const uint32_t pl = min(c + 32u * s, pieces - 1), blk = b0 + pl / T::P, cc = pl % T::P;
+                dst[s] = T::direct(rall, roff + blk * T::BYTES, cc);
+            }
+        }
+    };
     // Byte offset of tile row i of group g from base_al.
     auto row_offset = [&](uint32_t g, int i) -> uint32_t {
         const uint32_t row = g * rows_per_group + set * ROWS + i;
         return (uint32_t)(shift + (uint64_t)row * a.row_bytes + (uint64_t)b0 * T::BYTES);
     };
-    auto issue = [&](uint32_t g) {
+    // One buffer resource per tile row, from the 16-byte boundary below the
+    // row's slice to the end of the slice rounded up to a whole chunk: the
+    // loads need no per-lane range test, since chunks past the range read as
+    // zero without touching memory (the range check covers the per-lane
+    // offset; the scalar offset stays 0).  The rounded-up chunk ends within
+    // the 16 bytes after the slice, in the same page as its last byte.  Rows
+    // past n get an empty range.
+    auto issue = [&](uint32_t g, u32x4 *regs) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < ROWS; i++) {
-            const uint32_t off = row_offset(g, i), start = off & ~15u, need = (off & 15u) + slice_bytes;
+            const uint32_t row = g * rows_per_group + set * ROWS + i;
+            const uint32_t off = row_offset(g, i), start = off & ~15u;
+            const uint32_t need = row < p.n ? (off & 15u) + slice_bytes : 0u;
+            const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
+                (void *)(base_al + start), 0, (need + 15u) & ~15u, 0x00020000);
 #pragma unroll
-            for (int u = 0; u < LPR; u++) {
-                const uint32_t j = (uint32_t)(u * 64 + lane);
-                regs[i * LPR + u] = 16 * j < need
-                                        ? __builtin_amdgcn_raw_buffer_load_b128(rs, start + 16 * j, 0, 2 /* nontemporal */)
-                                        : u32x4{0, 0, 0, 0};
-            }
+            for (int u = 0; u < LPR; u++)
+                regs[i * LPR + u] = __builtin_amdgcn_raw_buffer_load_b128(rr, 16 * (64 * u + lane), 0, 2 /* nontemporal */);
         }
     };
 
-    uint32_t g = blockIdx.x;
-    if (g < a.ngroups) issue(g);
+    // The first 1024 float4 of x are requested before the weights: they come
+    // from L2 and arrive while the weights are still in flight (loads return
+    // in issue order).  A fused norm reads x itself first, so it does not.
+    const XT *xr = reinterpret_cast<const XT *>(a.x) + (uint64_t)input * p.k;
+    float xpre[4][4];
+    if constexpr (!NORM) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const uint32_t f = threadIdx.x + 256 * u;
+            if (f < p.k / 4) {
+                if constexpr (sizeof(XT) == 4) {
+                    const float4 t = reinterpret_cast<const float4 *>(xr)[f];
+                    xpre[u][0] = t.x; xpre[u][1] = t.y; xpre[u][2] = t.z; xpre[u][3] = t.w;
+                } else {
+                    const uint2 t = reinterpret_cast<const uint2 *>(xr)[f];
+                    xpre[u][0] = __uint_as_float(t.x << 16); xpre[u][1] = __uint_as_float(t.x & 0xffff0000u);
+                    xpre[u][2] = __uint_as_float(t.y << 16); xpre[u][3] = __uint_as_float(t.y & 0xffff0000u);
+                }
+            }
+        }
+    }
+
+    const uint32_t G = gridDim.x, g0 = blockIdx.x;
+    if constexpr (DIRECT) {
+        if (g0 < a.ngroups) issue_direct(g0, da);
+        if (g0 + G < a.ngroups) issue_direct(g0 + G, db);
+    } else {
+        if (g0 < a.ngroups) issue(g0, ra);
+        if (g0 + G < a.ngroups) issue(g0 + G, rb);
+    }
+    TL_STAMP(2);
 
     // Stage x (f32) in piece-major order, then the per-piece sums.  With a
     // fused norm, x is the bf16 row before normalisation: every workgroup
@@ -220,17 +329,17 @@ __global__ __launch_bounds__(256) void stream_kernel(StreamArgs a) {
     // staged values equal oco_norm's output bit for bit) and normalises
     // while staging.
     {
-        const XT *xr = reinterpret_cast<const XT *>(a.x) + (uint64_t)input * p.k;
         float inv = 1.f;
-        if (a.norm_mode) inv = block_inv_rms(reinterpret_cast<const uint16_t *>(xr), p.k, a.norm_eps, part);
-        // Four loads in flight per thread before any store: x arrives in one
-        // memory round trip, not one per loop iteration.
+        if constexpr (NORM != 0) inv = block_inv_rms(reinterpret_cast<const uint16_t *>(xr), p.k, a.norm_eps, part);
         for (uint32_t f0 = threadIdx.x; f0 < p.k / 4; f0 += 4 * 256) {
             float v[4][4];
 #pragma unroll
             for (int u = 0; u < 4; u++) {
                 const uint32_t f = f0 + 256 * u;
-                if (f < p.k / 4) {
+                if (!NORM && f0 == threadIdx.x) {
+#pragma unroll
+                    for (int e = 0; e < 4; e++) v[u][e] = xpre[u][e];
+                } else if (f < p.k / 4) {
                     if constexpr (sizeof(XT) == 4) {
                         const float4 t = reinterpret_cast<const float4 *>(xr)[f];
                         v[u][0] = t.x; v[u][1] = t.y; v[u][2] = t.z; v[u][3] = t.w;
@@ -245,7 +354,7 @@ __global__ __launch_bounds__(256) void stream_kernel(StreamArgs a) {
             for (int u = 0; u < 4; u++) {
                 const uint32_t f = f0 + 256 * u;
                 if (f < p.k / 4) {
-                    if (a.norm_mode) {
+                    if constexpr (NORM != 0) {
                         float wn[4];
                         if (((uintptr_t)a.norm_w & 15u) == 0) {
                             const float4 t = reinterpret_cast<const float4 *>(a.norm_w)[f];
@@ -256,7 +365,7 @@ __global__ __launch_bounds__(256) void stream_kernel(StreamArgs a) {
                         }
 #pragma unroll
                         for (int e = 0; e < 4; e++)
-                            v[u][e] = bf16_bits_to_f32(norm_value_bits(v[u][e], inv, wn[e], a.norm_mode == 2));
+                            v[u][e] = bf16_bits_to_f32(norm_value_bits(v[u][e], inv, wn[e], NORM == 2));
                     }
                     uint32_t pp, tt;
                     T::map(f, pp, tt);
@@ -267,7 +376,7 @@ __global__ __launch_bounds__(256) void stream_kernel(StreamArgs a) {
         if constexpr (T::NSUM > 0) {
             __syncthreads();
             for (uint32_t pp = threadIdx.x; pp < PT; pp += 256) {
-                float xv[32], sv[T::NSUM > 0 ? T::NSUM : 1];
+                float xv[32], sv[NS];
 #pragma unroll
                 for (int t = 0; t < 8; t++) {
                     float4 q = xs4[t * PT + pp];
@@ -280,94 +389,103 @@ __global__ __launch_bounds__(256) void stream_kernel(StreamArgs a) {
         }
         __syncthreads();
     }
+    TL_STAMP(3);
+
+    // Each lane keeps the activations (and sums) of its pieces -- c + 32 s of
+    // this wavefront's K slice, the same for every row group -- in registers.
+    float xv[NPL][32], sv[NPL][NS];
+#pragma unroll
+    for (int s = 0; s < NPL; s++) {
+        const uint32_t pg = b0 * T::P + min(c + 32u * s, pieces > 0 ? pieces - 1 : 0u);
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            const float4 q = xs4[t * PT + pg];
+            xv[s][4 * t] = q.x; xv[s][4 * t + 1] = q.y; xv[s][4 * t + 2] = q.z; xv[s][4 * t + 3] = q.w;
+        }
+#pragma unroll
+        for (int j = 0; j < T::NSUM; j++) sv[s][j] = xsum[j * PT + pg];
+    }
 
     uint8_t *tile = tiles + (size_t)wave * TILE;
-    for (; g < a.ngroups; g += gridDim.x) {
+    // One row group: its registers to this wavefront's LDS tile, the loads of
+    // the group two ahead into the freed registers, then the decode.
+    auto group = [&](uint32_t g, u32x4 *regs, typename T::Raw *dr) __attribute__((always_inline)) {
+        float acc = 0.f;
+        if constexpr (DIRECT) {
+            typename T::Raw cur[NPL];
 #pragma unroll
-        for (int i = 0; i < ROWS * LPR; i++) reinterpret_cast<u32x4 *>(tile)[i * 64 + lane] = regs[i];
-        uint32_t rbase[R];
+            for (int s = 0; s < NPL; s++) cur[s] = dr[s];
+            if (g + 2 * G < a.ngroups) issue_direct(g + 2 * G, dr);
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-            const int i = half * R + r;
-            rbase[r] = i * LPR * 1024 + (row_offset(g, i) & 15u);
-        }
-        const uint32_t gnext = g + gridDim.x;
-        if (gnext < a.ngroups) issue(gnext);
-
-        float acc[R];
+            for (int s = 0; s < NPL; s++) {
+                const uint32_t pl = c + 32 * s;
+                if (pl < pieces) acc += tile_dot<FMT>(cur[s], xv[s], sv[s], pl % T::P);
+            }
+        } else {
 #pragma unroll
-        for (int r = 0; r < R; r++) acc[r] = 0.f;
+            for (int i = 0; i < ROWS * LPR; i++) reinterpret_cast<u32x4 *>(tile)[i * 64 + lane] = regs[i];
+            if (g == blockIdx.x) TL_STAMP(4);
+            const uint32_t rbase = half * LPR * 1024 + (row_offset(g, half) & 15u);
+            if (g + 2 * G < a.ngroups) issue(g + 2 * G, regs);
 #pragma unroll
-        for (int s = 0; s < NPL; s++) {
-            const uint32_t pl = c + 32 * s;
-            if (pl < pieces) {
-                const uint32_t pg = b0 * T::P + pl;  // piece index in the full row
-                float xv[32], sv[T::NSUM > 0 ? T::NSUM : 1];
-#pragma unroll
-                for (int t = 0; t < 8; t++) {
-                    float4 q = xs4[t * PT + pg];
-                    xv[4 * t] = q.x; xv[4 * t + 1] = q.y; xv[4 * t + 2] = q.z; xv[4 * t + 3] = q.w;
-                }
-#pragma unroll
-                for (int j = 0; j < T::NSUM; j++) sv[j] = xsum[j * PT + pg];
-                const uint32_t blk = pl / T::P, cc = pl % T::P;
-#pragma unroll
-                for (int r = 0; r < R; r++) {
-                    typename T::Raw raw = T::load(tile + rbase[r] + blk * T::BYTES, cc);
-                    acc[r] += tile_dot<FMT>(raw, xv, sv, cc);
+            for (int s = 0; s < NPL; s++) {
+                const uint32_t pl = c + 32 * s;
+                if (pl < pieces) {
+                    const uint32_t blk = pl / T::P, cc = pl % T::P;
+                    typename T::Raw raw = T::load(tile + rbase + blk * T::BYTES, cc);
+                    acc += tile_dot<FMT>(raw, xv[s], sv[s], cc);
                 }
             }
         }
-#pragma unroll
-        for (int r = 0; r < R; r++) acc[r] = half_sum(acc[r]);
+        acc = half_sum(acc);
+        if (g == blockIdx.x) TL_STAMP(5);
 
-        const uint32_t row0 = g * rows_per_group + set * ROWS + half * R;
+        const uint32_t row = g * rows_per_group + set * ROWS + half;
         if (ks > 1) {
-            if (c == 0) {
-#pragma unroll
-                for (int r = 0; r < R; r++) part[(wave * 2 + half) * R + r] = acc[r];
-            }
+            if (c == 0) part[wave * 2 + half] = acc;
             __syncthreads();
             if (sl == 0) {
-#pragma unroll
-                for (int r = 0; r < R; r++) {
-                    float v = 0.f;
-                    for (uint32_t j = 0; j < ks; j++) v += part[((wave + j) * 2 + half) * R + r];
-                    acc[r] = v;
-                }
+                float v = 0.f;
+                for (uint32_t j = 0; j < ks; j++) v += part[(wave + j) * 2 + half];
+                acc = v;
             }
             __syncthreads();
         }
-        if (sl == 0 && c < R) {
-            float v = acc[0];
-#pragma unroll
-            for (int r = 1; r < R; r++)
-                if (c == (uint32_t)r) v = acc[r];
-            const uint32_t row = row0 + c;
-            if (row < p.n) {
-                if (p.has_bias)
-                    v += round_bf16(a.bias[(uint64_t)expert * p.n + row] + (p.has_bias == 2 ? 1.0f : 0.0f));
-                const uint64_t o = (uint64_t)route * p.n + row;
-                if (a.y_bf16)
-                    reinterpret_cast<uint16_t *>(a.y)[o] = f32_to_bf16_bits(v);
-                else
-                    reinterpret_cast<float *>(a.y)[o] = v;
-            }
+        if (sl == 0 && c == 0 && row < p.n) {
+            float v = acc;
+            if (p.has_bias) v += round_bf16(a.bias[(uint64_t)expert * p.n + row] + (p.has_bias == 2 ? 1.0f : 0.0f));
+            const uint64_t o = (uint64_t)route * p.n + row;
+            if (a.y_bf16)
+                reinterpret_cast<uint16_t *>(a.y)[o] = f32_to_bf16_bits(v);
+            else
+                reinterpret_cast<float *>(a.y)[o] = v;
         }
+    };
+    for (uint32_t g = g0; g < a.ngroups; g += 2 * G) {
+        group(g, ra, da);
+        if (g + G < a.ngroups) group(g + G, rb, db);
     }
+    TL_STAMP(6);
 }
 
-typedef void (*StreamFn)(StreamArgs);
+typedef void (*StreamFn)(const uint8_t *, const void *, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t,
+                         uint32_t, uint32_t, StreamArgs);
 
-template <int FMT, typename XT, int R>
-static StreamFn stream_pick_npl(int npl) {
+template <int FMT, typename XT, int NORM, bool DIRECT>
+static StreamFn stream_pick_npl_d(int npl) {
     switch (npl) {
-    case 1: return stream_kernel<FMT, XT, R, 1>;
-    case 2: return stream_kernel<FMT, XT, R, 2>;
-    case 3: return stream_kernel<FMT, XT, R, 3>;
-    case 4: return stream_kernel<FMT, XT, R, 4>;
+    case 1: return stream_kernel<FMT, XT, 1, NORM, DIRECT>;
+    case 2: return stream_kernel<FMT, XT, 2, NORM, DIRECT>;
+    case 3: return stream_kernel<FMT, XT, 3, NORM, DIRECT>;
+    case 4: return stream_kernel<FMT, XT, 4, NORM, DIRECT>;
     }
     return nullptr;
+}
+template <int FMT, typename XT, int NORM>
+static StreamFn stream_pick_npl(int npl, bool direct) {
+    if constexpr (DirectOk<FMT>::value)
+        if (direct) return stream_pick_npl_d<FMT, XT, NORM, true>(npl);
+    return stream_pick_npl_d<FMT, XT, NORM, false>(npl);
 }
 
 template <int FMT>
@@ -381,13 +499,18 @@ static int stream_lpr(int npl) {
     return 0;
 }
 
+// norm (fused RMS norm: 0 off, 1 on, 2 full_layer rounding) only with bf16 rows.
 template <typename XT>
-static StreamFn stream_pick_format(uint32_t fmt, int r, int npl, int &lpr) {
+static StreamFn stream_pick_format(uint32_t fmt, int norm, int npl, bool direct, int &lpr) {
     switch (fmt) {
 #define F(FM)                                                                                   \
     case FM:                                                                                    \
         lpr = stream_lpr<FM>(npl);                                                              \
-        return r == 1 ? stream_pick_npl<FM, XT, 1>(npl) : stream_pick_npl<FM, XT, 2>(npl);
+        if constexpr (sizeof(XT) == 2) {                                                        \
+            if (norm == 1) return stream_pick_npl<FM, XT, 1>(npl, direct);                      \
+            if (norm == 2) return stream_pick_npl<FM, XT, 2>(npl, direct);                      \
+        }                                                                                       \
+        return norm ? nullptr : stream_pick_npl<FM, XT, 0>(npl, direct);
         F(OCO_Q8_0) F(OCO_MXFP4) F(OCO_Q4_K) F(OCO_Q6_K) F(OCO_Q4_0) F(OCO_Q4_1) F(OCO_Q5_K)
 #undef F
     }
@@ -524,7 +647,6 @@ static int matvec_impl(uint32_t format, const void *w, const void *x, oco_dtype 
         const uint32_t nblocks = p->k / be;
         StreamPlan sp = stream_plan(format, p->k, p->n, p->m);
         if (sp.ks != 1 && sp.ks != 2 && sp.ks != 4) sp.ks = 1;
-        if (sp.r != 1 && sp.r != 2) sp.r = 1;
         uint32_t slice_blocks = (nblocks + sp.ks - 1) / sp.ks;
         int npl = (int)((slice_blocks * P + 31) / 32);
         while (npl > 4 && sp.ks < 4) {  // widen the K split until a lane's pieces fit
@@ -532,10 +654,25 @@ static int matvec_impl(uint32_t format, const void *w, const void *x, oco_dtype 
             slice_blocks = (nblocks + sp.ks - 1) / sp.ks;
             npl = (int)((slice_blocks * P + 31) / 32);
         }
+        // Q4_K / Q5_K blocks are whole 16-byte chunks: on a 16-byte aligned
+        // base every lane loads its own pieces (OCO_KNOB_STREAM_DIRECT 0 turns
+        // this off).
+        int32_t dov[4];
+        const bool direct = (format == OCO_Q4_K || format == OCO_Q5_K) && ((uintptr_t)w & 15u) == 0 &&
+                            !(plan_override(OCO_KNOB_STREAM_DIRECT, dov) && dov[0] == 0);
+        // Direct loads hold three register sets of pieces: past two pieces per
+        // lane that costs occupancy, so split K further (measured: Q4_K and
+        // Q5_K 12288 x 4096, 14.7 -> 11.1 us).
+        int32_t sov[4];
+        while (direct && npl > 2 && sp.ks < 4 && plan_override(OCO_KNOB_STREAM_PLAN, sov) != 3) {
+            sp.ks *= 2;
+            slice_blocks = (nblocks + sp.ks - 1) / sp.ks;
+            npl = (int)((slice_blocks * P + 31) / 32);
+        }
         int lpr = 0;
         StreamFn fn = npl > 4 ? nullptr
-                    : x_dtype == OCO_DT_F32 ? stream_pick_format<float>(format, sp.r, npl, lpr)
-                                            : stream_pick_format<bf16_t>(format, sp.r, npl, lpr);
+                    : x_dtype == OCO_DT_F32 ? stream_pick_format<float>(format, norm ? (norm->full_layer ? 2 : 1) : 0, npl, direct, lpr)
+                                            : stream_pick_format<bf16_t>(format, norm ? (norm->full_layer ? 2 : 1) : 0, npl, direct, lpr);
         if (fn) {
             StreamArgs a;
             a.w = (const uint8_t *)w;
@@ -551,13 +688,13 @@ static int matvec_impl(uint32_t format, const void *w, const void *x, oco_dtype 
             a.norm_mode = norm ? (norm->full_layer ? 2u : 1u) : 0u;
             a.norm_eps = norm ? norm->epsilon : 0.f;
             a.norm_w = norm ? norm->w : nullptr;
-            const uint32_t rows_per_group = (4 / sp.ks) * 2 * sp.r;
+            const uint32_t rows_per_group = (4 / sp.ks) * 2;
             a.ngroups = (p->n + rows_per_group - 1) / rows_per_group;
             const uint32_t nsum = (format == OCO_Q8_0 || format == OCO_Q4_0 || format == OCO_Q4_1) ? 1
                                   : (format == OCO_Q4_K || format == OCO_Q5_K)                    ? 2
                                   : format == OCO_Q6_K                                            ? 4
                                                                                                   : 0;
-            const size_t tile = (size_t)2 * sp.r * lpr * 1024;
+            const size_t tile = direct ? 0 : (size_t)2 * lpr * 1024;
             const size_t lds = (size_t)p->k * 4 + (size_t)nsum * (p->k / 32) * 4 + 4 * tile + 32 * sizeof(float);
             if (lds > 160 * 1024)
                 return fail(OCO_ERR_UNSUPPORTED, "oco_matvec: k=%u needs %zu bytes of LDS", p->k, lds);
@@ -566,7 +703,11 @@ static int matvec_impl(uint32_t format, const void *w, const void *x, oco_dtype 
                                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
                                   "hipFuncSetAttribute"));
             const uint32_t grid = std::min<uint32_t>(a.ngroups, (uint32_t)(cus * sp.wg_per_cu));
-            hipLaunchKernelGGL(fn, dim3(grid, p->m), dim3(256), lds, (hipStream_t)stream, a);
+            if (a.p.routes > 0x7fffffffu) return fail(OCO_ERR_INVALID, "oco_matvec: routes=%u", a.p.routes);
+            const uint32_t mode = sp.ks == 4 ? 2u : sp.ks == 2 ? 1u : 0u;
+            hipLaunchKernelGGL(fn, dim3(grid, p->m), dim3(256), lds, (hipStream_t)stream, a.w, a.x,
+                               (uint32_t)a.row_bytes, a.p.n, a.p.k, mode, a.slice_blocks, a.ngroups, a.p.experts,
+                               a.p.routes | (a.p.route_major ? 0x80000000u : 0u), a);
             return launch_check("oco_matvec");
         }
     }
@@ -600,6 +741,12 @@ static int matvec_impl(uint32_t format, const void *w, const void *x, oco_dtype 
     hipLaunchKernelGGL(fn, grid, dim3(256), 0, (hipStream_t)stream, a);
     return launch_check("oco_matvec");
 }
+
+#ifdef OCO_TIMELINE
+extern "C" int oco_timeline_read(void *host, size_t bytes) {
+    return hip_check(hipMemcpyFromSymbol(host, HIP_SYMBOL(g_tl), bytes), "timeline");
+}
+#endif
 
 extern "C" int oco_matvec(uint32_t format, const void *w, const void *x, oco_dtype x_dtype, void *y,
                           oco_dtype y_dtype, const float *bias, const uint32_t *ids,

@@ -48,6 +48,15 @@ __device__ __forceinline__ uint32_t lds_u16(const uint8_t *p) {
 template <int FMT>
 struct Tile;
 
+// Two nibble codes at once: byte c < 16 read as E4M3 is exactly c * 2^-9,
+// so v_cvt_scalef32_pk_f32_fp8 on a dword of masked nibbles (bytes 0-1 or
+// 2-3 by HI) with the scale 2^9 gives c0 and c1 as floats.  (The scale
+// operand acts as a power of two: only its exponent is applied.)
+template <bool HI>
+__device__ __forceinline__ f32x2 nib2(uint32_t masked) {
+    return __builtin_amdgcn_cvt_scalef32_pk_f32_fp8((int)masked, 512.f, HI);
+}
+
 // MXFP4: piece = block {e, 16 code bytes}; code byte i holds columns i (low
 // nibble) and 16 + i (high nibble) of the block.  gfx950's
 // v_cvt_scalef32_pk_f32_fp4 decodes two E2M1 codes per instruction.
@@ -165,6 +174,17 @@ struct Tile<OCO_Q4_K> {
         r.qs = lds_u128(blk + 16 + 16 * c);
         return r;
     }
+    // Piece c of the block at byte `off` straight from memory (16-byte
+    // aligned blocks: 144 is a multiple of 16).
+    static constexpr bool DIRECT = true;
+    __device__ __forceinline__ static Raw direct(__amdgpu_buffer_rsrc_t rs, uint32_t off, uint32_t c) {
+        Raw r;
+        const u32x4 h = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 2);
+        const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16 + 16 * c, 0, 2);
+        r.hdr = make_uint4(h.x, h.y, h.z, h.w);
+        r.qs = make_uint4(q.x, q.y, q.z, q.w);
+        return r;
+    }
     __device__ __forceinline__ static float dot(const Raw &r, const float *x, const float *s, int c) {
         const uint32_t g = (uint32_t)c >> 1;
         // (scale, min) of sub-blocks 2g and 2g+1 (weights.metal:70-71) from
@@ -184,18 +204,23 @@ struct Tile<OCO_Q4_K> {
         }
         const uint32_t sc0 = scm[0][0], mn0 = scm[0][1], sc1 = scm[1][0], mn1 = scm[1][1];
         const uint32_t w[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
+        const float d = half_bits_to_f32(r.hdr.x & 0xffffu), dmin = half_bits_to_f32(r.hdr.x >> 16);
         float a0 = 0.f, a1 = 0.f;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            uint32_t lo = w[j] & 0x0f0f0f0fu, hi = (w[j] >> 4) & 0x0f0f0f0fu;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                a0 = fmaf(ub(lo, i), x[4 * j + i], a0);
-                a1 = fmaf(ub(hi, i), x[16 + 4 * j + i], a1);
-            }
+            const uint32_t lo = w[j] & 0x0f0f0f0fu, hi = (w[j] >> 4) & 0x0f0f0f0fu;
+            const f32x2 l0 = nib2<false>(lo), l1 = nib2<true>(lo);
+            const f32x2 h0 = nib2<false>(hi), h1 = nib2<true>(hi);
+            a0 = fmaf(l0.x, x[4 * j], a0);
+            a1 = fmaf(h0.x, x[16 + 4 * j], a1);
+            a0 = fmaf(l0.y, x[4 * j + 1], a0);
+            a1 = fmaf(h0.y, x[16 + 4 * j + 1], a1);
+            a0 = fmaf(l1.x, x[4 * j + 2], a0);
+            a1 = fmaf(h1.x, x[16 + 4 * j + 2], a1);
+            a0 = fmaf(l1.y, x[4 * j + 3], a0);
+            a1 = fmaf(h1.y, x[16 + 4 * j + 3], a1);
         }
-        float d = half_bits_to_f32(r.hdr.x & 0xffffu), dmin = half_bits_to_f32(r.hdr.x >> 16);
-        float v = fmaf(d * (float)sc0, a0, -(dmin * (float)mn0) * s[0]);
+        const float v = fmaf(d * (float)sc0, a0, -(dmin * (float)mn0) * s[0]);
         return fmaf(d * (float)sc1, a1, fmaf(-(dmin * (float)mn1), s[1], v));
     }
 };
@@ -281,17 +306,23 @@ struct Tile<OCO_Q4_0> {
         r.q = lds_u128(blk + 2);
         return r;
     }
+    // sum of code * x over the block
     __device__ __forceinline__ static float nibble_dot(const uint4 &q, const float *x) {
         const uint32_t w[4] = {q.x, q.y, q.z, q.w};
         float a0 = 0.f, a1 = 0.f;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const uint32_t lo = w[j] & 0x0f0f0f0fu, hi = (w[j] >> 4) & 0x0f0f0f0fu;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                a0 = fmaf(ub(lo, i), x[4 * j + i], a0);
-                a1 = fmaf(ub(hi, i), x[16 + 4 * j + i], a1);
-            }
+            const f32x2 l0 = nib2<false>(lo), l1 = nib2<true>(lo);
+            const f32x2 h0 = nib2<false>(hi), h1 = nib2<true>(hi);
+            a0 = fmaf(l0.x, x[4 * j], a0);
+            a1 = fmaf(h0.x, x[16 + 4 * j], a1);
+            a0 = fmaf(l0.y, x[4 * j + 1], a0);
+            a1 = fmaf(h0.y, x[16 + 4 * j + 1], a1);
+            a0 = fmaf(l1.x, x[4 * j + 2], a0);
+            a1 = fmaf(h1.x, x[16 + 4 * j + 2], a1);
+            a0 = fmaf(l1.y, x[4 * j + 3], a0);
+            a1 = fmaf(h1.y, x[16 + 4 * j + 3], a1);
         }
         return a0 + a1;
     }
@@ -346,6 +377,19 @@ struct Tile<OCO_Q5_K> {
         r.hdr = lds_u128(blk);
         r.qh = lds_u128(blk + 16 + 16 * (c & 1));
         r.qs = lds_u128(blk + 48 + 16 * c);
+        return r;
+    }
+    // Piece c of the block at byte `off` straight from memory (176 is a
+    // multiple of 16).
+    static constexpr bool DIRECT = true;
+    __device__ __forceinline__ static Raw direct(__amdgpu_buffer_rsrc_t rs, uint32_t off, uint32_t c) {
+        Raw r;
+        const u32x4 h = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 2);
+        const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16 + 16 * (c & 1), 0, 2);
+        const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 48 + 16 * c, 0, 2);
+        r.hdr = make_uint4(h.x, h.y, h.z, h.w);
+        r.qh = make_uint4(b.x, b.y, b.z, b.w);
+        r.qs = make_uint4(q.x, q.y, q.z, q.w);
         return r;
     }
     __device__ __forceinline__ static float dot(const Raw &r, const float *x, const float *s, int c) {
