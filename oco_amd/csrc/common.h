@@ -109,6 +109,36 @@ struct WSrc {
     }
 };
 
+// Kernel arguments in preloaded SGPRs.  The command processor preloads the
+// leading scalar (and vector) kernel arguments into SGPRs when the code is
+// built with -amdgpu-kernarg-preload-count, but not a struct passed by
+// value, whose fields the waves then fetch from the kernarg segment before
+// anything that depends on them can start.  Kernels that take a parameter
+// struct therefore also take its first 56 bytes as four vector arguments
+// (KPRE_PARAMS), launched with KPRE_ARGS(s), and overwrite the struct's
+// head with them (kpre_apply), so the fields laid out first in each struct
+// are read from SGPRs.
+struct KPre {
+    u32x4 a, b, c;
+    u32x2 d;
+};
+constexpr size_t KPRE_BYTES = 56;
+template <class S>
+inline KPre kpre(const S &s) {
+    KPre k;
+    memset(&k, 0, sizeof k);
+    memcpy(&k, &s, sizeof(S) < KPRE_BYTES ? sizeof(S) : KPRE_BYTES);
+    return k;
+}
+template <class S>
+__device__ __forceinline__ void kpre_apply(S &s, u32x4 a, u32x4 b, u32x4 c, u32x2 d) {
+    const uint32_t w[14] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, c.x, c.y, c.z, c.w, d.x, d.y};
+    __builtin_memcpy(&s, w, sizeof(S) < KPRE_BYTES ? sizeof(S) : KPRE_BYTES);
+}
+#define KPRE_PARAMS u32x4 kpre_a, u32x4 kpre_b, u32x4 kpre_c, u32x2 kpre_d
+#define KPRE_APPLY(s) kpre_apply(s, kpre_a, kpre_b, kpre_c, kpre_d)
+#define KPRE_ARGS(s) kpre(s).a, kpre(s).b, kpre(s).c, kpre(s).d
+
 // E8M0 shared exponent: finite powers exact, 0 -> 2^-127, 255 -> NaN
 // (projections.metal:19-23).
 __device__ __forceinline__ float e8m0_scale(uint32_t e) {

@@ -23,19 +23,22 @@
 
 namespace oco {
 
+// The first 56 bytes arrive in SGPRs (KPre): what the tile choice and the
+// first weight loads depend on comes first.
 struct MoeArgs {
     const uint8_t *w[2];     // gated: {gate, up}; otherwise {down, unused}
-    const float *bias[2];    // per-matrix f32 biases [experts * n] or null
+    const float *logits;     // single token: select the experts in-kernel
+    const uint32_t *ids;     // [routes] expert per route (no plan, no logits)
+    const uint32_t *plan;    // route plan (tile = (expert, first row)) or null (tile = route)
+    uint32_t k, n, experts, topk;
     const void *x;           // activations
     uint32_t x_bf16;         // activation element type
     uint32_t input_div;      // route -> activation row: route / input_div
+    const float *bias[2];    // per-matrix f32 biases [experts * n] or null
     float *out0, *out1;      // gated: activation, up (may be null); otherwise y
-    const uint32_t *ids;     // [routes] expert per route (no plan, no logits)
-    const float *logits;     // single token: select the experts in-kernel
     uint32_t *ids_out;       // with logits: selected ids / probabilities
     float *probs_out;
-    const uint32_t *plan;    // route plan (tile = (expert, first row)) or null (tile = route)
-    uint32_t k, n, experts, topk, routes;
+    uint32_t routes;
     uint64_t row_bytes;
     uint32_t ngroups;
     uint32_t act, up_one;
@@ -59,8 +62,10 @@ __device__ __forceinline__ float activation(uint32_t act, float g, float u) {
 constexpr uint32_t PLAN_TILE = 16;  // routes per route-plan tile (its minimum, see oco_route_plan)
 
 template <int FMT, bool GATED, int T, int NPL>
-__global__ __launch_bounds__(256) void moe_kernel(MoeArgs a) {
+__global__ __launch_bounds__(256) void moe_kernel(KPRE_PARAMS, MoeArgs a) {
+    KPRE_APPLY(a);
     using Tl = Tile<FMT>;
+    a.row_bytes = (uint64_t)(a.k / Tl::BLOCK) * Tl::BYTES;
     constexpr int NM = GATED ? 2 : 1;             // matrices streamed together
     constexpr int LPR = (NPL * 32 * Tl::BYTES / Tl::P + 32 + 1023) / 1024;
     constexpr int TROWS = 2 * NM;                 // tile rows per wavefront (R = 1 per half)
@@ -261,7 +266,7 @@ __global__ __launch_bounds__(256) void moe_kernel(MoeArgs a) {
     }
 }
 
-typedef void (*MoeFn)(MoeArgs);
+typedef void (*MoeFn)(u32x4, u32x4, u32x4, u32x2, MoeArgs);
 constexpr int MOE_T = 4;  // routes per tile (plan tiles); one-route tiles without a plan use T = 1
 
 template <int FMT, bool GATED, int T>
@@ -332,7 +337,7 @@ static int moe_launch(uint32_t fmt, bool gated, MoeArgs a, uint32_t tiles, uint3
     const uint32_t target = per_cu * device_cus();
     uint32_t gx = std::max<uint32_t>(1, target / std::max<uint32_t>(1, parallel_tiles));
     gx = std::min(gx, a.ngroups);
-    hipLaunchKernelGGL(fn, dim3(gx, tiles), dim3(256), lds, stream, a);
+    hipLaunchKernelGGL(fn, dim3(gx, tiles), dim3(256), lds, stream, KPRE_ARGS(a), a);
     return launch_check("experts projection");
 }
 
@@ -465,8 +470,8 @@ static int experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype,
         g.m = routes;
         g.n = w->ffn;
         g.k = w->hidden;
-        g.row_bytes = oco_row_bytes(w->format, w->hidden);
-        g.expert_bytes = g.row_bytes * w->ffn;
+        g.row_bytes = (uint32_t)oco_row_bytes(w->format, w->hidden);
+        g.expert_bytes = (uint64_t)g.row_bytes * w->ffn;
         g.plan = plan;
         g.routes = routes;
         g.experts = w->experts;
@@ -484,8 +489,8 @@ static int experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype,
         d.y_bf16 = routed ? 0 : 1;
         d.n = w->hidden;
         d.k = w->ffn;
-        d.row_bytes = oco_row_bytes(w->format, w->ffn);
-        d.expert_bytes = d.row_bytes * w->hidden;
+        d.row_bytes = (uint32_t)oco_row_bytes(w->format, w->ffn);
+        d.expert_bytes = (uint64_t)d.row_bytes * w->hidden;
         OCO_TRY(mx_experts_launch(MM_DOWN, d, arec, 3, tile_rows, s));
         return oco_moe_sum(down, routed ? OCO_DT_F32 : OCO_DT_BF16, probs, out, w->hidden, tokens, w->k, stream);
     }
@@ -519,8 +524,8 @@ static int experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype,
         g.m = routes;
         g.n = w->ffn;
         g.k = w->hidden;
-        g.row_bytes = oco_row_bytes(w->format, w->hidden);
-        g.expert_bytes = g.row_bytes * w->ffn;
+        g.row_bytes = (uint32_t)oco_row_bytes(w->format, w->hidden);
+        g.expert_bytes = (uint64_t)g.row_bytes * w->ffn;
         g.plan = plan;
         g.routes = routes;
         g.experts = w->experts;
@@ -548,8 +553,8 @@ static int experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype,
         d.y_bf16 = routed ? 0 : 1;
         d.n = w->hidden;
         d.k = w->ffn;
-        d.row_bytes = oco_row_bytes(w->format, w->ffn);
-        d.expert_bytes = d.row_bytes * w->hidden;
+        d.row_bytes = (uint32_t)oco_row_bytes(w->format, w->ffn);
+        d.expert_bytes = (uint64_t)d.row_bytes * w->hidden;
         OCO_TRY(q4 ? moe_q4k_launch(MM_DOWN, d, bm, s) : grouped_matmul_launch(MM_DOWN, w->format, d, bm, s));
         return oco_moe_sum(down, routed ? OCO_DT_F32 : OCO_DT_BF16, probs, out, w->hidden, tokens, w->k, stream);
     }

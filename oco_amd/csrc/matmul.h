@@ -5,20 +5,23 @@
 
 namespace oco {
 
+// The first 56 bytes arrive in SGPRs (KPre): the fields the tiles' first
+// loads depend on come first.
 struct MatmulArgs {
+    const uint32_t *plan;  // grouped (routed-expert) mode: route plan with tile_rows = BM
     const uint8_t *w;
-    const void *x;
+    const uint8_t *w2;     // up weights (gate/up mode)
+    const void *x;         // activations (MXFP4 expert tiles: their E4M3 split records)
+    uint32_t n, k;
+    uint32_t row_bytes;    // bytes of one weight row (< 4 GiB)
+    uint32_t routes, experts, topk;
+    uint64_t expert_bytes; // bytes of one expert's matrix
     void *y;
     const float *bias;
-    uint32_t m, n, k;
-    uint64_t row_bytes;
+    uint32_t m;
     uint32_t x_f16, y_bf16;
-    // Grouped (routed-expert) mode: tiles come from a route plan.
-    const uint32_t *plan;  // route plan with tile_rows = BM
-    const uint8_t *w2;     // up weights (gate/up mode)
     const float *bias2;    // up bias (gate/up mode)
-    uint64_t expert_bytes; // bytes of one expert's matrix
-    uint32_t routes, experts, topk, act, up_one;
+    uint32_t act, up_one;
     uint32_t *rowmax;      // [routes] max |activation| bits per expert-sorted row (gate/up writes, down reads)
     uint8_t *yrec;         // MXFP4 gate/up: the activations' E4M3 split records in place of f32 rows (or null)
 };

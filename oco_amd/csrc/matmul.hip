@@ -213,7 +213,8 @@ struct Stage {
 // BN/2 gate and the same BN/2 up rows, placed so each wavefront holds a gate
 // column and its up column in the same lane: the activation is fused.
 template <int FMT, bool BF, int BM, int BN, int G = MM_DENSE>
-__global__ __launch_bounds__(256) void matmul_kernel(MatmulArgs a) {
+__global__ __launch_bounds__(256) void matmul_kernel(KPRE_PARAMS, MatmulArgs a) {
+    KPRE_APPLY(a);
     using PP = PrefillPiece<FMT, BF>;
     using ST = Stage<FMT, BF, BM, BN>;
     constexpr int BK = 128, LD = BK + 8;  // LDS row stride: 136 halves (272 bytes, conflict-free fragments)
@@ -476,7 +477,7 @@ __global__ __launch_bounds__(256) void matmul_kernel(MatmulArgs a) {
         }
 }
 
-typedef void (*MatmulFn)(MatmulArgs);
+typedef void (*MatmulFn)(u32x4, u32x4, u32x4, u32x2, MatmulArgs);
 
 template <int BM, int BN>
 static MatmulFn matmul_pick_tile(uint32_t fmt) {
@@ -537,7 +538,7 @@ int grouped_matmul_launch(int mode, uint32_t fmt, const MatmulArgs &a, uint32_t 
     if (lds > 64 * 1024)
         OCO_TRY(hip_check(hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
                           "hipFuncSetAttribute"));
-    hipLaunchKernelGGL(fn, grid, dim3(256), lds, stream, a);
+    hipLaunchKernelGGL(fn, grid, dim3(256), lds, stream, KPRE_ARGS(a), a);
     return launch_check("experts grouped matmul");
 }
 
@@ -584,7 +585,7 @@ static int matmul_decode_launch(uint32_t format, const void *w, const void *x, o
     a.m = p->m;
     a.n = p->n;
     a.k = p->k;
-    a.row_bytes = oco_row_bytes(format, p->k);
+    a.row_bytes = (uint32_t)oco_row_bytes(format, p->k);
     a.x_f16 = x_dtype == OCO_DT_F16;
     a.y_bf16 = y_dtype == OCO_DT_BF16;
     dim3 grid((p->n + bn - 1) / bn, (p->m + bm - 1) / bm);
@@ -592,7 +593,7 @@ static int matmul_decode_launch(uint32_t format, const void *w, const void *x, o
     if (lds > 64 * 1024)
         OCO_TRY(hip_check(hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
                           "hipFuncSetAttribute"));
-    hipLaunchKernelGGL(fn, grid, dim3(256), lds, stream, a);
+    hipLaunchKernelGGL(fn, grid, dim3(256), lds, stream, KPRE_ARGS(a), a);
     return launch_check("oco_matmul");
 }
 

@@ -171,7 +171,8 @@ __device__ __forceinline__ void q4_load_lds16(const void *src, void *lds) {
 
 
 template <int G, int MI, int NW>
-__global__ __launch_bounds__(64 * NW) void moe_q4k_kernel(MatmulArgs a, uint32_t chunks) {
+__global__ __launch_bounds__(64 * NW) void moe_q4k_kernel(KPRE_PARAMS, MatmulArgs a, uint32_t chunks) {
+    KPRE_APPLY(a);
     constexpr int ROWS = 16 * MI;
     constexpr int XL = ROWS / (2 * NW);  // activation loads per lane per step (16 bytes each)
     constexpr int STAGE = ROWS * 512;    // one super-block of f16 rows
@@ -481,7 +482,7 @@ static int q4_launch(const MatmulArgs &a, uint32_t bm, hipStream_t stream) {
     uint64_t grid = std::min<uint64_t>(max_units, (uint64_t)per_cu * cus);
     grid = std::max<uint64_t>(grid, (max_units + span - 1) / span);
     if (grid > 0x7fffffffu) return fail(OCO_ERR_INVALID, "experts: Q4_K grid of %llu units", (unsigned long long)max_units);
-    hipLaunchKernelGGL((moe_q4k_kernel<G, MI, Q4_NW>), dim3((unsigned)grid), dim3(64 * Q4_NW), 0, stream, a, chunks);
+    hipLaunchKernelGGL((moe_q4k_kernel<G, MI, Q4_NW>), dim3((unsigned)grid), dim3(64 * Q4_NW), 0, stream, KPRE_ARGS(a), a, chunks);
     return OCO_OK;
 }
 

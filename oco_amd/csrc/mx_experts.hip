@@ -36,7 +36,10 @@ uint64_t mx_rows_bytes(uint32_t rows, uint32_t k, int terms) {
 // top of the next quad, so one vmcnt(0) and two barriers per quad order
 // everything.
 template <int G, int NW, int TERMS, int TR, int KS>
-__global__ __launch_bounds__(64 * NW) void mx_experts_kernel(MatmulArgs a, const uint8_t *xrec) {
+__global__ __launch_bounds__(64 * NW) void mx_experts_kernel(KPRE_PARAMS, MatmulArgs a) {
+    KPRE_APPLY(a);
+    const uint8_t *xrec = reinterpret_cast<const uint8_t *>(a.x);
+    const uint64_t expert_bytes = (uint64_t)a.n * a.row_bytes;
     constexpr int NT = 1;                          // weight tiles per wavefront
     constexpr int WROWS = 32 * NT;                 // weight rows per wavefront
     constexpr int WLD = WROWS * 10 / 64;           // 16-byte loads per lane per quad (10 per row)
@@ -106,9 +109,9 @@ __global__ __launch_bounds__(64 * NW) void mx_experts_kernel(MatmulArgs a, const
     uint32_t rsh[NT];
 #pragma unroll
     for (int j = 0; j < NT; j++) {
-        const uint8_t *eb = (upw ? a.w2 : a.w) + expert * a.expert_bytes;
+        const uint8_t *eb = (upw ? a.w2 : a.w) + expert * expert_bytes;
         rsh[j] = (uint32_t)(uintptr_t)eb & 15u;
-        const uint64_t span = (a.expert_bytes + rsh[j] + 160 + 15) & ~15ull;
+        const uint64_t span = (expert_bytes + rsh[j] + 160 + 15) & ~15ull;
         rw[j] = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(eb - rsh[j]), 0,
                                                   (uint32_t)std::min<uint64_t>(span, 0xffffffffull), 0x00020000);
     }
@@ -283,7 +286,9 @@ static int mx_experts_go(const MatmulArgs &a, const uint8_t *xrec, hipStream_t s
                       "hipFuncSetAttribute"));
     const uint32_t cols = 32 * (G == MM_GATE_UP ? MXE_NW / 2 : MXE_NW) / KS;
     const dim3 grid((a.n + cols - 1) / cols, (a.routes + TR - 1) / TR + a.experts);
-    hipLaunchKernelGGL(fn, grid, dim3(64 * MXE_NW), lds, stream, a, xrec);
+    MatmulArgs b = a;
+    b.x = xrec;
+    hipLaunchKernelGGL(fn, grid, dim3(64 * MXE_NW), lds, stream, KPRE_ARGS(b), b);
     return OCO_OK;
 }
 

@@ -70,7 +70,8 @@ __device__ __forceinline__ int mx_scale_exp(float amax) {
 // (term, block) interleaves groups p and p + 2 (byte 2i: value 8p + i,
 // byte 2i + 1: value 8p + 16 + i), so partner lanes q and q ^ 2 swap their
 // codes and each stores 8 of the chunk's 16 bytes.
-__global__ __launch_bounds__(256) void mx_split_kernel(MxSplitArgs a) {
+__global__ __launch_bounds__(256) void mx_split_kernel(KPRE_PARAMS, MxSplitArgs a) {
+    KPRE_APPLY(a);
     const uint32_t rec = blockIdx.x;
     const uint32_t tile = rec / a.ksteps, s = rec % a.ksteps;
     const int tid = threadIdx.x, q = tid & 3, pair = tid >> 2, r = pair & 31, blk = pair >> 5;
@@ -126,15 +127,16 @@ __global__ __launch_bounds__(256) void mx_split_kernel(MxSplitArgs a) {
     if (q == 0) *reinterpret_cast<uint32_t *>(out + MX_DATA + (r + 32 * blk) * 4) = scales;
 }
 
+// The first 56 bytes arrive in SGPRs (KPre).
 struct MxArgs {
     const uint8_t *w;
     const uint8_t *frag;
+    uint32_t m, n, k, ksteps, tiles;
+    uint32_t row_bytes;
+    uint32_t wspan;  // weight bytes from the dword-aligned base, rounded up to 4 (< 4 GiB)
+    uint32_t y_bf16;
     void *y;
     const float *bias;
-    uint32_t m, n, k, ksteps, tiles;
-    uint64_t row_bytes;
-    uint32_t y_bf16;
-    uint32_t wspan;  // weight bytes from the dword-aligned base, rounded up to 4 (< 4 GiB)
 };
 
 template <int I>
@@ -149,7 +151,7 @@ __device__ __forceinline__ void static_for(F &&f) {
     }
 }
 
-typedef void (*MxFn)(MxArgs);
+typedef void (*MxFn)(u32x4, u32x4, u32x4, u32x2, MxArgs);
 
 // A buffer resource the compiler keeps in SGPRs: every field goes through
 // readfirstlane (the values are uniform; without this a resource built next
@@ -194,7 +196,8 @@ struct MxPlan {
 };
 
 template <int WM, int CTW, int RB>
-__global__ __launch_bounds__(256) void mx_matmul_kernel(MxArgs a) {
+__global__ __launch_bounds__(256) void mx_matmul_kernel(KPRE_PARAMS, MxArgs a) {
+    KPRE_APPLY(a);
     using P = MxPlan<WM, CTW, RB>;
     constexpr int BN = P::BN, BU = P::BU, STAGE = P::STAGE, RA = P::RA, CT = CTW;
     constexpr int PER = RB;  // double steps per unrolled round: RB, 3 stages and RA / 2 all divide it
@@ -421,7 +424,7 @@ int mx_matmul_launch(const void *w, const void *x, void *y, bool y_bf16, const f
     sa.k = k;
     sa.ksteps = ksteps;
     sa.records = tiles * ksteps;
-    hipLaunchKernelGGL(mx_split_kernel, dim3(sa.records), dim3(256), 0, stream, sa);
+    hipLaunchKernelGGL(mx_split_kernel, dim3(sa.records), dim3(256), 0, stream, KPRE_ARGS(sa), sa);
     OCO_TRY(launch_check("oco_matmul (mx split)"));
     size_t lds = 0;
     MxFn fn = plan.wm == 2 ? (plan.ctw == 3 ? mx_kernel_fn<2, 3>(lds) : mx_kernel_fn<2, 6>(lds))
@@ -439,14 +442,14 @@ int mx_matmul_launch(const void *w, const void *x, void *y, bool y_bf16, const f
     a.k = k;
     a.ksteps = ksteps;
     a.tiles = tiles;
-    a.row_bytes = (uint64_t)(k / 32) * 17;
+    a.row_bytes = (k / 32) * 17;
     a.y_bf16 = y_bf16;
     const uint64_t wspan = ((uint64_t)n * a.row_bytes + ((uintptr_t)w & 3u) + 3) & ~3ull;
     if (wspan > 0xffffff00ull)
         return fail(OCO_ERR_UNSUPPORTED, "oco_matmul: MXFP4 weight of %llu bytes (4 GiB limit)",
                     (unsigned long long)wspan);
     a.wspan = (uint32_t)wspan;
-    hipLaunchKernelGGL(fn, dim3(plan.col_tiles, plan.groups), dim3(256), lds, stream, a);
+    hipLaunchKernelGGL(fn, dim3(plan.col_tiles, plan.groups), dim3(256), lds, stream, KPRE_ARGS(a), a);
     return launch_check("oco_matmul (mx)");
 }
 
