@@ -403,8 +403,9 @@ uint64_t oco_experts_workspace(const oco_experts *w, uint32_t tokens) {
     uint64_t bytes = align256(oco_route_plan_words((uint32_t)routes, w->experts) * 4) + align256(routes * w->ffn * 4) +
                      align256((uint64_t)tokens * w->hidden * 2) + align256(routes * 4) + align256(routes * w->hidden * 4);
     if (w->format == OCO_Q4_K) bytes += align256(routes * w->ffn * 2);
-    if (w->format == OCO_MXFP4)
-        bytes += align256(mx_rows_bytes(tokens, w->hidden, 3)) + align256(mx_rows_bytes((uint32_t)routes, w->ffn, 3));
+    if (w->format == OCO_MXFP4)  // ... and the plan's tile descriptors (tiles of up to 32 rows)
+        bytes += align256(mx_rows_bytes(tokens, w->hidden, 3)) + align256(mx_rows_bytes((uint32_t)routes, w->ffn, 3)) +
+                 align256(plan_desc_words((uint32_t)routes, w->experts, 32) * 4);
     // router logits of oco_experts_forward, last
     return bytes + align256((uint64_t)tokens * w->experts * 4);
 }
@@ -413,7 +414,8 @@ uint64_t oco_experts_workspace(const oco_experts *w, uint32_t tokens) {
 
 // The layer after the router logits.  With `logits`, the experts are
 // selected on the device (ids/probs are written): at one token inside the
-// routed gate/up kernel (expert_expand's selection), else by route_select.
+// routed gate/up kernel (expert_expand's selection), else inside the route
+// plan's launch.
 static int experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype, uint32_t *ids, float *probs,
                          const float *logits, uint32_t tokens, uint16_t *out, float *routed, void *workspace,
                          uint64_t workspace_bytes, hipStream_t s, const char *who) {
@@ -426,9 +428,21 @@ static int experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype,
         return fail(OCO_ERR_INVALID, "%s: workspace of %llu bytes, need %llu", who,
                     (unsigned long long)workspace_bytes, (unsigned long long)oco_experts_workspace(w, tokens));
     oco_stream stream = (oco_stream)s;
-    // Selection inside the gate/up kernel covers one token over <= 64 experts.
+    // Selection inside the gate/up kernel covers one token over <= 64 experts;
+    // otherwise it runs in the route plan's workgroup, before the plan.
     const bool fused_select = logits && tokens == 1 && w->experts <= 64;
+    PlanSide sel = {};
+#if defined(OCO_ABL) && OCO_ABL == 4
     if (logits && !fused_select) OCO_TRY(oco_route_select(logits, tokens, w->experts, w->k, ids, probs, stream));
+#else
+    if (logits && !fused_select) {
+        sel.logits = logits;
+        sel.tokens = tokens;
+        sel.topk = w->k;
+        sel.ids_out = ids;
+        sel.probs_out = probs;
+    }
+#endif
     const uint32_t routes = tokens * w->k;
     uint8_t *ws = (uint8_t *)workspace;
     uint32_t *plan = (uint32_t *)ws;
@@ -454,7 +468,9 @@ static int experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype,
         // The input rows' split runs beside the plan; the activations are
         // split by the gate/up tiles themselves.
         const int xterms = x_dtype == OCO_DT_BF16 ? 2 : 3;  // bf16 rows are exact in two terms
-        PlanSide side = {};
+        uint32_t *desc = (uint32_t *)(arec + align256(mx_rows_bytes(routes, w->ffn, 3)));
+        PlanSide side = sel;
+        side.desc = desc;
         side.x = x;
         side.x_bf16 = x_dtype == OCO_DT_BF16 ? 1u : 0u;
         side.rec = xrec;
@@ -462,6 +478,7 @@ static int experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype,
         side.k = w->hidden;
         OCO_TRY(route_plan_launch(ids, routes, w->experts, tile_rows, 0, 0, plan, &side, s));
         MatmulArgs g = {};
+        g.desc = desc;
         g.w = (const uint8_t *)w->gate;
         g.w2 = (const uint8_t *)w->up;
         g.bias = w->gate_bias;
@@ -509,7 +526,13 @@ static int experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype,
                                : (mean <= 40 ? 32 : 64);
         // The tiles take f16 rows (the reference's half(x)); the conversion
         // and the clearing of the row maxima run beside the plan.
-        const PlanSide side = {x, x_dtype == OCO_DT_BF16 ? 1u : 0u, x16, (uint64_t)tokens * w->hidden, rowmax, routes};
+        PlanSide side = sel;
+        side.x = x;
+        side.x_bf16 = x_dtype == OCO_DT_BF16 ? 1u : 0u;
+        side.y = x16;
+        side.n = (uint64_t)tokens * w->hidden;
+        side.zero = rowmax;
+        side.nzero = routes;
         OCO_TRY(route_plan_launch(ids, routes, w->experts, bm, 0, 0, plan, &side, s));
         const void *xin = x16;
         MatmulArgs g = {};
@@ -603,7 +626,7 @@ static int experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype,
         return oco_moe_sum(down, OCO_DT_F32, probs, out, w->hidden, tokens, w->k, stream);
     }
     if (tokens > 1) {
-        OCO_TRY(oco_route_plan(ids, routes, w->experts, PLAN_TILE, 0, 0, plan, stream));
+        OCO_TRY(route_plan_launch(ids, routes, w->experts, PLAN_TILE, 0, 0, plan, &sel, s));
         use_plan = plan;
         tiles = ((routes + PLAN_TILE - 1) / PLAN_TILE + w->experts) * (PLAN_TILE / MOE_T);
         parallel = std::min(routes, w->experts);

@@ -8,6 +8,7 @@ namespace oco {
 // The first 56 bytes arrive in SGPRs (KPre): the fields the tiles' first
 // loads depend on come first.
 struct MatmulArgs {
+    const uint32_t *desc;  // MXFP4 expert tiles: the route plan's tile descriptors (route.h)
     const uint32_t *plan;  // grouped (routed-expert) mode: route plan with tile_rows = BM
     const uint8_t *w;
     const uint8_t *w2;     // up weights (gate/up mode)

@@ -9,6 +9,7 @@
 // Activations come split per row into TERMS E4M3 terms (mxsplit.h).
 #include "matmul.h"
 #include "mxsplit.h"
+#include "route.h"
 #include "stream.h"
 
 namespace oco {
@@ -54,16 +55,18 @@ __global__ __launch_bounds__(64 * NW) void mx_experts_kernel(KPRE_PARAMS, Matmul
     static_assert((KS - 1) * (NW / KS) * 16 * 64 * 4 <= KS * TR * AROW, "the K-part sums fit the record region");
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, c = lane & 31, part = lane >> 5;
     const int kh = wave / WPK, wsub = wave % WPK;  // K part, wavefront within it
+    // The plan's tile count (word 1) spreads exactly the used tiles evenly
+    // over the XCDs, each XCD a contiguous range of them (tile-major); then
+    // the tile's descriptor: expert, rows, first sorted row, its route ids.
     const uint32_t used = gridDim.x * min(a.plan[1], gridDim.y);
     const uint32_t lin = xcd_order(blockIdx.x + gridDim.x * blockIdx.y, used);
     if (lin >= used) return;  // uniform: a surplus workgroup
     const uint32_t bx = lin % gridDim.x, y = lin / gridDim.x;
-    const uint32_t expert = a.plan[6 + 2 * y], first = a.plan[7 + 2 * y];
-    const uint64_t grouped = 6 + 2 * ((uint64_t)(a.routes + 15) / 16 + a.experts);
-    const uint64_t list = grouped + (uint64_t)expert * (a.routes + 1);
-    const uint64_t sorted = grouped + (uint64_t)a.experts * (a.routes + 1);
-    const uint32_t rows = min((uint32_t)TR, a.plan[list] - first);
-    const uint32_t sorted0 = a.plan[sorted + expert] + first;
+    const uint32_t *dsc = a.desc + (uint64_t)y * (PLAN_DESC_HEAD + TR);
+    const uint4 head = *reinterpret_cast<const uint4 *>(dsc);
+    const uint32_t *rid = dsc + PLAN_DESC_HEAD;
+    const uint32_t expert = head.x, rows = head.y, sorted0 = head.z;
+    if (rows == 0) return;  // uniform: an unused tile slot
     // Wavefronts past the last column still load (clamped rows) and join the
     // barriers; they store nothing.
     const bool upw = G == MM_GATE_UP && wsub >= CT;  // an up wavefront
@@ -90,7 +93,7 @@ __global__ __launch_bounds__(64 * NW) void mx_experts_kernel(KPRE_PARAMS, Matmul
         const uint32_t p = threadIdx.x + 64 * NW * i, kp = min(p / (rows * APR), KS - 1u), pr = p - kp * rows * APR;
         const uint32_t r = min(pr / APR, TR - 1u), q16 = pr % APR;
         uint32_t xrow = 0;
-        if (p < pieces) xrow = G == MM_GATE_UP ? a.plan[list + 1 + first + r] / a.topk : sorted0 + r;
+        if (p < pieces) xrow = G == MM_GATE_UP ? rid[r] / a.topk : sorted0 + r;
         asrc[i] = xrow * ksteps * AREC + kp * qpart * 4 * AREC + 16 * q16;
         adst[i] = (kp * TR + r) * AROW + 16 * q16;
     }
@@ -140,7 +143,11 @@ __global__ __launch_bounds__(64 * NW) void mx_experts_kernel(KPRE_PARAMS, Matmul
         const uint32_t qg = q0 + q, sw = 136 * qg - 8 * (qg & 1), sa = 4 * q * AREC;  // q: this part's quad
 #pragma unroll
         for (int i = 0; i < WLD; i++)
+#if defined(OCO_ABL) && OCO_ABL == 2
+            wreg[i] = u32x4{boff[i][par], sw, (uint32_t)i, 7u};
+#else
             wreg[i] = __builtin_amdgcn_raw_buffer_load_b128(rw[(lane + 64 * i) / 10 / 32], boff[i][par], sw, 0);
+#endif
 #pragma unroll
         for (int i = 0; i < ALD; i++)
             if (threadIdx.x + 64 * NW * i < pieces) areg[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, asrc[i], sa, 0);
@@ -183,6 +190,10 @@ __global__ __launch_bounds__(64 * NW) void mx_experts_kernel(KPRE_PARAMS, Matmul
                 const mxe_i32x8 bv =
                     live ? mxe_i32x8{(int)qd[0], (int)qd[1], (int)qd[2], (int)qd[3], 0, 0, 0, 0} : mxe_i32x8{};
                 const int sb = live ? (int)wlds[pay - 1] : 127;
+#if defined(OCO_ABL) && OCO_ABL == 1
+                acc[j][0] += __int_as_float(bv[0] ^ bv[3] ^ sb ^ (int)sa ^ (int)av[0][0].x ^ (int)av[TERMS - 1][1].w);
+                continue;
+#endif
 #pragma unroll
                 for (int t = 0; t < TERMS; t++) {
                     const mxe_i32x8 avt{(int)av[t][0].x, (int)av[t][0].y, (int)av[t][0].z, (int)av[t][0].w,
@@ -266,7 +277,7 @@ __global__ __launch_bounds__(64 * NW) void mx_experts_kernel(KPRE_PARAMS, Matmul
             const uint32_t r = 8 * (v / 4) + 4 * part + (v % 4);
             if (r >= rows) continue;
             const float val = acc[0][v] + b;
-            const uint64_t o = (uint64_t)a.plan[list + 1 + first + r] * a.n + col;
+            const uint64_t o = (uint64_t)rid[r] * a.n + col;
             if (a.y_bf16)
                 reinterpret_cast<uint16_t *>(a.y)[o] = f32_to_bf16_bits(val);
             else

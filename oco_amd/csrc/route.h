@@ -9,6 +9,15 @@ namespace oco {
 // elements per thread, and `nzero` words of `zero` cleared; or, with `rec`
 // set, the rows' E4M3 split records (mxsplit.h: bf16 rows in two terms, f32
 // rows in three) in place of the f16 copy.
+//
+// Also optional, in the plan's own workgroup: the expert selection itself
+// (`logits` set: top-`topk` of each of `tokens` rows of `experts` logits, as
+// oco_route_select, into ids_out / probs_out, which then are the plan's ids),
+// and per-tile descriptors (`desc` set), so that a tile's consumer finds all
+// it needs in one contiguous read: PLAN_DESC_HEAD words {expert, rows (0 for
+// an unused tile slot), first sorted row, first list row} then the tile's
+// `tile_rows` route ids in list order, for every one of the plan's
+// ceil(routes / 16) + experts tile slots.
 struct PlanSide {
     const void *x;
     uint32_t x_bf16;
@@ -18,7 +27,16 @@ struct PlanSide {
     uint32_t nzero;
     uint8_t *rec;       // split records of rows x k (k % 32 == 0), or null
     uint32_t rows, k;
+    const float *logits;
+    uint32_t tokens, topk;
+    uint32_t *ids_out;
+    float *probs_out;
+    uint32_t *desc;
 };
+constexpr uint32_t PLAN_DESC_HEAD = 4;
+__host__ __device__ inline uint64_t plan_desc_words(uint32_t routes, uint32_t experts, uint32_t tile_rows) {
+    return ((uint64_t)(routes + 15) / 16 + experts) * (PLAN_DESC_HEAD + tile_rows);
+}
 
 // oco_route_plan with an optional side job (null: none).
 // Router logits [tokens, experts] (routing.metal:96-146) into `logits`.

@@ -150,6 +150,25 @@ __global__ __launch_bounds__(PLAN_THREADS) void route_plan_kernel(const uint32_t
         }
         return;
     }
+    // The expert selection first, a token per wavefront; the plan then reads
+    // the selected ids back (written and read by this workgroup only).
+    if (side.logits) {
+        const uint32_t wave0 = threadIdx.x >> 6;
+        for (uint32_t t = wave0; t < side.tokens; t += PLAN_THREADS / 64) {
+            const float *lt = side.logits + (uint64_t)t * experts;
+            uint32_t *it = side.ids_out + (uint64_t)t * side.topk;
+            float *pt = side.probs_out + (uint64_t)t * side.topk;
+            if (experts <= 64)
+                select_topk<1>(lt, experts, side.topk, it, pt);
+            else if (experts <= 128)
+                select_topk<2>(lt, experts, side.topk, it, pt);
+            else
+                select_topk<4>(lt, experts, side.topk, it, pt);
+        }
+        __threadfence_block();
+        __syncthreads();
+        ids = side.ids_out;
+    }
     // LDS: chunk ids [1024]; run, tile base, offset [experts]; per-wavefront
     // histograms [16][experts] (experts <= PLAN_HIST_EXPERTS)
     extern __shared__ __attribute__((aligned(16))) uint32_t sh[];
@@ -281,12 +300,26 @@ __global__ __launch_bounds__(PLAN_THREADS) void route_plan_kernel(const uint32_t
         plan[5] = 1;
     }
     __syncthreads();
+    const uint32_t DW = PLAN_DESC_HEAD + tile_rows;  // descriptor words per tile
     for (uint32_t e = tid; e < experts; e += PLAN_THREADS) {
         uint32_t t = tbase[e];
         for (uint32_t b = 0; b < run[e]; b += tile_rows, t++) {
             plan[6 + 2 * (uint64_t)t] = e;
             plan[6 + 2 * (uint64_t)t + 1] = b;
+            if (side.desc) {
+                uint32_t *d = side.desc + (uint64_t)t * DW;
+                d[0] = e;
+                d[1] = min(tile_rows, run[e] - b);
+                d[2] = offs[e] + b;
+                d[3] = b;
+            }
         }
+    }
+    if (side.desc) {  // unused tile slots: no rows
+        const uint32_t slots = (routes + 15) / 16 + experts;
+        uint32_t total = 0;  // tiles in use: the per-wavefront tile sums of step 2
+        for (uint32_t w = 0; w < 16; w++) total += wsum[16 + w];
+        for (uint32_t t = total + tid; t < slots; t += PLAN_THREADS) side.desc[(uint64_t)t * DW + 1] = 0;
     }
     if (one_pass) {
         __syncthreads();  // offs[] is complete
@@ -298,6 +331,8 @@ __global__ __launch_bounds__(PLAN_THREADS) void route_plan_kernel(const uint32_t
                 const uint32_t pos = hist[(c * 16 + wave) * experts + e] + rk[c];
                 plan[grouped + (uint64_t)e * (routes + 1) + 1 + pos] = i;
                 plan[sorted + experts + i] = offs[e] + pos;
+                if (side.desc)
+                    side.desc[(uint64_t)(tbase[e] + pos / tile_rows) * DW + PLAN_DESC_HEAD + pos % tile_rows] = i;
             }
         }
         return;
@@ -351,6 +386,8 @@ __global__ __launch_bounds__(PLAN_THREADS) void route_plan_kernel(const uint32_t
         if (e < experts) {
             plan[grouped + (uint64_t)e * (routes + 1) + 1 + pos] = i;
             plan[sorted + experts + i] = offs[e] + pos;
+            if (side.desc)
+                side.desc[(uint64_t)(tbase[e] + pos / tile_rows) * DW + PLAN_DESC_HEAD + pos % tile_rows] = i;
             atomicAdd(&run[e], 1u);
         }
         __syncthreads();
