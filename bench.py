@@ -88,6 +88,32 @@ class Matvec(Workload):
         return float(self.bytes)
 
 
+class ReadFloor(Workload):
+    """The plain HBM read stream the decode matvec is bounded by: the XOR of
+    every word of the headline's 8,812,800 weight bytes (oco_buffer_xor32,
+    four 16-byte nontemporal loads in flight per thread), over the same
+    rotated copies.  Work = bytes read."""
+    name = "read_floor_8812800"
+
+    def setup(self, oco, stream):
+        from oco_amd import synth
+        self.oco, self.stream = oco, stream
+        data = synth.weights(39, 5760, 2880, 1)
+        self.bytes = data.nbytes
+        self.copies = max(1, math.ceil(ROTATE_BYTES / self.bytes))
+        self.stride = (self.bytes + 255) // 256 * 256
+        self.w = oco.DeviceBuffer(self.stride * self.copies)
+        for c in range(self.copies):
+            self.w.upload(data, c * self.stride)
+        self.out = oco.DeviceBuffer(4096)
+
+    def launch(self, i):
+        self.w.xor32(self.out, stream=self.stream, offset=(i % self.copies) * self.stride, nbytes=self.bytes)
+
+    def work_per_step(self):
+        return float(self.bytes)
+
+
 class MatvecStack(Workload):
     """Qwen3-8B-shaped decode stack: ffn_up/gate Q4_K, ffn_down Q6_K, lm_head Q6_K."""
     name = "qwen3_8b_q4km_decode_stack"
@@ -367,6 +393,7 @@ WORKLOADS = {
     "q4_1_matvec_4096x4096": lambda: Matvec("q4_1_matvec_4096x4096", 3, 4096, 4096),
     "q5_k_matvec_12288x4096": lambda: Matvec("q5_k_matvec_12288x4096", 13, 12288, 4096),
     "qwen3_8b_q4km_decode_stack": MatvecStack,
+    "read_floor_8812800": ReadFloor,
     "moe_decode_gpt_oss_b1": lambda: MoeDecode(1),
     "moe_decode_gpt_oss_b4": lambda: MoeDecode(4),
     "moe_decode_gpt_oss_b16": lambda: MoeDecode(16),
@@ -525,7 +552,7 @@ def main():
                      "q6_k_lm_head_151936x4096", "qwen3_8b_q4km_decode_stack", "moe_decode_gpt_oss_b1",
                      "moe_decode_gpt_oss_b4", "moe_decode_gpt_oss_b16", "prefill_mxfp4_5760x2880_m512",
                      "moe_prefill_qwen3_30b_a3b", "lm_head_argmax_qwen3_8b", "argmax_f32_151936",
-                     "norm_up_gate_qwen3_8b_fused", "norm_up_gate_qwen3_8b_unfused"]:
+                     "norm_up_gate_qwen3_8b_fused", "norm_up_gate_qwen3_8b_unfused", "read_floor_8812800"]:
             if name == wl.name:
                 continue
             w2 = WORKLOADS[name]()

@@ -133,6 +133,16 @@ int oco_buffer_copy(void *dst, const void *src, size_t bytes, oco_stream stream)
  * dispatch_tests.rs:12-13); safe inside captured graphs. */
 int oco_buffer_fill32(void *dst, uint32_t pattern, size_t words, oco_stream stream);
 
+/* XOR of `words` 32-bit words at src (16-byte aligned, words a multiple of
+ * 4, under 4 GiB) into OCO_XOR32_SLOTS words of device memory at out: the
+ * XOR of out[0 .. OCO_XOR32_SLOTS - 1] is the XOR of the words (each
+ * workgroup stores its share; all slots are written).  No
+ * counterpart in the reference: an integrity check of weights made
+ * resident, and the plain HBM read stream the matvec kernels are compared
+ * against (the bench's read-floor workload). */
+#define OCO_XOR32_SLOTS 1024u
+int oco_buffer_xor32(const void *src, size_t words, uint32_t *out, oco_stream stream);
+
 /* One queue per session (src/weights/compute.rs:36-55). */
 int oco_stream_create(oco_stream *out);
 int oco_stream_sync(oco_stream stream);

@@ -141,6 +141,7 @@ SIGNATURES = {
     "oco_buffer_download": (_i32, [_vp, _vp, _sz]),
     "oco_buffer_copy": (_i32, [_vp, _vp, _sz, _vp]),
     "oco_buffer_fill32": (_i32, [_vp, _u32, _sz, _vp]),
+    "oco_buffer_xor32": (_i32, [_vp, _sz, _vp, _vp]),
     "oco_stream_create": (_i32, [ctypes.POINTER(_vp)]),
     "oco_stream_sync": (_i32, [_vp]),
     "oco_stream_destroy": (_i32, [_vp]),
@@ -361,6 +362,11 @@ class DeviceBuffer:
     def fill32(self, pattern: int, stream=None):
         _check(load_library().oco_buffer_fill32(self.ptr, pattern & 0xFFFFFFFF, self.nbytes // 4,
                                                 _stream(stream)))
+
+    def xor32(self, out, stream=None, offset: int = 0, nbytes=None):
+        """out[0..1023] (device) XOR to the XOR of the buffer's 32-bit words (oco_buffer_xor32)."""
+        n = (self.nbytes - offset) if nbytes is None else nbytes
+        _check(load_library().oco_buffer_xor32(self.ptr + offset, n // 4, _addr(out), _stream(stream)))
 
     def at(self, offset: int) -> int:
         return self.ptr + offset

@@ -245,8 +245,12 @@ __global__ __launch_bounds__(256) void mx_matmul_kernel(KPRE_PARAMS, MxArgs a) {
         const uint32_t so = s * MX_REC;
 #pragma unroll
         for (int t = 0; t < 2; t++) {
+#if defined(OCO_ABL) && OCO_ABL == 6
+            const u32x4 lo = u32x4{so, (uint32_t)t, 3u, 4u}, hi = u32x4{(uint32_t)lane, so, 1u, 2u};
+#else
             const u32x4 lo = __builtin_amdgcn_raw_buffer_load_b128(ra_rs, lane * 16 + 2 * t * 1024, so, 0);
             const u32x4 hi = __builtin_amdgcn_raw_buffer_load_b128(ra_rs, lane * 16 + (2 * t + 1) * 1024, so, 0);
+#endif
             av[U][t] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
         }
         as[U] = __builtin_amdgcn_raw_buffer_load_b32(ra_rs, MX_DATA + lane * 4, so, 0);
@@ -255,8 +259,13 @@ __global__ __launch_bounds__(256) void mx_matmul_kernel(KPRE_PARAMS, MxArgs a) {
         constexpr int U = decltype(slot)::value;
 #pragma unroll
         for (int u = 0; u < BU; u++) {
+#if defined(OCO_ABL) && OCO_ABL == 7
+            bv[U][u] = u32x4{boff[u], j, 5u, 6u};
+            bx4[U][u] = boff[u] ^ j;
+#else
             bv[U][u] = __builtin_amdgcn_raw_buffer_load_b128(rb_rs, boff[u], j * 68, 0);
             bx4[U][u] = __builtin_amdgcn_raw_buffer_load_b32(rb_rs, boff[u] + 16, j * 68, 0);
+#endif
         }
     };
     auto store_b = [&](auto slot, auto stage) {
@@ -313,6 +322,11 @@ __global__ __launch_bounds__(256) void mx_matmul_kernel(KPRE_PARAMS, MxArgs a) {
             const bool dead = part && (nblk & 1) && s == a.ksteps - 1;
 #pragma unroll
             for (int j = 0; j < CT; j++) scl[j] = dead ? 0x7f7f7f7fu : scl[j];
+#if defined(OCO_ABL) && OCO_ABL == 5
+#pragma unroll
+            for (int j = 0; j < CT; j++) acc[j][0] += __int_as_float(av[U][0][0] ^ av[U][1][7] ^ bf[PA][j][0] ^ bf[PA][j][3] ^ (int)scl[j] ^ (int)as[U]);
+            return;
+#endif
 #pragma unroll
             for (int t = 0; t < 2; t++)
 #pragma unroll

@@ -37,6 +37,31 @@ int plan_override(uint32_t knob, int32_t *vals) {
     return (int)n;
 }
 
+// XOR of all 32-bit words: each thread keeps four 16-byte nontemporal loads
+// in flight per round (the shape of a plain HBM stream); workgroup b stores
+// its XOR to out[b] (an atomic per workgroup into one word costs
+// microseconds of contention), workgroup 0 zeroes the slots no workgroup
+// owns.  XOR is order-independent: exact.
+__global__ __launch_bounds__(256) void xor32_kernel(const uint8_t *src, uint32_t bytes, uint32_t *out) {
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(src), 0, bytes, 0x00020000);
+    constexpr int U = 4;
+    uint32_t acc = 0;
+    for (uint32_t base = blockIdx.x * 256u * U * 16u; base < bytes; base += gridDim.x * 256u * U * 16u) {
+        u32x4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) v[u] = __builtin_amdgcn_raw_buffer_load_b128(r, base + (u * 256 + threadIdx.x) * 16, 0, 2);
+#pragma unroll
+        for (int u = 0; u < U; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    __shared__ uint32_t part[4];
+    for (int o = 32; o > 0; o >>= 1) acc ^= (uint32_t)__shfl_xor((int)acc, o);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) out[blockIdx.x] = part[0] ^ part[1] ^ part[2] ^ part[3];
+    if (blockIdx.x == 0)
+        for (uint32_t i = gridDim.x + threadIdx.x; i < OCO_XOR32_SLOTS; i += 256) out[i] = 0;
+}
+
 __global__ void fill32_kernel(uint32_t *dst, uint32_t pattern, size_t words) {
     size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     size_t stride = (size_t)gridDim.x * blockDim.x;
@@ -131,6 +156,18 @@ int oco_buffer_fill32(void *dst, uint32_t pattern, size_t words, oco_stream stre
     hipLaunchKernelGGL(fill32_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
                        (uint32_t *)dst, pattern, words);
     return launch_check("fill32");
+}
+
+int oco_buffer_xor32(const void *src, size_t words, uint32_t *out, oco_stream stream) {
+    if (!words) return OCO_OK;
+    if (!src || !out) return fail(OCO_ERR_INVALID, "oco_buffer_xor32: null pointer");
+    if (((uintptr_t)src & 15u) || words % 4) return fail(OCO_ERR_INVALID, "oco_buffer_xor32: needs 16-byte aligned whole chunks");
+    if (words > 0x3fffffffull) return fail(OCO_ERR_INVALID, "oco_buffer_xor32: over 4 GiB");
+    const uint32_t bytes = (uint32_t)(words * 4);
+    const uint32_t rounds = (bytes + 16383u) / 16384u;  // 16 KiB per workgroup round
+    const uint32_t grid = rounds < OCO_XOR32_SLOTS ? rounds : OCO_XOR32_SLOTS;
+    hipLaunchKernelGGL(xor32_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, (const uint8_t *)src, bytes, out);
+    return launch_check("xor32");
 }
 
 int oco_stream_create(oco_stream *out) {

@@ -176,3 +176,17 @@ def test_matvec_norm_routed_rows(lib):
     lib.matvec_norm(12, wb, xb, nb, 1e-5, y2.ptr, p, False, lib.DType.F32, None, ib)
     lib.synchronize()
     assert np.array_equal(y1.read(np.uint32), y2.read(np.uint32))
+
+
+@pytest.mark.parametrize("words", [4, 4096, 2203200, 2203204])
+def test_buffer_xor32(lib, words):
+    """oco_buffer_xor32 (the read-floor stream) equals numpy's XOR over the
+    words, accumulating into the caller's word; partial rounds and tails."""
+    rng = np.random.default_rng(words)
+    data = rng.integers(0, 2 ** 32, size=words, dtype=np.uint64).astype(np.uint32)
+    buf = lib.DeviceBuffer.from_array(data)
+    # stale slots hold garbage before the call: every slot is written
+    out = lib.DeviceBuffer.from_array(rng.integers(0, 2 ** 32, size=1024, dtype=np.uint64).astype(np.uint32))
+    buf.xor32(out)
+    lib.synchronize()
+    assert np.bitwise_xor.reduce(out.download(np.uint32)) == np.bitwise_xor.reduce(data)
