@@ -245,7 +245,9 @@ __global__ __launch_bounds__(256) void stream_kernel(const uint8_t *w_, const vo
 
     // Two groups' loads in flight per wavefront: a ring of two register sets.
     u32x4 ra[DIRECT ? 1 : ROWS * LPR], rb[DIRECT ? 1 : ROWS * LPR];
-    typename T::Raw da[DIRECT ? NPL : 1], db[DIRECT ? NPL : 1];
+    // DIRECT: a ring of three sets of pieces; a set is refilled right after
+    // its group is decoded, so two groups stay in flight with no copies.
+    typename T::Raw da[DIRECT ? NPL : 1], db[DIRECT ? NPL : 1], dc[DIRECT ? NPL : 1];
     __amdgpu_buffer_rsrc_t rall;
     if constexpr (DIRECT) {
         const uint64_t bytes = (uint64_t)p.n * a.row_bytes;
@@ -317,6 +319,7 @@ __global__ __launch_bounds__(256) void stream_kernel(const uint8_t *w_, const vo
     if constexpr (DIRECT) {
         if (g0 < a.ngroups) issue_direct(g0, da);
         if (g0 + G < a.ngroups) issue_direct(g0 + G, db);
+        if (g0 + 2 * G < a.ngroups) issue_direct(g0 + 2 * G, dc);
     } else {
         if (g0 < a.ngroups) issue(g0, ra);
         if (g0 + G < a.ngroups) issue(g0 + G, rb);
@@ -412,15 +415,12 @@ __global__ __launch_bounds__(256) void stream_kernel(const uint8_t *w_, const vo
     auto group = [&](uint32_t g, u32x4 *regs, typename T::Raw *dr) __attribute__((always_inline)) {
         float acc = 0.f;
         if constexpr (DIRECT) {
-            typename T::Raw cur[NPL];
-#pragma unroll
-            for (int s = 0; s < NPL; s++) cur[s] = dr[s];
-            if (g + 2 * G < a.ngroups) issue_direct(g + 2 * G, dr);
 #pragma unroll
             for (int s = 0; s < NPL; s++) {
                 const uint32_t pl = c + 32 * s;
-                if (pl < pieces) acc += tile_dot<FMT>(cur[s], xv[s], sv[s], pl % T::P);
+                if (pl < pieces) acc += tile_dot<FMT>(dr[s], xv[s], sv[s], pl % T::P);
             }
+            if (g + 3 * G < a.ngroups) issue_direct(g + 3 * G, dr);
         } else {
 #pragma unroll
             for (int i = 0; i < ROWS * LPR; i++) reinterpret_cast<u32x4 *>(tile)[i * 64 + lane] = regs[i];
@@ -461,9 +461,17 @@ __global__ __launch_bounds__(256) void stream_kernel(const uint8_t *w_, const vo
                 reinterpret_cast<float *>(a.y)[o] = v;
         }
     };
-    for (uint32_t g = g0; g < a.ngroups; g += 2 * G) {
-        group(g, ra, da);
-        if (g + G < a.ngroups) group(g + G, rb, db);
+    if constexpr (DIRECT) {
+        for (uint32_t g = g0; g < a.ngroups; g += 3 * G) {
+            group(g, ra, da);
+            if (g + G < a.ngroups) group(g + G, rb, db);
+            if (g + 2 * G < a.ngroups) group(g + 2 * G, ra, dc);
+        }
+    } else {
+        for (uint32_t g = g0; g < a.ngroups; g += 2 * G) {
+            group(g, ra, da);
+            if (g + G < a.ngroups) group(g + G, rb, db);
+        }
     }
     TL_STAMP(6);
 }
