@@ -102,7 +102,8 @@ typedef enum oco_knob {
     OCO_KNOB_MOE_Q4_ROWS = 8,     /* Q4_K grouped tiles: rows per tile (32|48|64), value 0: the f16 LDS tiles */
     OCO_KNOB_MOE_WG = 9,          /* routed decode kernel: workgroups per CU */
     OCO_KNOB_MX_EXPERTS_KS = 10,  /* MXFP4 expert down tiles of 16 rows: K split (1|2) */
-    OCO_KNOB_STREAM_DIRECT = 11,  /* value 0: Q4_K/Q5_K streaming matvec through the LDS tile even when aligned */
+    OCO_KNOB_STREAM_DIRECT = 11,  /* value 0: Q4_K/Q5_K streaming matvec through the LDS tile even when aligned;
+                                     second value (optional): activations 0 staged in LDS, 1 in registers */
     OCO_KNOB_COUNT = 12
 } oco_knob;
 int oco_plan_override(uint32_t knob, const int32_t *values, uint32_t count);

@@ -187,7 +187,10 @@ struct DirectOk<OCO_Q5_K> {
 // DIRECT (Q4_K / Q5_K on a 16-byte aligned base, whose blocks are then all
 // 16-byte aligned): each lane loads its pieces' 16-byte chunks straight into
 // registers, with no LDS tile and no realignment.
-template <int FMT, typename XT, int NPL, int NORM, bool DIRECT>
+// Where the streaming kernel's activations come from.
+enum { XS_STAGED = 0, XS_NORM = 1, XS_NORM_FULL = 2, XS_REG = 3 };
+
+template <int FMT, typename XT, int NPL, int XS, bool DIRECT>
 __global__ __launch_bounds__(256) void stream_kernel(const uint8_t *w_, const void *x_, uint32_t row_bytes_,
                                                      uint32_t n_, uint32_t k_, uint32_t mode_, uint32_t slice_,
                                                      uint32_t ngroups_, uint32_t experts_, uint32_t routes_,
@@ -216,9 +219,12 @@ __global__ __launch_bounds__(256) void stream_kernel(const uint8_t *w_, const vo
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const oco_matrix &p = a.p;
     const uint32_t PT = p.k / T::BLOCK * T::P;  // pieces per full row
+    // LDS: [x f32, piece-major][per-piece sums] (staged x only), the
+    // wavefronts' tiles, the K-split partials.
+    const size_t xbytes = XS != XS_REG ? (size_t)p.k * 4 + (size_t)T::NSUM * PT * 4 : 0;
     float4 *xs4 = reinterpret_cast<float4 *>(smem);
     float *xsum = reinterpret_cast<float *>(smem + (size_t)p.k * 4);
-    uint8_t *tiles = smem + (size_t)p.k * 4 + (size_t)T::NSUM * PT * 4;
+    uint8_t *tiles = smem + xbytes;
     float *part = reinterpret_cast<float *>(tiles + 4 * TILE);
 
     // The wavefront index is uniform: as a scalar, every row and group offset
@@ -293,12 +299,15 @@ __global__ __launch_bounds__(256) void stream_kernel(const uint8_t *w_, const vo
         }
     };
 
+    // Each lane keeps the activations (and sums) of its pieces -- c + 32 s of
+    // this wavefront's K slice, the same for every row group -- in registers.
+    float xv[NPL][32], sv[NPL][NS];
     // The first 1024 float4 of x are requested before the weights: they come
     // from L2 and arrive while the weights are still in flight (loads return
     // in issue order).  A fused norm reads x itself first, so it does not.
     const XT *xr = reinterpret_cast<const XT *>(a.x) + (uint64_t)input * p.k;
     float xpre[4][4];
-    if constexpr (!NORM) {
+    if constexpr (XS == XS_STAGED) {
 #pragma unroll
         for (int u = 0; u < 4; u++) {
             const uint32_t f = threadIdx.x + 256 * u;
@@ -315,6 +324,29 @@ __global__ __launch_bounds__(256) void stream_kernel(const uint8_t *w_, const vo
         }
     }
 
+    // XS_REG: every lane reads its pieces' activations straight from memory
+    // (L2 after the first workgroups), before the weights: no LDS for x, no
+    // workgroup barrier.  The reads are 16-byte vectors at a stride of one
+    // piece, so for short rows staging through LDS is cheaper.
+    if constexpr (XS == XS_REG) {
+#pragma unroll
+        for (int s = 0; s < NPL; s++) {
+            const uint32_t pg = b0 * T::P + min(c + 32u * s, pieces > 0 ? pieces - 1 : 0u);
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                const uint32_t f = T::unmap(pg, t);
+                if constexpr (sizeof(XT) == 4) {
+                    const float4 q = reinterpret_cast<const float4 *>(xr)[f];
+                    xv[s][4 * t] = q.x; xv[s][4 * t + 1] = q.y; xv[s][4 * t + 2] = q.z; xv[s][4 * t + 3] = q.w;
+                } else {
+                    const uint2 q = reinterpret_cast<const uint2 *>(xr)[f];
+                    xv[s][4 * t] = __uint_as_float(q.x << 16); xv[s][4 * t + 1] = __uint_as_float(q.x & 0xffff0000u);
+                    xv[s][4 * t + 2] = __uint_as_float(q.y << 16); xv[s][4 * t + 3] = __uint_as_float(q.y & 0xffff0000u);
+                }
+            }
+        }
+    }
+
     const uint32_t G = gridDim.x, g0 = blockIdx.x;
     if constexpr (DIRECT) {
         if (g0 < a.ngroups) issue_direct(g0, da);
@@ -326,20 +358,20 @@ __global__ __launch_bounds__(256) void stream_kernel(const uint8_t *w_, const vo
     }
     TL_STAMP(2);
 
-    // Stage x (f32) in piece-major order, then the per-piece sums.  With a
+    // Staged: x (f32) to LDS in piece-major order, then the per-piece sums.  With a
     // fused norm, x is the bf16 row before normalisation: every workgroup
     // takes its inverse RMS (the same routine and order as oco_norm, so the
     // staged values equal oco_norm's output bit for bit) and normalises
     // while staging.
-    {
+    if constexpr (XS != XS_REG) {
         float inv = 1.f;
-        if constexpr (NORM != 0) inv = block_inv_rms(reinterpret_cast<const uint16_t *>(xr), p.k, a.norm_eps, part);
+        if constexpr (XS == XS_NORM || XS == XS_NORM_FULL) inv = block_inv_rms(reinterpret_cast<const uint16_t *>(xr), p.k, a.norm_eps, part);
         for (uint32_t f0 = threadIdx.x; f0 < p.k / 4; f0 += 4 * 256) {
             float v[4][4];
 #pragma unroll
             for (int u = 0; u < 4; u++) {
                 const uint32_t f = f0 + 256 * u;
-                if (!NORM && f0 == threadIdx.x) {
+                if (XS == XS_STAGED && f0 == threadIdx.x) {
 #pragma unroll
                     for (int e = 0; e < 4; e++) v[u][e] = xpre[u][e];
                 } else if (f < p.k / 4) {
@@ -357,7 +389,7 @@ __global__ __launch_bounds__(256) void stream_kernel(const uint8_t *w_, const vo
             for (int u = 0; u < 4; u++) {
                 const uint32_t f = f0 + 256 * u;
                 if (f < p.k / 4) {
-                    if constexpr (NORM != 0) {
+                    if constexpr (XS == XS_NORM || XS == XS_NORM_FULL) {
                         float wn[4];
                         if (((uintptr_t)a.norm_w & 15u) == 0) {
                             const float4 t = reinterpret_cast<const float4 *>(a.norm_w)[f];
@@ -368,7 +400,7 @@ __global__ __launch_bounds__(256) void stream_kernel(const uint8_t *w_, const vo
                         }
 #pragma unroll
                         for (int e = 0; e < 4; e++)
-                            v[u][e] = bf16_bits_to_f32(norm_value_bits(v[u][e], inv, wn[e], NORM == 2));
+                            v[u][e] = bf16_bits_to_f32(norm_value_bits(v[u][e], inv, wn[e], XS == XS_NORM_FULL));
                     }
                     uint32_t pp, tt;
                     T::map(f, pp, tt);
@@ -379,35 +411,36 @@ __global__ __launch_bounds__(256) void stream_kernel(const uint8_t *w_, const vo
         if constexpr (T::NSUM > 0) {
             __syncthreads();
             for (uint32_t pp = threadIdx.x; pp < PT; pp += 256) {
-                float xv[32], sv[NS];
+                float xt[32], st[NS];
 #pragma unroll
                 for (int t = 0; t < 8; t++) {
                     float4 q = xs4[t * PT + pp];
-                    xv[4 * t] = q.x; xv[4 * t + 1] = q.y; xv[4 * t + 2] = q.z; xv[4 * t + 3] = q.w;
+                    xt[4 * t] = q.x; xt[4 * t + 1] = q.y; xt[4 * t + 2] = q.z; xt[4 * t + 3] = q.w;
                 }
-                T::sums(xv, sv);
+                T::sums(xt, st);
 #pragma unroll
-                for (int j = 0; j < T::NSUM; j++) xsum[j * PT + pp] = sv[j];
+                for (int j = 0; j < T::NSUM; j++) xsum[j * PT + pp] = st[j];
             }
         }
         __syncthreads();
     }
-    TL_STAMP(3);
-
-    // Each lane keeps the activations (and sums) of its pieces -- c + 32 s of
-    // this wavefront's K slice, the same for every row group -- in registers.
-    float xv[NPL][32], sv[NPL][NS];
+    if constexpr (XS == XS_REG) {
 #pragma unroll
-    for (int s = 0; s < NPL; s++) {
-        const uint32_t pg = b0 * T::P + min(c + 32u * s, pieces > 0 ? pieces - 1 : 0u);
+        for (int s = 0; s < NPL; s++) T::sums(xv[s], sv[s]);
+    } else {
 #pragma unroll
-        for (int t = 0; t < 8; t++) {
-            const float4 q = xs4[t * PT + pg];
-            xv[s][4 * t] = q.x; xv[s][4 * t + 1] = q.y; xv[s][4 * t + 2] = q.z; xv[s][4 * t + 3] = q.w;
+        for (int s = 0; s < NPL; s++) {
+            const uint32_t pg = b0 * T::P + min(c + 32u * s, pieces > 0 ? pieces - 1 : 0u);
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                const float4 q = xs4[t * PT + pg];
+                xv[s][4 * t] = q.x; xv[s][4 * t + 1] = q.y; xv[s][4 * t + 2] = q.z; xv[s][4 * t + 3] = q.w;
+            }
+#pragma unroll
+            for (int j = 0; j < T::NSUM; j++) sv[s][j] = xsum[j * PT + pg];
         }
-#pragma unroll
-        for (int j = 0; j < T::NSUM; j++) sv[s][j] = xsum[j * PT + pg];
     }
+    TL_STAMP(3);
 
     uint8_t *tile = tiles + (size_t)wave * TILE;
     // One row group: its registers to this wavefront's LDS tile, the loads of
@@ -479,21 +512,21 @@ __global__ __launch_bounds__(256) void stream_kernel(const uint8_t *w_, const vo
 typedef void (*StreamFn)(const uint8_t *, const void *, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t,
                          uint32_t, uint32_t, StreamArgs);
 
-template <int FMT, typename XT, int NORM, bool DIRECT>
+template <int FMT, typename XT, int XS, bool DIRECT>
 static StreamFn stream_pick_npl_d(int npl) {
     switch (npl) {
-    case 1: return stream_kernel<FMT, XT, 1, NORM, DIRECT>;
-    case 2: return stream_kernel<FMT, XT, 2, NORM, DIRECT>;
-    case 3: return stream_kernel<FMT, XT, 3, NORM, DIRECT>;
-    case 4: return stream_kernel<FMT, XT, 4, NORM, DIRECT>;
+    case 1: return stream_kernel<FMT, XT, 1, XS, DIRECT>;
+    case 2: return stream_kernel<FMT, XT, 2, XS, DIRECT>;
+    case 3: return stream_kernel<FMT, XT, 3, XS, DIRECT>;
+    case 4: return stream_kernel<FMT, XT, 4, XS, DIRECT>;
     }
     return nullptr;
 }
-template <int FMT, typename XT, int NORM>
+template <int FMT, typename XT, int XS>
 static StreamFn stream_pick_npl(int npl, bool direct) {
     if constexpr (DirectOk<FMT>::value)
-        if (direct) return stream_pick_npl_d<FMT, XT, NORM, true>(npl);
-    return stream_pick_npl_d<FMT, XT, NORM, false>(npl);
+        if (direct) return stream_pick_npl_d<FMT, XT, XS, true>(npl);
+    return stream_pick_npl_d<FMT, XT, XS, false>(npl);
 }
 
 template <int FMT>
@@ -507,18 +540,19 @@ static int stream_lpr(int npl) {
     return 0;
 }
 
-// norm (fused RMS norm: 0 off, 1 on, 2 full_layer rounding) only with bf16 rows.
+// xs: an XS_* source of x; the fused norms only with bf16 rows.
 template <typename XT>
-static StreamFn stream_pick_format(uint32_t fmt, int norm, int npl, bool direct, int &lpr) {
+static StreamFn stream_pick_format(uint32_t fmt, int xs, int npl, bool direct, int &lpr) {
     switch (fmt) {
 #define F(FM)                                                                                   \
     case FM:                                                                                    \
         lpr = stream_lpr<FM>(npl);                                                              \
         if constexpr (sizeof(XT) == 2) {                                                        \
-            if (norm == 1) return stream_pick_npl<FM, XT, 1>(npl, direct);                      \
-            if (norm == 2) return stream_pick_npl<FM, XT, 2>(npl, direct);                      \
+            if (xs == XS_NORM) return stream_pick_npl<FM, XT, XS_NORM>(npl, direct);            \
+            if (xs == XS_NORM_FULL) return stream_pick_npl<FM, XT, XS_NORM_FULL>(npl, direct);  \
         }                                                                                       \
-        return norm ? nullptr : stream_pick_npl<FM, XT, 0>(npl, direct);
+        if (xs == XS_REG) return stream_pick_npl<FM, XT, XS_REG>(npl, direct);                  \
+        return xs == XS_STAGED ? stream_pick_npl<FM, XT, XS_STAGED>(npl, direct) : nullptr;
         F(OCO_Q8_0) F(OCO_MXFP4) F(OCO_Q4_K) F(OCO_Q6_K) F(OCO_Q4_0) F(OCO_Q4_1) F(OCO_Q5_K)
 #undef F
     }
@@ -641,7 +675,9 @@ static int matvec_impl(uint32_t format, const void *w, const void *x, oco_dtype 
         return fail(OCO_ERR_UNSUPPORTED, "oco_matvec: output must be f32 or bf16");
     const int routed_f32 = p->experts > 1 && !p->route_major;
     int32_t plain[4];
-    if (streamable(format) && !(plan_override(OCO_KNOB_MATVEC_PLAIN, plain) && plain[0])) {
+    // The streaming kernel reads x in 16-byte (f32) or 8-byte (bf16) vectors.
+    const bool x_vec = ((uintptr_t)x & (x_dtype == OCO_DT_F32 ? 15u : 7u)) == 0;
+    if (streamable(format) && x_vec && !(plan_override(OCO_KNOB_MATVEC_PLAIN, plain) && plain[0])) {
         static int cus = 0;
         if (!cus) {
             int dev = 0;
@@ -677,10 +713,19 @@ static int matvec_impl(uint32_t format, const void *w, const void *x, oco_dtype 
             slice_blocks = (nblocks + sp.ks - 1) / sp.ks;
             npl = (int)((slice_blocks * P + 31) / 32);
         }
+        // Where the activations come from: a fused norm stages them through
+        // LDS; otherwise rows past 8192 values read them straight into
+        // registers, since staged x would take LDS that occupancy needs
+        // (measured, Q6_K 4096 x 12288: 15.2 -> 14.5 us), while shorter rows
+        // stage (MXFP4 5760 x 2880: 5.25 us staged, 7.7 us from registers).
+        // OCO_KNOB_STREAM_DIRECT's second value, when given, picks: 0 staged,
+        // 1 registers.
+        int xs = norm ? (norm->full_layer ? XS_NORM_FULL : XS_NORM) : p->k > 8192 ? XS_REG : XS_STAGED;
+        if (!norm && plan_override(OCO_KNOB_STREAM_DIRECT, dov) >= 2) xs = dov[1] ? XS_REG : XS_STAGED;
         int lpr = 0;
         StreamFn fn = npl > 4 ? nullptr
-                    : x_dtype == OCO_DT_F32 ? stream_pick_format<float>(format, norm ? (norm->full_layer ? 2 : 1) : 0, npl, direct, lpr)
-                                            : stream_pick_format<bf16_t>(format, norm ? (norm->full_layer ? 2 : 1) : 0, npl, direct, lpr);
+                    : x_dtype == OCO_DT_F32 ? stream_pick_format<float>(format, xs, npl, direct, lpr)
+                                            : stream_pick_format<bf16_t>(format, xs, npl, direct, lpr);
         if (fn) {
             StreamArgs a;
             a.w = (const uint8_t *)w;
@@ -703,7 +748,8 @@ static int matvec_impl(uint32_t format, const void *w, const void *x, oco_dtype 
                                   : format == OCO_Q6_K                                            ? 4
                                                                                                   : 0;
             const size_t tile = direct ? 0 : (size_t)2 * lpr * 1024;
-            const size_t lds = (size_t)p->k * 4 + (size_t)nsum * (p->k / 32) * 4 + 4 * tile + 32 * sizeof(float);
+            const size_t xbytes = xs != XS_REG ? (size_t)p->k * 4 + (size_t)nsum * (p->k / 32) * 4 : 0;
+            const size_t lds = xbytes + 4 * tile + 32 * sizeof(float);
             if (lds > 160 * 1024)
                 return fail(OCO_ERR_UNSUPPORTED, "oco_matvec: k=%u needs %zu bytes of LDS", p->k, lds);
             if (lds > 64 * 1024)

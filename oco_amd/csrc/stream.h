@@ -71,6 +71,8 @@ struct Tile<OCO_MXFP4> {
         p = f >> 3;
         t = f & 7;
     }
+    // float4 index of run t of piece p (the inverse of map)
+    __device__ __forceinline__ static uint32_t unmap(uint32_t p, uint32_t t) { return p * 8 + t; }
     __device__ __forceinline__ static void sums(const float *, float *) {}
     __device__ __forceinline__ static Raw load(const uint8_t *blk, int) {
         Raw r;
@@ -111,6 +113,8 @@ struct Tile<OCO_Q8_0> {
         p = f >> 3;
         t = f & 7;
     }
+    // float4 index of run t of piece p (the inverse of map)
+    __device__ __forceinline__ static uint32_t unmap(uint32_t p, uint32_t t) { return p * 8 + t; }
     __device__ __forceinline__ static void sums(const float *x, float *s) {
         float a = 0.f;
 #pragma unroll
@@ -157,6 +161,10 @@ struct Tile<OCO_Q4_K> {
         uint32_t odd = (w & 7) >> 2;
         p = b * 8 + 2 * g + odd;
         t = (w >> 3) * 4 + (w & 3);
+    }
+    __device__ __forceinline__ static uint32_t unmap(uint32_t p, uint32_t t) {
+        const uint32_t c = p & 7;
+        return (p >> 3) * 64 + (c >> 1) * 16 + (t >> 2) * 8 + (c & 1) * 4 + (t & 3);
     }
     __device__ __forceinline__ static void sums(const float *x, float *s) {
         float a = 0.f, b = 0.f;
@@ -239,6 +247,10 @@ struct Tile<OCO_Q6_K> {
         p = b * 8 + 4 * h + (w >> 1);
         t = 2 * q + (w & 1);
     }
+    __device__ __forceinline__ static uint32_t unmap(uint32_t p, uint32_t t) {
+        const uint32_t c = p & 7;
+        return (p >> 3) * 64 + (c >> 2) * 32 + (t >> 1) * 8 + (c & 3) * 2 + (t & 1);
+    }
     __device__ __forceinline__ static void sums(const float *x, float *s) {
 #pragma unroll
         for (int q = 0; q < 4; q++) {
@@ -294,6 +306,8 @@ struct Tile<OCO_Q4_0> {
         p = f >> 3;
         t = f & 7;
     }
+    // float4 index of run t of piece p (the inverse of map)
+    __device__ __forceinline__ static uint32_t unmap(uint32_t p, uint32_t t) { return p * 8 + t; }
     __device__ __forceinline__ static void sums(const float *x, float *s) {
         float a = 0.f;
 #pragma unroll
@@ -344,6 +358,8 @@ struct Tile<OCO_Q4_1> {
         p = f >> 3;
         t = f & 7;
     }
+    // float4 index of run t of piece p (the inverse of map)
+    __device__ __forceinline__ static uint32_t unmap(uint32_t p, uint32_t t) { return p * 8 + t; }
     __device__ __forceinline__ static void sums(const float *x, float *s) { Tile<OCO_Q4_0>::sums(x, s); }
     __device__ __forceinline__ static Raw load(const uint8_t *blk, int) {
         Raw r;
@@ -371,6 +387,7 @@ struct Tile<OCO_Q5_K> {
         uint4 hdr, qh, qs;
     };
     __device__ __forceinline__ static void map(uint32_t f, uint32_t &p, uint32_t &t) { Tile<OCO_Q4_K>::map(f, p, t); }
+    __device__ __forceinline__ static uint32_t unmap(uint32_t p, uint32_t t) { return Tile<OCO_Q4_K>::unmap(p, t); }
     __device__ __forceinline__ static void sums(const float *x, float *s) { Tile<OCO_Q4_K>::sums(x, s); }
     __device__ __forceinline__ static Raw load(const uint8_t *blk, int c) {
         Raw r;

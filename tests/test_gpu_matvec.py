@@ -208,6 +208,14 @@ def test_matvec_stream_plans(lib, plan):
         _stream_plan_cases(lib, plan)
 
 
+@pytest.mark.parametrize("direct,xreg", [(1, 0), (1, 1), (0, 1), (0, 0)])
+def test_matvec_stream_x_source(lib, direct, xreg):
+    """Activations staged through LDS or read straight into registers, with
+    and without per-lane direct weight loads, on every streaming format."""
+    with lib.overridden(lib.Knob.STREAM_DIRECT, [direct, xreg]):
+        _stream_plan_cases(lib, f"direct {direct} xreg {xreg}")
+
+
 def _stream_plan_cases(lib, plan):
     from oco_amd import synth
     for fmt, n, k in [(O.MXFP4, 131, 2880), (P.Q8_0, 77, 4096), (P.Q4_K, 257, 2048), (P.Q6_K, 300, 4096),
