@@ -353,7 +353,9 @@ def _select(logits, k):
 
 
 class Prefill(Workload):
-    """Dense prefill Y = X W^T on MFMA: weight [n x k] GGUF, `m` bf16 tokens."""
+    """Dense prefill Y = X W^T on MFMA: weight [n x k] GGUF, `m` bf16 tokens,
+    bf16 output rows (the reference's matrix kernels store bf16 unless asked
+    for f32: shaders/matrix/weights.metal:24-33)."""
     bound = "mfma"
     unit = "TFLOP/s"
 
@@ -370,14 +372,14 @@ class Prefill(Workload):
         for c in range(self.copies):
             self.w.upload(w, c * self.bytes)
         self.x = oco.DeviceBuffer.from_array(synth.bf16_bits(synth.activations(8, self.m * self.k)))
-        self.y = oco.DeviceBuffer(self.m * self.n * 4)
+        self.y = oco.DeviceBuffer(self.m * self.n * 2)
         self.p = oco.Matrix(self.k, self.n, self.m, 0, 1, 1, 0)
         self.ws_bytes = oco.matmul_workspace(self.fmt, self.p)
         self.ws = oco.DeviceBuffer(max(self.ws_bytes, 256))
 
     def launch(self, i):
         self.oco.matmul(self.fmt, self.w.ptr + (i % self.copies) * self.bytes, self.x, self.y, self.p,
-                        stream=self.stream, workspace=self.ws, workspace_bytes=self.ws_bytes)
+                        y_dtype=self.oco.DType.BF16, stream=self.stream, workspace=self.ws, workspace_bytes=self.ws_bytes)
 
     def work_per_step(self):
         return 2.0 * self.m * self.n * self.k

@@ -94,7 +94,7 @@ typedef enum oco_knob {
     OCO_KNOB_STREAM_PLAN = 0,     /* streaming matvec: 1 (reserved), K split (1|2|4), WGs per CU */
     OCO_KNOB_MATVEC_PLAN = 1,     /* plain matvec (F32/F16/BF16): rows per wave, K split */
     OCO_KNOB_MATVEC_PLAIN = 2,    /* value 1: quantized formats take the plain matvec, not the streaming one */
-    OCO_KNOB_MX_TILE = 3,         /* MXFP4 prefill tile: wavefronts along rows, 32-column tiles per wave */
+    OCO_KNOB_MX_TILE = 3,         /* reserved (the MXFP4 prefill has a single tile: 128 x 96) */
     OCO_KNOB_MX_PREFILL_OFF = 4,  /* value 1: MXFP4 prefill takes the f16 MFMA tiles instead of the FP4 ones */
     OCO_KNOB_MATMUL_TILE = 5,     /* f16 MFMA prefill tile choice index */
     OCO_KNOB_MOE_MX_TOKENS = 6,   /* MXFP4 banks take the block-scaled MFMA tiles from this many tokens */

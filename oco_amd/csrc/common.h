@@ -43,6 +43,17 @@ __device__ __forceinline__ float half_bits_to_f32(uint32_t h) {
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
+// A pointer in the global address space.  Pointers unpacked from the
+// preloaded argument words (KPRE_APPLY) are generic to the compiler, so
+// their loads and stores become FLAT operations, which count in lgkmcnt as
+// well as vmcnt: every LDS wait behind them then also waits for memory
+// (measured: a store loop with an LDS read per iteration went from ~700 to
+// a few clocks per iteration as global stores).
+template <class T>
+__device__ __forceinline__ __attribute__((address_space(1))) T *gp(T *p) {
+    return (__attribute__((address_space(1))) T *)p;
+}
+
 // float -> bf16 bits, round to nearest even, NaN stays quiet.
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
     uint32_t u = __float_as_uint(f);

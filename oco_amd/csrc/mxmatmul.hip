@@ -6,20 +6,24 @@
 //  * W (GGUF MXFP4: per 32 values one E8M0 byte, then 16 bytes of E2M1 nibbles,
 //    value j in the low nibble of byte j and value j+16 in the high nibble) is
 //    the B operand as stored.  Its E8M0 byte is the B block scale.
-//  * X (bf16) is split once per call into two E4M3 terms with their own E8M0
-//    scale per 32-block: x = s1 q1 + s2 q2.  s1 is the smallest power of two
-//    with max|x| / s1 <= 448; the residual x - s1 q1 is exact in fp32 and its
-//    rounding to E4M3 under s2 leaves at most 2^-8 of the residual's block
-//    maximum.  The split stores the terms in the MFMA's register order with
-//    the k order of each block permuted to match W's nibble order, so every
-//    operand load is one contiguous 16-byte access.
+//  * X (bf16) is split once per call into two E2M3 (FP6) terms with their own
+//    E8M0 scale per 32-block: x = s1 q1 + s2 q2.  s1 is the smallest power
+//    of two with max|x| / s1 <= 7.5; the residual x - s1 q1 is exact in fp32
+//    and its rounding to E2M3 under s2 leaves at most 1/225 of the block
+//    maximum per value (relative L2 ~3.4e-4 on the product for N(0,1)
+//    activations, ~4.4e-4 for values spanning 2^+-30 in a block).  FP6 x
+//    FP4 issues in 40 clocks against 64 for FP8 x FP4 (measured), and the
+//    terms are 24 bytes per 32 values against 32.  The split stores the
+//    terms in the MFMA's register order, so every operand load is
+//    contiguous.
 //
 // Operand layout of the 32x32x64 scaled MFMA (measured on gfx950), row
 // (column, for B) r = l % 32, block b = 0, 1 of the K=64 step:
 //  * B, E2M1: lane r + 32b holds block b as 16 bytes, element e in nibble
 //    e & 1 of byte e / 2 -- exactly a GGUF MXFP4 block's payload;
-//  * A, E4M3: block b's elements 0..15 are bytes 16b .. 16b + 15 of lane r,
-//    elements 16..31 the same bytes of lane r + 32;
+//  * A, E2M3: lane r + 32b holds block b as 24 bytes, element e in bits
+//    6e .. 6e + 5; element e of both operands is block column e / 2 for even
+//    e and 16 + e / 2 for odd e (the GGUF nibble order);
 //  * block b's scale is in lane r + 32b (A and B), byte chosen by op_sel.
 // The accumulator holds column l % 32, rows 8 (v / 4) + 4 (l / 32) + v % 4.
 #include <stdio.h>
@@ -34,9 +38,14 @@ namespace oco {
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-// One record per (32-row tile, K step of 64): [term 2][block 2][lane 64][16 B]
-// of E4M3 codes, then [lane 64] u32 of E8M0 scales (byte t = term t).
-constexpr uint32_t MX_DATA = 2 * 2 * 64 * 16, MX_REC = MX_DATA + 64 * 4;
+// One record per (32-row tile, K step of 64): [term 2][lane 64][16 B] then
+// [term 2][lane 64][8 B] of E2M3 codes (lane l's 24-byte fragment is its
+// 16-byte part and its 8-byte part), then [lane 64] u32 of E8M0 scales
+// (byte t = term t).  Lane l = row l % 32, block l / 32 of the step.
+constexpr uint32_t MX_LO = 2 * 64 * 16, MX_DATA = 2 * 64 * 24, MX_REC = MX_DATA + 64 * 4;
+
+typedef float f32x32 __attribute__((ext_vector_type(32)));
+typedef int i32x6 __attribute__((ext_vector_type(6)));
 
 struct MxSplitArgs {
     const uint16_t *x;
@@ -44,87 +53,111 @@ struct MxSplitArgs {
     uint32_t m, k, ksteps, records;
 };
 
-// Smallest E with amax <= 448 * 2^E, as the E8M0 byte E + 127 (0 for a zero
-// block, 255 -- NaN -- for a non-finite one).
-__device__ __forceinline__ int mx_scale_exp(float amax) {
-    if (!(amax <= 3.402823466e38f)) return 128;
-    if (amax == 0.f) return -127;
-    const uint32_t b = __float_as_uint(amax);
+// Smallest E with amax <= 7.5 * 2^E (7.5 = 1.875 * 2^2, the largest E2M3
+// value), as E; 128 (the NaN byte) for a non-finite block, -127 at least.
+__device__ __forceinline__ int mx6_scale_exp(uint32_t amax_bits) {
+    if (amax_bits >= 0x7f800000u) return 128;
+    if (amax_bits == 0) return -127;
     int e;
     uint32_t mant;
-    if (b >> 23) {
-        e = (int)(b >> 23) - 127;
-        mant = b & 0x7fffffu;
+    if (amax_bits >> 23) {
+        e = (int)(amax_bits >> 23) - 127;
+        mant = amax_bits & 0x7fffffu;
     } else {  // subnormal amax: normalise
-        const int lz = __builtin_clz(b) - 8;
+        const int lz = __builtin_clz(amax_bits) - 8;
         e = -126 - lz;
-        mant = (b << lz) & 0x7fffffu;
+        mant = (amax_bits << lz) & 0x7fffffu;
     }
-    const int E = mant <= 0x600000u ? e - 8 : e - 7;  // m <= 1.75 <=> m * 256 <= 448
+    const int E = mant <= 0x700000u ? e - 2 : e - 1;  // m <= 1.875 <=> m * 2^e <= 7.5 * 2^(e - 2)
     return E < -127 ? -127 : E;
 }
 
-// One workgroup per record: four lanes per (row, block), each holding 8 of
-// the block's 32 values (q = lane % 4: values 8q .. 8q + 7).  The block's
-// maximum meets over the quad through DPP; in the record, chunk p of a
-// (term, block) interleaves groups p and p + 2 (byte 2i: value 8p + i,
-// byte 2i + 1: value 8p + 16 + i), so partner lanes q and q ^ 2 swap their
-// codes and each stores 8 of the chunk's 16 bytes.
-__global__ __launch_bounds__(256) void mx_split_kernel(KPRE_PARAMS, MxSplitArgs a) {
+// E2M3 codes of 32 values: position 2i takes lo[i], 2i + 1 hi[i] (measured
+// on gfx950).  The asm statement keeps the sources live until the result
+// exists: hipcc otherwise may give the result registers that overlap the
+// sources, and the instruction then reads inputs it has already overwritten
+// (seen: v_cvt_scalef32_2xpk16_fp6_f32 v[34:39], v[32:47], v[0:15]).
+__device__ __forceinline__ i32x6 fp6_pack(const f32x16 &lo, const f32x16 &hi) {
+    i32x6 c = __builtin_amdgcn_cvt_scalef32_2xpk16_fp6_f32(lo, hi, 1.0f);
+    asm volatile("" ::"v"(lo), "v"(hi), "v"(c));
+    return c;
+}
+// The 32 values of E2M3 codes, in position order (same register rule).
+__device__ __forceinline__ f32x32 fp6_unpack(const i32x6 &c) {
+    f32x32 d = __builtin_amdgcn_cvt_scalef32_pk32_f32_fp6(c, 1.0f);
+    asm volatile("" ::"v"(c), "v"(d));
+    return d;
+}
+
+// One wavefront (workgroup) per record, so the records spread over every CU;
+// lane l = (row l % 32, block l / 32), each lane
+// splitting its whole block in registers: x = s1 q1 + s2 q2 with E2M3 codes
+// q and E8M0 scales s (s1 the smallest power of two with max|x| / s1 <= 7.5,
+// s2 likewise for the residual x - s1 q1, which is exact in fp32).  The
+// codes go in MFMA k order: k = 2i is the block's column i, k = 2i + 1 its
+// column 16 + i -- the nibble order of the GGUF MXFP4 payload the B operand
+// holds as stored.  The second term leaves at most 1/225 of the block
+// maximum per value: a few 1e-4 relative L2 on the product (N(0,1) rows).
+__global__ __launch_bounds__(64) void mx_split_kernel(KPRE_PARAMS, MxSplitArgs a) {
     KPRE_APPLY(a);
     const uint32_t rec = blockIdx.x;
-    const uint32_t tile = rec / a.ksteps, s = rec % a.ksteps;
-    const int tid = threadIdx.x, q = tid & 3, pair = tid >> 2, r = pair & 31, blk = pair >> 5;
-    const uint32_t row = tile * 32 + r, k0 = s * 64 + 32 * blk;
-    float v[8];
+    const uint32_t lane = threadIdx.x, tile = rec / a.ksteps, s = rec % a.ksteps;
+    const uint32_t row = tile * 32 + (lane & 31), k0 = s * 64 + 32 * (lane >> 5);
+    uint32_t w[16];
     if (row < a.m && k0 < a.k) {
-        const uint4 u = *reinterpret_cast<const uint4 *>(a.x + (uint64_t)row * a.k + k0 + 8 * q);
-        const uint32_t w4[4] = {u.x, u.y, u.z, u.w};
+        const auto src = gp(reinterpret_cast<const u32x4 *>(a.x + (uint64_t)row * a.k + k0));
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            v[2 * j] = __uint_as_float(w4[j] << 16);
-            v[2 * j + 1] = __uint_as_float(w4[j] & 0xffff0000u);
+        for (int q = 0; q < 4; q++) {
+            const u32x4 u = src[q];
+            w[4 * q] = u.x; w[4 * q + 1] = u.y; w[4 * q + 2] = u.z; w[4 * q + 3] = u.w;
         }
     } else {
 #pragma unroll
-        for (int i = 0; i < 8; i++) v[i] = 0.f;
+        for (int i = 0; i < 16; i++) w[i] = 0;
     }
-    uint8_t *out = a.frag + (uint64_t)rec * MX_REC;
+    float v[32];  // column order
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        v[2 * i] = __uint_as_float(w[i] << 16);
+        v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+    auto out = gp(a.frag + (uint64_t)rec * MX_REC);
     uint32_t scales = 0;
 #pragma unroll
     for (int t = 0; t < 2; t++) {
-        // |x| bit patterns order like the values, with Inf above every
-        // finite value and NaN above Inf: the integer maximum carries both.
-        uint32_t m = 0;
+        // |x| bit patterns order like the values, with Inf above every finite
+        // value and NaN above Inf: the integer maximum carries both.
+        // (a tree, so the 32-value maximum is five dependent steps, not 16)
+        uint32_t mt[16];
 #pragma unroll
-        for (int i = 0; i < 8; i++) m = max(m, __float_as_uint(v[i]) & 0x7fffffffu);
-        m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0xB1, 0xf, 0xf, false));  // quad xor 1
-        m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x4E, 0xf, 0xf, false));  // quad xor 2
-        const int E = mx_scale_exp(__uint_as_float(m));
+        for (int i = 0; i < 16; i++) mt[i] = max(__float_as_uint(v[i]) & 0x7fffffffu, __float_as_uint(v[16 + i]) & 0x7fffffffu);
+#pragma unroll
+        for (int w = 8; w > 0; w >>= 1)
+#pragma unroll
+            for (int i = 0; i < w; i++) mt[i] = max(mt[i], mt[i + w]);
+        const int E = mx6_scale_exp(mt[0]);
         scales |= (uint32_t)(E + 127) << (8 * t);
         const float inv = E == 128 ? 0.f : __builtin_ldexpf(1.f, -E), sc = E == 128 ? 0.f : __builtin_ldexpf(1.f, E);
-        uint32_t c[2];  // codes of values 8q .. 8q + 3 and 8q + 4 .. 8q + 7
+        f32x16 lo, hi;
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            int pk = __builtin_amdgcn_cvt_pk_fp8_f32(v[4 * h] * inv, v[4 * h + 1] * inv, 0, false);
-            pk = __builtin_amdgcn_cvt_pk_fp8_f32(v[4 * h + 2] * inv, v[4 * h + 3] * inv, pk, true);
-            c[h] = (uint32_t)pk;
-            v[4 * h] -= __builtin_amdgcn_cvt_f32_fp8(pk, 0) * sc;
-            v[4 * h + 1] -= __builtin_amdgcn_cvt_f32_fp8(pk, 1) * sc;
-            v[4 * h + 2] -= __builtin_amdgcn_cvt_f32_fp8(pk, 2) * sc;
-            v[4 * h + 3] -= __builtin_amdgcn_cvt_f32_fp8(pk, 3) * sc;
+        for (int i = 0; i < 16; i++) {
+            lo[i] = v[i] * inv;
+            hi[i] = v[16 + i] * inv;
         }
-        const uint32_t o0 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)c[0], 0x4E, 0xf, 0xf, false);
-        const uint32_t o1 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)c[1], 0x4E, 0xf, 0xf, false);
-        // Lane q < 2 (group p = q) stores bytes 0..7 of chunk p: its values
-        // 0..3 with the partner's; lane q >= 2 (group p + 2) bytes 8..15: the
-        // partner's values 4..7 with its own.
-        const uint32_t ev = q < 2 ? c[0] : o1, od = q < 2 ? o0 : c[1];
-        const uint32_t lo = __builtin_amdgcn_perm(od, ev, 0x05010400u), hi = __builtin_amdgcn_perm(od, ev, 0x07030602u);
-        const int p = q & 1;
-        *reinterpret_cast<uint2 *>(out + ((t * 2 + blk) * 64 + r + 32 * p) * 16 + (q >= 2 ? 8 : 0)) = make_uint2(lo, hi);
+        const i32x6 c = fp6_pack(lo, hi);
+        *reinterpret_cast<__attribute__((address_space(1))) u32x4 *>(out + (t * 64 + lane) * 16) =
+            u32x4{(uint32_t)c[0], (uint32_t)c[1], (uint32_t)c[2], (uint32_t)c[3]};
+        *reinterpret_cast<__attribute__((address_space(1))) u32x2 *>(out + MX_LO + (t * 64 + lane) * 8) = u32x2{(uint32_t)c[4], (uint32_t)c[5]};
+        if (t == 0) {
+            const f32x32 d = fp6_unpack(c);
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                v[i] -= d[2 * i] * sc;
+                v[16 + i] -= d[2 * i + 1] * sc;
+            }
+        }
     }
-    if (q == 0) *reinterpret_cast<uint32_t *>(out + MX_DATA + (r + 32 * blk) * 4) = scales;
+    *reinterpret_cast<__attribute__((address_space(1))) uint32_t *>(out + MX_DATA + lane * 4) = scales;
 }
 
 // The first 56 bytes arrive in SGPRs (KPre).
@@ -133,7 +166,7 @@ struct MxArgs {
     const uint8_t *frag;
     uint32_t m, n, k, ksteps, tiles;
     uint32_t row_bytes;
-    uint32_t wspan;  // weight bytes from the dword-aligned base, rounded up to 4 (< 4 GiB)
+    uint32_t wspan;  // weight bytes from the 16-byte aligned base, rounded up to 16 (< 4 GiB)
     uint32_t y_bf16;
     void *y;
     const float *bias;
@@ -169,40 +202,48 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void *p, ui
 // 32-row activation tile and CTW 32-column weight tiles, so a K step is
 // 2 CTW independent MFMAs (the two activation terms of every column tile).
 //
-// Sizing (measured on MI355X): an L2-resident operand stream reaches about
-// 33 bytes/clock per CU, and a 32x32x64 MFMA takes 64 clocks.  A workgroup
-// tile of BM rows x BN columns loads 2 BM x 64 bytes of activations and
-// 34 BN / 32 bytes of weights per K step.  At 128 x 96 (WM = 4) that is
-// 53 bytes per 384 MFMA clocks: the L2 stream, not the MFMA, sets the pace.
-// At 64 x 192 (WM = 2) the two wavefronts of a row tile read the same
-// activation records (the second from the CU's L1), and L2 traffic falls to
-// 39 bytes per 384 clocks for the same number of workgroups.
-//
 //  * A: each wavefront's split records go straight into a register ring RA
 //    K steps deep, through a buffer resource whose step offset is scalar.
-//  * B: GGUF rows staged a double step (4 blocks, 68 bytes) at a time: each
-//    thread moves whole blocks (the 20-byte dword-aligned span holding 17
-//    bytes), realigned into LDS as [block][row] 16-byte payloads and scale
-//    words whose byte (step parity) the MFMA's op_sel picks.  A register
-//    ring RB double steps deep feeds three LDS stages; one barrier per
-//    double step.
-template <int WM, int CTW, int RB>
+//  * B: GGUF rows staged eight K steps (16 blocks, 272 bytes) at a time.
+//    272 is a multiple of 16, so a row's stage span starts at the same
+//    misalignment every time: it is fetched as the 18 aligned 16-byte
+//    chunks that cover it, 18 consecutive lanes per row -- nearly the
+//    contiguous pattern L2 serves best (measured from L2: contiguous 1 KB
+//    wavefront loads ~55 bytes/clock per CU; four lanes per 68-byte row
+//    segment ~19).  The chunks land in a raw LDS buffer as they are; one
+//    pass per stage, shared by the workgroup, realigns every 17-byte block
+//    into an aligned [block][row] payload array and a [row][block] array
+//    of scale bytes.  A step then reads one aligned 16-byte fragment per
+//    column tile, and the stage's eight scales per row come in one 8-byte
+//    read (op_sel picks the step's byte).  Realigning per wavefront at
+//    fragment-read time instead put five dependent LDS reads and four
+//    v_alignbyte per fragment on every wavefront's critical path
+//    (measured: that loop alone, without loads or MFMAs, took 15 us).
+//
+//    Per stage o (one barrier): realign raw stage o + 1; write stage
+//    o + 2's chunks (in registers since stage o - 1) to the other raw
+//    buffer; request stage o + 3's chunks; run the eight steps of stage o.
+template <int WM, int CTW>
 struct MxPlan {
-    static constexpr int WN = 4 / WM, BM = 32 * WM, BN = 32 * CTW * WN, BLOCKS = 4 * BN, BU = (BLOCKS + 255) / 256;
-    static constexpr int PAY = 4 * BN * 16, SCL = 2 * BN * 4, STAGE = PAY + SCL + 16;  // + landing pad of unused slots
-    static constexpr int NST = 3, LDS = NST * STAGE, RA = 6;
-    static_assert(WM * WN == 4, "four wavefronts");
-    static_assert(RB % 3 == 0 && RB >= 3, "the B ring is a whole number of LDS stage rounds");
+    static constexpr int WN = 4 / WM, BM = 32 * WM, BN = 32 * CTW * WN;
+    static constexpr int OCT = 8;     // K steps per B stage
+    static constexpr int CH = 18;     // 16-byte chunks per row and stage
+    static constexpr int RSTR = 296;  // raw LDS bytes per row (18 chunks + pad)
+    static constexpr int BU = (BN * CH + 255) / 256;        // chunk slots per thread
+    static constexpr int RU = (BN * 2 * OCT + 255) / 256;   // realigned blocks per thread
+    static constexpr int PROW = BN + 1;                     // payload slots per block row
+    static constexpr int RAW = BN * RSTR, PAY = 2 * OCT * PROW * 16, SCL = BN * 2 * OCT;
+    static constexpr int ALN = PAY + SCL;
+    static constexpr int LDS = 2 * RAW + 2 * ALN, RA = 8;
 };
 
-template <int WM, int CTW, int RB>
+template <int WM, int CTW>
 __global__ __launch_bounds__(256) void mx_matmul_kernel(KPRE_PARAMS, MxArgs a) {
     KPRE_APPLY(a);
-    using P = MxPlan<WM, CTW, RB>;
-    constexpr int BN = P::BN, BU = P::BU, STAGE = P::STAGE, RA = P::RA, CT = CTW;
-    constexpr int PER = RB;  // double steps per unrolled round: RB, 3 stages and RA / 2 all divide it
-    static_assert(PER % 3 == 0 && (2 * PER) % RA == 0, "ring periods");
+    using P = MxPlan<WM, CTW>;
+    constexpr int BN = P::BN, BU = P::BU, RU = P::RU, RA = P::RA, CT = CTW, OCT = P::OCT;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    uint8_t *const raw = lds, *const aln = lds + 2 * P::RAW;
     // The wavefront index is uniform: readfirstlane keeps the A resource in SGPRs.
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, c = lane & 31,
               part = lane >> 5;
@@ -217,72 +258,80 @@ __global__ __launch_bounds__(256) void mx_matmul_kernel(KPRE_PARAMS, MxArgs a) {
     // A: this wavefront's records; steps past the end read as zero.
     const __amdgpu_buffer_rsrc_t ra_rs =
         uniform_rsrc(a.frag + (uint64_t)min(tile, a.tiles - 1) * a.ksteps * MX_REC, a.ksteps * MX_REC);
-    // B: the tensor from its dword-aligned base; bytes past the end read as zero.
-    const uint32_t wsh = (uint32_t)((uintptr_t)a.w & 3u);
+    // B: the tensor from its 16-byte aligned base; bytes past the end read as zero.
+    const uint32_t wsh = (uint32_t)((uintptr_t)a.w & 15u);
     const __amdgpu_buffer_rsrc_t rb_rs = uniform_rsrc(a.w - wsh, a.wspan);
     const uint32_t rbytes = (uint32_t)a.row_bytes;
-    // Staging: thread slot g = tid + 256 u moves block g % 4 of row g / 4 of
-    // each double step, realigned into the payload and scale arrays.
-    uint32_t boff[BU], bsh[BU], bpay[BU], bscl[BU];
+    // Chunk slot q = tid + 256 u: chunk q % 18 of tile row q / 18 (rows past
+    // n repeat row n - 1 and are never stored).
+    uint32_t boff[BU], bdst[BU];
 #pragma unroll
     for (int u = 0; u < BU; u++) {
-        const uint32_t g = tid + 256 * u, row = min(g / 4, (uint32_t)BN - 1), blk = g % 4;
-        const uint32_t at = wsh + min(col0 + row, a.n - 1) * rbytes + 17 * blk;
-        const bool live = g < (uint32_t)P::BLOCKS;
-        boff[u] = at & ~3u;
-        bsh[u] = at & 3u;
-        bpay[u] = live ? (blk * BN + row) * 16 : P::PAY + P::SCL;  // unused slots: the landing pad
-        bscl[u] = live ? P::PAY + ((blk & 1) * BN + row) * 4 + (blk >> 1) : P::PAY + P::SCL;
+        const uint32_t q = tid + 256 * u, row = min(q / P::CH, (uint32_t)BN - 1), ch = q % P::CH;
+        const bool live = q < (uint32_t)(BN * P::CH);
+        boff[u] = live ? ((wsh + min(col0 + row, a.n - 1) * rbytes) & ~15u) + 16 * ch : 0u;
+        bdst[u] = live ? row * P::RSTR + 16 * ch : ~0u;  // ~0: no slot (the last round's spare threads)
+    }
+    // Realign slot r = tid + 256 u: block r / BN of tile row r % BN; its
+    // scale byte sits at rsrc in the raw buffer, its payload right after.
+    uint32_t rsrc[RU], rpay[RU], rscl[RU];
+#pragma unroll
+    for (int u = 0; u < RU; u++) {
+        const uint32_t r = tid + 256 * u, row = r % BN, blk = r / BN;
+        const bool live = r < (uint32_t)(BN * 2 * OCT);
+        rsrc[u] = row * P::RSTR + ((wsh + min(col0 + row, a.n - 1) * rbytes) & 15u) + 17 * blk;
+        rpay[u] = live ? (blk * P::PROW + row) * 16 : ~0u;
+        rscl[u] = P::PAY + row * 2 * OCT + (blk & 1) * OCT + (blk >> 1);
     }
     const uint32_t wcol = wn * CT * 32;  // this wavefront's first column within the tile
 
     i32x8 av[RA][2];
     uint32_t as[RA];
-    u32x4 bv[RB][BU];
-    uint32_t bx4[RB][BU];
+    u32x4 bv[BU];
     auto load_a = [&](auto slot, uint32_t s) {
         constexpr int U = decltype(slot)::value;
         const uint32_t so = s * MX_REC;
 #pragma unroll
         for (int t = 0; t < 2; t++) {
-#if defined(OCO_ABL) && OCO_ABL == 6
-            const u32x4 lo = u32x4{so, (uint32_t)t, 3u, 4u}, hi = u32x4{(uint32_t)lane, so, 1u, 2u};
-#else
-            const u32x4 lo = __builtin_amdgcn_raw_buffer_load_b128(ra_rs, lane * 16 + 2 * t * 1024, so, 0);
-            const u32x4 hi = __builtin_amdgcn_raw_buffer_load_b128(ra_rs, lane * 16 + (2 * t + 1) * 1024, so, 0);
-#endif
-            av[U][t] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+            const u32x4 lo = __builtin_amdgcn_raw_buffer_load_b128(ra_rs, (t * 64 + lane) * 16, so, 0);
+            const u32x2 hi = __builtin_amdgcn_raw_buffer_load_b64(ra_rs, MX_LO + (t * 64 + lane) * 8, so, 0);
+            av[U][t] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, 0, 0};
         }
         as[U] = __builtin_amdgcn_raw_buffer_load_b32(ra_rs, MX_DATA + lane * 4, so, 0);
     };
-    auto load_b = [&](auto slot, uint32_t j) {
-        constexpr int U = decltype(slot)::value;
+    // B chunks of stage o (steps 8 o .. 8 o + 7) into register set V.
+    const uint32_t nst = (nsteps + OCT - 1) / OCT;
+    u32x4 bw[BU];  // the prologue's second set
+    auto load_b = [&](auto set, uint32_t o) {
+        u32x4 *v = decltype(set)::value ? bw : bv;
+#pragma unroll
+        for (int u = 0; u < BU; u++) v[u] = __builtin_amdgcn_raw_buffer_load_b128(rb_rs, boff[u], o * 272, 0);
+    };
+    auto store_b = [&](auto buf, auto set) {
+        constexpr int S = decltype(buf)::value;
+        const u32x4 *v = decltype(set)::value ? bw : bv;
 #pragma unroll
         for (int u = 0; u < BU; u++) {
-#if defined(OCO_ABL) && OCO_ABL == 7
-            bv[U][u] = u32x4{boff[u], j, 5u, 6u};
-            bx4[U][u] = boff[u] ^ j;
-#else
-            bv[U][u] = __builtin_amdgcn_raw_buffer_load_b128(rb_rs, boff[u], j * 68, 0);
-            bx4[U][u] = __builtin_amdgcn_raw_buffer_load_b32(rb_rs, boff[u] + 16, j * 68, 0);
-#endif
+            if ((BN * P::CH) % 256 == 0 || u + 1 < BU || bdst[u] != ~0u) {
+                *reinterpret_cast<u32x2 *>(raw + S * P::RAW + bdst[u]) = u32x2{v[u].x, v[u].y};
+                *reinterpret_cast<u32x2 *>(raw + S * P::RAW + bdst[u] + 8) = u32x2{v[u].z, v[u].w};
+            }
         }
     };
-    auto store_b = [&](auto slot, auto stage) {
-        constexpr int U = decltype(slot)::value, S = decltype(stage)::value;
+    // Raw buffer S to aligned buffer S.
+    auto realign = [&](auto buf) {
+        constexpr int S = decltype(buf)::value;
 #pragma unroll
-        for (int u = 0; u < BU; u++) {
-            const u32x4 v = bv[U][u];
-            const uint32_t w4 = bx4[U][u], sh = bsh[u];
-            // Span bytes: scale at sh, payload at sh + 1 .. sh + 16.
-            // alignbyte shifts by 0..3 bytes: a shift of 4 is the next dword.
-            const uint32_t sh1 = sh + 1;
-            const uint32_t d0 = sh1 == 4 ? v.y : __builtin_amdgcn_alignbyte(v.y, v.x, sh1);
-            const uint32_t d1 = sh1 == 4 ? v.z : __builtin_amdgcn_alignbyte(v.z, v.y, sh1);
-            const uint32_t d2 = sh1 == 4 ? v.w : __builtin_amdgcn_alignbyte(v.w, v.z, sh1);
-            const uint32_t d3 = sh1 == 4 ? w4 : __builtin_amdgcn_alignbyte(w4, v.w, sh1);
-            *reinterpret_cast<u32x4 *>(lds + S * STAGE + bpay[u]) = u32x4{d0, d1, d2, d3};
-            lds[S * STAGE + bscl[u]] = (uint8_t)(v.x >> (8 * sh));
+        for (int u = 0; u < RU; u++) {
+            if ((BN * 2 * OCT) % 256 == 0 || u + 1 < RU || rpay[u] != ~0u) {
+                const uint32_t o = S * P::RAW + rsrc[u], p = o + 1, sh = p & 3u;
+                const uint32_t *w = reinterpret_cast<const uint32_t *>(raw + (p & ~3u));
+                const uint32_t w0 = w[0], w1 = w[1], w2 = w[2], w3 = w[3], w4 = w[4];
+                *reinterpret_cast<u32x4 *>(aln + S * P::ALN + rpay[u]) =
+                    u32x4{__builtin_amdgcn_alignbyte(w1, w0, sh), __builtin_amdgcn_alignbyte(w2, w1, sh),
+                          __builtin_amdgcn_alignbyte(w3, w2, sh), __builtin_amdgcn_alignbyte(w4, w3, sh)};
+                aln[S * P::ALN + rscl[u]] = raw[o];
+            }
         }
     };
 
@@ -292,121 +341,135 @@ __global__ __launch_bounds__(256) void mx_matmul_kernel(KPRE_PARAMS, MxArgs a) {
 #pragma unroll
     for (int j = 0; j < CT; j++) acc[j] = f32x16{};
 
-    // B fragments: payload per step (double-buffered by parity), scales per
-    // double step (byte = step parity, chosen by op_sel).
+    // The stage's scale bytes of this lane's rows: 8 steps, byte L of word L / 4.
+    u32x2 sw[CT];
+    // Fragments of step L of aligned buffer S: read one step ahead of their
+    // MFMAs, so the LDS latency hides behind the previous step's.
     i32x8 bf[2][CT];
-    uint32_t sw[CT];
-    auto frag_read = [&](auto stage, auto par) {
-        constexpr int S = decltype(stage)::value, PA = decltype(par)::value;
-        const uint8_t *base = lds + S * STAGE;
+    auto frag = [&](auto buf, auto local) {
+        constexpr int S = decltype(buf)::value, L = decltype(local)::value;
 #pragma unroll
-        for (int j = 0; j < CT; j++) {
-            const u32x4 q = *reinterpret_cast<const u32x4 *>(base + ((2 * PA + part) * BN + wcol + j * 32 + c) * 16);
-            bf[PA][j] = i32x8{(int)q.x, (int)q.y, (int)q.z, (int)q.w, 0, 0, 0, 0};
-            if (PA == 0)
-                sw[j] = *reinterpret_cast<const uint32_t *>(base + P::PAY + (part * BN + wcol + j * 32 + c) * 4);
+        for (int t = 0; t < CT; t++) {
+            const u32x4 v = *reinterpret_cast<const u32x4 *>(aln + S * P::ALN +
+                                                             ((2 * L + part) * P::PROW + wcol + t * 32 + c) * 16);
+            bf[L & 1][t] = i32x8{(int)v.x, (int)v.y, (int)v.z, (int)v.w, 0, 0, 0, 0};
         }
     };
-    // Local K step s = 2 j + PA (A slot U): read step s + 1's payload (and,
-    // at the end of a double step, the next double step's scales) from LDS
-    // stage NS, then multiply step s.
-    auto step = [&](auto par, auto aslot, auto nstage, uint32_t s) {
-        constexpr int PA = decltype(par)::value, U = decltype(aslot)::value;
+    // Step s = 8 o + L of stage o (aligned buffer S).
+    auto step = [&](auto buf, auto local, uint32_t s) {
+        constexpr int S = decltype(buf)::value, L = decltype(local)::value;
+        if constexpr (L + 1 < OCT) frag(buf, Int<L + 1>{});
         if (s < nsteps) {
+            // A block past K (odd block count, last step): its weight scale
+            // byte may be E8M0 255 (NaN); the activations there are zero, so
+            // scale 1 keeps it out.
+            const bool dead = part && (nblk & 1) && s == nsteps - 1;
             uint32_t scl[CT];
 #pragma unroll
-            for (int j = 0; j < CT; j++) scl[j] = sw[j];
-            frag_read(nstage, Int<1 - PA>{});
-            // A block past K (odd block count, last step): its scale byte may be
-            // E8M0 255 (NaN); the activations there are zero, so scale 1 keeps it out.
-            const bool dead = part && (nblk & 1) && s == a.ksteps - 1;
+            for (int t = 0; t < CT; t++) scl[t] = dead ? 0x7f7f7f7fu : (L < 4 ? sw[t].x : sw[t].y);
+            constexpr int U = L % RA, B = L & 3;
 #pragma unroll
-            for (int j = 0; j < CT; j++) scl[j] = dead ? 0x7f7f7f7fu : scl[j];
-#if defined(OCO_ABL) && OCO_ABL == 5
+            for (int t = 0; t < CT; t++)
+                acc[t] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av[U][0], bf[L & 1][t], acc[t], 2, 4, 0,
+                                                                          (int)as[U], B, (int)scl[t]);
 #pragma unroll
-            for (int j = 0; j < CT; j++) acc[j][0] += __int_as_float(av[U][0][0] ^ av[U][1][7] ^ bf[PA][j][0] ^ bf[PA][j][3] ^ (int)scl[j] ^ (int)as[U]);
-            return;
-#endif
-#pragma unroll
-            for (int t = 0; t < 2; t++)
-#pragma unroll
-                for (int j = 0; j < CT; j++) {
-                    if (t == 0)
-                        acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av[U][0], bf[PA][j], acc[j], 0, 4, 0,
-                                                                                  (int)as[U], PA, (int)scl[j]);
-                    else
-                        acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av[U][1], bf[PA][j], acc[j], 0, 4, 1,
-                                                                                  (int)as[U], PA, (int)scl[j]);
-                }
+            for (int t = 0; t < CT; t++)
+                acc[t] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av[U][1], bf[L & 1][t], acc[t], 2, 4, 1,
+                                                                          (int)as[U], B, (int)scl[t]);
         }
+        (void)S;
     };
 
-    // Double step j (ring position Q = j mod PER): stage j % 3 holds B of j
-    // (steps 2j, 2j + 1) and stage (j + 1) % 3 B of j + 1 (read for step
-    // 2j + 2 before this round's barrier); B of j + 2 goes to stage
-    // (j + 2) % 3, last read before the previous barrier.
-    auto body = [&](auto q, uint32_t j) {
-        constexpr int Q = decltype(q)::value;
-        store_b(Int<(Q + 2) % RB>{}, Int<(Q + 2) % 3>{});
-        load_b(Int<(Q + 2) % RB>{}, j + 2 + RB);
-        step(Int<0>{}, Int<(2 * Q) % RA>{}, Int<Q % 3>{}, 2 * j);
-        load_a(Int<(2 * Q) % RA>{}, 2 * j + RA);
-        step(Int<1>{}, Int<(2 * Q + 1) % RA>{}, Int<(Q + 1) % 3>{}, 2 * j + 1);
-        load_a(Int<(2 * Q + 1) % RA>{}, 2 * j + 1 + RA);
+    auto body = [&](auto par, uint32_t o) {
+        constexpr int S = decltype(par)::value;
+        realign(Int<1 - S>{});
+        if (o + 2 < nst) store_b(Int<S>{}, Int<0>{});
+        // (no requests past the last stage: they would be HBM reads that
+        // the kernel's tail waits behind)
+        if (o + 3 < nst) load_b(Int<0>{}, o + 3);
+#pragma unroll
+        for (int t = 0; t < CT; t++)
+            sw[t] = *reinterpret_cast<const u32x2 *>(aln + S * P::ALN + P::PAY + (wcol + t * 32 + c) * 2 * OCT + part * OCT);
+        frag(Int<S>{}, Int<0>{});
+        static_for<OCT>([&](auto l) {
+            step(Int<S>{}, l, o * OCT + l.value);
+            load_a(Int<l.value % RA>{}, o * OCT + l.value + RA);
+        });
         __syncthreads();
     };
 
-    // Prologue, in the order the first steps need the data.
+    // Prologue: stages 0 and 1 requested together; stage 0 realigned,
+    // stage 1 raw in LDS, stage 2 in registers.
     load_b(Int<0>{}, 0);
-    load_b(Int<1>{}, 1);
+    if (nst > 1) load_b(Int<1>{}, 1);
     static_for<RA>([&](auto u) { load_a(u, u.value); });
-    static_for<RB - 2>([&](auto u) { load_b(Int<u.value + 2>{}, u.value + 2); });
     store_b(Int<0>{}, Int<0>{});
-    store_b(Int<1>{}, Int<1>{});
-    load_b(Int<0>{}, RB);
-    load_b(Int<1>{}, RB + 1);
+    if (nst > 2) load_b(Int<0>{}, 2);
     __syncthreads();
-    frag_read(Int<0>{}, Int<0>{});
-    const uint32_t nd = (nsteps + 1) / 2;
-    for (uint32_t j = 0; j < nd; j += PER)
-        static_for<PER>([&](auto q) { body(q, j + q.value); });
+    realign(Int<0>{});
+    if (nst > 1) store_b(Int<1>{}, Int<1>{});
+    __syncthreads();
+    for (uint32_t o = 0; o < nst; o += 2) {
+        body(Int<0>{}, o);
+        if (o + 1 < nst) body(Int<1>{}, o + 1);
+    }
 
-    if (tile >= a.tiles) return;
+    // Output: the tile goes through LDS (f32, [row][column], the raw
+    // buffers are free after the loop's last barrier), then out as rows of
+    // 4-column chunks -- contiguous 8- or 16-byte stores instead of one
+    // 2-byte store per accumulator.
+    float *ot = reinterpret_cast<float *>(lds);
+    constexpr int OROW = BN + 4;  // floats per LDS row (pad: rows 4 banks apart)
 #pragma unroll
-    for (int j = 0; j < CT; j++) {
-        const uint32_t col = col0 + wcol + j * 32 + c;
+    for (int j = 0; j < CT; j++)
+#pragma unroll
+        for (int v = 0; v < 16; v++)
+            ot[(wm * 32 + 8 * (v / 4) + 4 * part + (v % 4)) * OROW + wcol + j * 32 + c] = acc[j][v];
+    __syncthreads();
+    constexpr int CPR = BN / 4;  // chunks per row
+    const uint32_t rows = min((uint32_t)P::BM, a.m - min(a.m, by * P::BM));
+    for (uint32_t q = tid; q < rows * CPR; q += 256) {
+        const uint32_t r = q / CPR, cc = (q % CPR) * 4, col = col0 + cc;
         if (col >= a.n) continue;
-        const float bias = a.bias ? round_bf16(a.bias[col]) : 0.f;
+        float v[4];
 #pragma unroll
-        for (int v = 0; v < 16; v++) {
-            const uint32_t row = tile * 32 + 8 * (v / 4) + 4 * part + (v % 4);
-            if (row >= a.m) continue;
-            const float r = acc[j][v] + bias;
-            const uint64_t o = (uint64_t)row * a.n + col;
-            if (a.y_bf16)
-                reinterpret_cast<uint16_t *>(a.y)[o] = f32_to_bf16_bits(r);
-            else
-                reinterpret_cast<float *>(a.y)[o] = r;
+        for (int e = 0; e < 4; e++) v[e] = ot[r * OROW + cc + e];
+        if (a.bias) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) v[e] += col + e < a.n ? round_bf16(gp(a.bias)[col + e]) : 0.f;
+        }
+        const uint64_t o = (uint64_t)(by * P::BM + r) * a.n + col;
+        const bool whole = col + 4 <= a.n;
+        if (a.y_bf16) {
+            auto y = gp(reinterpret_cast<uint16_t *>(a.y) + o);
+            if (whole && (o & 3) == 0) {
+                *reinterpret_cast<__attribute__((address_space(1))) u32x2 *>(y) =
+                    u32x2{(uint32_t)f32_to_bf16_bits(v[0]) | ((uint32_t)f32_to_bf16_bits(v[1]) << 16),
+                          (uint32_t)f32_to_bf16_bits(v[2]) | ((uint32_t)f32_to_bf16_bits(v[3]) << 16)};
+            } else {
+                for (uint32_t e = 0; e < 4 && col + e < a.n; e++) y[e] = f32_to_bf16_bits(v[e]);
+            }
+        } else {
+            auto y = gp(reinterpret_cast<float *>(a.y) + o);
+            if (whole && (o & 3) == 0) {
+                *reinterpret_cast<__attribute__((address_space(1))) u32x4 *>(y) =
+                    u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])};
+            } else {
+                for (uint32_t e = 0; e < 4 && col + e < a.n; e++) y[e] = v[e];
+            }
         }
     }
 }
 
 // Tile plan of one call: wavefronts along the activation rows (WM) and
-// column tiles per wavefront (CTW).
+// column tiles per wavefront (CTW); 128 x 96 is the one that fits LDS with
+// both buffer pairs (192 columns would need 219 KB).
 struct MxTilePlan {
     int wm, ctw;
     uint32_t col_tiles, groups;
 };
 static MxTilePlan mx_plan(uint32_t m, uint32_t n) {
-    int wm = 4, ctw = 3;  // 128 x 96: measured fastest at 512 x 5760 x 2880
-    int32_t ov[4];
-    if (plan_override(OCO_KNOB_MX_TILE, ov) == 2) {
-        const int w2 = ov[0], c2 = ov[1];
-        if ((w2 == 2 || w2 == 4) && (c2 == 3 || c2 == 6)) {
-            wm = w2;
-            ctw = c2;
-        }
-    }
+    const int wm = 4, ctw = 3;  // 128 x 96: 240 workgroups at 512 x 5760
     MxTilePlan p;
     p.wm = wm;
     p.ctw = ctw;
@@ -423,8 +486,8 @@ uint64_t mx_workspace_bytes(uint32_t m, uint32_t n, uint32_t k) {
 
 template <int WM, int CTW>
 static MxFn mx_kernel_fn(size_t &lds) {
-    lds = (size_t)MxPlan<WM, CTW, 3>::LDS;
-    return mx_matmul_kernel<WM, CTW, 3>;
+    lds = (size_t)MxPlan<WM, CTW>::LDS;
+    return mx_matmul_kernel<WM, CTW>;
 }
 
 int mx_matmul_launch(const void *w, const void *x, void *y, bool y_bf16, const float *bias, uint32_t m, uint32_t n,
@@ -438,11 +501,10 @@ int mx_matmul_launch(const void *w, const void *x, void *y, bool y_bf16, const f
     sa.k = k;
     sa.ksteps = ksteps;
     sa.records = tiles * ksteps;
-    hipLaunchKernelGGL(mx_split_kernel, dim3(sa.records), dim3(256), 0, stream, KPRE_ARGS(sa), sa);
+    hipLaunchKernelGGL(mx_split_kernel, dim3(sa.records), dim3(64), 0, stream, KPRE_ARGS(sa), sa);
     OCO_TRY(launch_check("oco_matmul (mx split)"));
     size_t lds = 0;
-    MxFn fn = plan.wm == 2 ? (plan.ctw == 3 ? mx_kernel_fn<2, 3>(lds) : mx_kernel_fn<2, 6>(lds))
-                           : (plan.ctw == 3 ? mx_kernel_fn<4, 3>(lds) : mx_kernel_fn<4, 6>(lds));
+    MxFn fn = mx_kernel_fn<4, 3>(lds);
     if (lds > 64 * 1024)
         OCO_TRY(hip_check(hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
                           "hipFuncSetAttribute"));
@@ -458,7 +520,9 @@ int mx_matmul_launch(const void *w, const void *x, void *y, bool y_bf16, const f
     a.tiles = tiles;
     a.row_bytes = (k / 32) * 17;
     a.y_bf16 = y_bf16;
-    const uint64_t wspan = ((uint64_t)n * a.row_bytes + ((uintptr_t)w & 3u) + 3) & ~3ull;
+    // Bytes from the 16-byte aligned base through the last row, rounded up
+    // to a whole chunk (stage spans past the end read as zero).
+    const uint64_t wspan = ((uint64_t)n * a.row_bytes + ((uintptr_t)w & 15u) + 15) & ~15ull;
     if (wspan > 0xffffff00ull)
         return fail(OCO_ERR_UNSUPPORTED, "oco_matmul: MXFP4 weight of %llu bytes (4 GiB limit)",
                     (unsigned long long)wspan);
