@@ -195,12 +195,13 @@ int oco_matvec(uint32_t format, const void *w, const void *x, oco_dtype x_dtype,
 /* Y[m, n] = X[m, k] W^T (+ bias) on MFMA with fp32 accumulation.
  * Replaces DenseMatrix::apply's tiled plans (compute/matrix.rs:130-379,
  * `matmul`/`matmul_q4*`/`matmul_tensor_*`, batch.metal:24-79, tensor.metal:9-102).
- * Operands: MXFP4 weights and bf16 activations enter bf16 MFMA exactly;
- * other formats decode to f16 (the reference's half(w), tile.metal:16-80)
- * with activations converted to f16.  X is bf16 or f16 row-major; Y f32 or
- * bf16.  MXFP4 instead runs the block-scaled FP8 x FP4 MFMA on the GGUF bytes
- * as stored, with X split into two E4M3 terms (exact for bf16 inputs up to
- * 2^-8 of each residual block maximum); that split needs a workspace, which
+ * Operands: formats other than MXFP4 decode to f16 (the reference's
+ * half(w), tile.metal:16-80) with activations converted to f16.  X is bf16
+ * or f16 row-major; Y f32 or bf16.  MXFP4 runs the block-scaled FP6 x FP4
+ * MFMA on the GGUF bytes as stored, with each 32-block of X split into two
+ * E2M3 terms with their own E8M0 scales (at most 1/225 of the block maximum
+ * per value; relative L2 of the product a few 1e-4, inside the 2e-3 bound
+ * for bf16-activation MFMA prefill); that split needs a workspace, which
  * oco_matmul takes from the stream-ordered pool (hipMallocAsync). */
 int oco_matmul(uint32_t format, const void *w, const void *x, oco_dtype x_dtype, void *y,
                oco_dtype y_dtype, const float *bias, const oco_matrix *p, oco_stream stream);
