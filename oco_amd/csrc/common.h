@@ -87,6 +87,28 @@ __device__ __forceinline__ uint4 ld_u128(const uint8_t *p) {
     return v;
 }
 
+// The same loads through global-address-space pointers (gp below): global
+// instructions instead of FLAT ones.  A FLAT load counts in lgkmcnt as well
+// as vmcnt, so in a kernel that also uses LDS every wait for an LDS read
+// waits for the FLAT loads issued before it -- weight prefetches included.
+#define GLOBAL __attribute__((address_space(1)))
+typedef const GLOBAL uint8_t *gbytes;
+typedef uint16_t u16_u __attribute__((aligned(1)));
+typedef uint32_t u32_u __attribute__((aligned(1)));
+typedef uint32_t u32x2_u __attribute__((ext_vector_type(2), aligned(1)));
+typedef uint32_t u32x4_u __attribute__((ext_vector_type(4), aligned(1)));
+__device__ __forceinline__ uint32_t ld_u8(gbytes p) { return *p; }
+__device__ __forceinline__ uint32_t ld_u16(gbytes p) { return *(const GLOBAL u16_u *)p; }
+__device__ __forceinline__ uint32_t ld_u32(gbytes p) { return *(const GLOBAL u32_u *)p; }
+__device__ __forceinline__ uint2 ld_u64(gbytes p) {
+    const u32x2_u v = *(const GLOBAL u32x2_u *)p;
+    return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ uint4 ld_u128(gbytes p) {
+    const u32x4_u v = *(const GLOBAL u32x4_u *)p;
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // Streamed weight bytes are read through a buffer resource: loads carry the
 // nontemporal hint (read once per call, so they should not displace the
 // activations from L2/MALL), accept any byte offset, and return zero past

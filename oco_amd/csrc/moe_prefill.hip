@@ -165,8 +165,8 @@ __device__ __forceinline__ void q4_touch(const uint4 &v) {
 
 // 16 bytes per lane from global memory straight into LDS: lane l writes
 // lds + 16 l (global_load_lds_dwordx4; lds must be uniform).
-__device__ __forceinline__ void q4_load_lds16(const void *src, void *lds) {
-    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)lds, 16, 0, 0);
+__device__ __forceinline__ void q4_load_lds16(gbytes src, void *lds) {
+    __builtin_amdgcn_global_load_lds((const GLOBAL void *)src, (__attribute__((address_space(3))) void *)lds, 16, 0, 0);
 }
 
 
@@ -191,7 +191,8 @@ __global__ __launch_bounds__(64 * NW) void moe_q4k_kernel(KPRE_PARAMS, MatmulArg
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c16 = lane & 15, q = lane >> 4;
     const uint32_t grid = gridDim.x, lg = xcd_order(blockIdx.x, grid);
-    const uint32_t U = a.plan[1] * chunks;
+    const auto plan = gp(a.plan);
+    const uint32_t U = plan[1] * chunks;
     const uint32_t lo = (uint32_t)((uint64_t)lg * U / grid), hi = (uint32_t)((uint64_t)(lg + 1) * U / grid);
     if (lo >= hi) return;  // uniform
     const uint32_t y0 = lo / chunks, ny = (hi - 1) / chunks - y0 + 1;  // <= Q4_TILES (launch)
@@ -205,13 +206,13 @@ __global__ __launch_bounds__(64 * NW) void moe_q4k_kernel(KPRE_PARAMS, MatmulArg
         const uint32_t ti = tid / ROWS, r = tid % ROWS;
         if (ti < ny) {
             const uint32_t y = y0 + ti;
-            const uint32_t expert = a.plan[6 + 2 * y], first = a.plan[7 + 2 * y];
+            const uint32_t expert = plan[6 + 2 * y], first = plan[7 + 2 * y];
             const uint64_t list = grouped + (uint64_t)expert * (a.routes + 1);
-            const uint32_t rows = min((uint32_t)ROWS, a.plan[list] - first);
-            const uint32_t sorted0 = a.plan[sorted + expert] + first;
+            const uint32_t rows = min((uint32_t)ROWS, plan[list] - first);
+            const uint32_t sorted0 = plan[sorted + expert] + first;
             const uint32_t rr = min(r, rows - 1);  // padding rows repeat the last row (discarded)
-            t_route[ti][r] = a.plan[list + 1 + first + rr];
-            if constexpr (G == MM_DOWN) t_inv[ti][r] = 1.0f / row_gain(a.rowmax[sorted0 + rr]);
+            t_route[ti][r] = plan[list + 1 + first + rr];
+            if constexpr (G == MM_DOWN) t_inv[ti][r] = 1.0f / row_gain(gp(a.rowmax)[sorted0 + rr]);
             if (r == 0) {
                 t_info[ti][0] = expert;
                 t_info[ti][1] = rows;
@@ -223,17 +224,17 @@ __global__ __launch_bounds__(64 * NW) void moe_q4k_kernel(KPRE_PARAMS, MatmulArg
     // the up bias folds in the clipped SwiGLU's + 1).
     for (uint32_t e = tid; e < nu * 2 * 16 * NW; e += 64 * NW) {
         const uint32_t j = e / (2 * 16 * NW), c = e % (2 * 16 * NW), u = lo + j, y = u / chunks, ch = u - y * chunks;
-        const uint32_t expert = a.plan[6 + 2 * y];
+        const uint32_t expert = plan[6 + 2 * y];
         float b = 0.f;
         if constexpr (G == MM_GATE_UP) {
             const bool up = c >= 16 * NW;
             const uint32_t col = ch * (NW * COLS) + c % (16 * NW);
             const float *bias = up ? a.bias2 : a.bias;
             const float one = up && a.up_one ? 1.0f : 0.0f;
-            b = col < a.n && bias ? round_bf16(bias[(uint64_t)expert * a.n + col] + one) : one;
+            b = col < a.n && bias ? round_bf16(gp(bias)[(uint64_t)expert * a.n + col] + one) : one;
         } else {
             const uint32_t col = ch * (NW * COLS) + c;
-            b = col < a.n && a.bias ? round_bf16(a.bias[(uint64_t)expert * a.n + col]) : 0.f;
+            b = col < a.n && a.bias ? round_bf16(gp(a.bias)[(uint64_t)expert * a.n + col]) : 0.f;
         }
         u_bias[j][c] = b;
     }
@@ -241,12 +242,12 @@ __global__ __launch_bounds__(64 * NW) void moe_q4k_kernel(KPRE_PARAMS, MatmulArg
 
     const uint32_t nsb = a.k / 256, T = nu * nsb;
     const uint64_t xrow = (uint64_t)a.k * 2;
-    const uint8_t *x8 = reinterpret_cast<const uint8_t *>(a.x);
+    const gbytes x8 = gp(reinterpret_cast<const uint8_t *>(a.x));
 
     // Prefetch cursor: unit pu, super-block psb; per-lane source offsets.
     uint32_t pu = lo, psb = 0;
     uint32_t xoff[XL];
-    const uint8_t *wrow[2];
+    gbytes wrow[2];
     auto set_unit = [&](uint32_t u) __attribute__((always_inline)) {
         const uint32_t y = u / chunks, ch = u - y * chunks, ti = y - y0;
         const uint32_t expert = __builtin_amdgcn_readfirstlane(t_info[ti][0]);
@@ -261,7 +262,7 @@ __global__ __launch_bounds__(64 * NW) void moe_q4k_kernel(KPRE_PARAMS, MatmulArg
 #pragma unroll
         for (int f = 0; f < 2; f++) {
             const uint32_t col = ch * (NW * COLS) + wave * COLS + (G == MM_GATE_UP ? 0 : 16 * f) + c16;
-            const uint8_t *base = (G == MM_GATE_UP && f == 1 ? a.w2 : a.w) + (uint64_t)expert * a.expert_bytes;
+            const gbytes base = gp((G == MM_GATE_UP && f == 1 ? a.w2 : a.w) + (uint64_t)expert * a.expert_bytes);
             wrow[f] = base + (uint64_t)min(col, a.n - 1) * a.row_bytes;
         }
     };
@@ -275,7 +276,7 @@ __global__ __launch_bounds__(64 * NW) void moe_q4k_kernel(KPRE_PARAMS, MatmulArg
         constexpr int K = decltype(kk)::value;
         if constexpr (K < 6) {
             constexpr int f = K / 3, part = K % 3;
-            const uint8_t *blk = wrow[f] + psb * 144;
+            const gbytes blk = wrow[f] + psb * 144;
             if constexpr (part == 0) wn[f].hdr = ld_u128(blk);
             if constexpr (part == 1) wn[f].q0 = ld_u128(blk + 16 + 32 * q);
             if constexpr (part == 2) wn[f].q1 = ld_u128(blk + 32 + 32 * q);
@@ -343,7 +344,7 @@ __global__ __launch_bounds__(64 * NW) void moe_q4k_kernel(KPRE_PARAMS, MatmulArg
                 for (int v = 0; v < 4; v++) {
                     const uint32_t r = i * 16 + cr + v;
                     const float act = expert_activation(a.act, acc[i][0][v] + bg, acc[i][1][v] + bu);
-                    if (cok && r < rows) reinterpret_cast<float *>(a.y)[(uint64_t)(sorted0 + r) * a.n + col] = act;
+                    if (cok && r < rows) gp(reinterpret_cast<float *>(a.y))[(uint64_t)(sorted0 + r) * a.n + col] = act;
                     if (cok) rmax[i][v] = max(rmax[i][v], __float_as_uint(act) & 0x7fffffffu);
                 }
             // Row maxima go out once per (workgroup, tile): after the tile's
@@ -388,9 +389,9 @@ __global__ __launch_bounds__(64 * NW) void moe_q4k_kernel(KPRE_PARAMS, MatmulArg
                         const float val = acc[i][f][v] * __uint_as_float(ig[i][v]) + b;
                         const uint64_t o = (uint64_t)rt[i][v] * a.n + col;
                         if (a.y_bf16)
-                            reinterpret_cast<uint16_t *>(a.y)[o] = f32_to_bf16_bits(val);
+                            gp(reinterpret_cast<uint16_t *>(a.y))[o] = f32_to_bf16_bits(val);
                         else
-                            reinterpret_cast<float *>(a.y)[o] = val;
+                            gp(reinterpret_cast<float *>(a.y))[o] = val;
                     }
             }
         }

@@ -229,16 +229,21 @@ struct MxPlan {
     static constexpr int OCT = 8;     // K steps per B stage
     static constexpr int CH = 18;     // 16-byte chunks per row and stage
     static constexpr int RSTR = 296;  // raw LDS bytes per row (18 chunks + pad)
-    static constexpr int BU = (BN * CH + 255) / 256;        // chunk slots per thread
-    static constexpr int RU = (BN * 2 * OCT + 255) / 256;   // realigned blocks per thread
+    static constexpr int NTH = 512;                          // threads: two wavefronts per (row tile, columns)
+    static constexpr int BU = (BN * CH + NTH - 1) / NTH;      // chunk slots per thread
+    static constexpr int RU = (BN * 2 * OCT + NTH - 1) / NTH; // realigned blocks per thread
     static constexpr int PROW = BN + 1;                     // payload slots per block row
     static constexpr int RAW = BN * RSTR, PAY = 2 * OCT * PROW * 16, SCL = BN * 2 * OCT;
     static constexpr int ALN = PAY + SCL;
-    static constexpr int LDS = 2 * RAW + 2 * ALN, RA = 8;
+    static constexpr int LDS = 2 * RAW + 2 * ALN;
+    static constexpr int RA = 2;  // A ring: this wavefront's next two own steps (four K steps ahead)
+    static_assert((OCT / 2) % RA == 0, "ring slots repeat every stage");
+    static constexpr int RED = 4 * CTW * 16 * 64 * 4, OROW = BN + 4, OUT = BM * OROW * 4;
+    static_assert(RED + OUT <= LDS, "the K-half sums and the output tile fit the stage buffers");
 };
 
 template <int WM, int CTW>
-__global__ __launch_bounds__(256) void mx_matmul_kernel(KPRE_PARAMS, MxArgs a) {
+__global__ __launch_bounds__(512) void mx_matmul_kernel(KPRE_PARAMS, MxArgs a) {
     KPRE_APPLY(a);
     using P = MxPlan<WM, CTW>;
     constexpr int BN = P::BN, BU = P::BU, RU = P::RU, RA = P::RA, CT = CTW, OCT = P::OCT;
@@ -247,7 +252,9 @@ __global__ __launch_bounds__(256) void mx_matmul_kernel(KPRE_PARAMS, MxArgs a) {
     // The wavefront index is uniform: readfirstlane keeps the A resource in SGPRs.
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, c = lane & 31,
               part = lane >> 5;
-    const int wm = wave % WM, wn = wave / WM;
+    // Wavefronts w and w + 4 share a row tile and its column tiles: kw = 0
+    // takes the even steps of every stage, kw = 1 the odd ones.
+    const int kw = wave >> 2, w4 = wave & 3, wm = w4 % WM, wn = w4 / WM;
     // Logical (column tile, row group), column-major per XCD: the row groups
     // of one weight column tile share its GGUF bytes in one L2.
     const uint32_t lin = xcd_order(blockIdx.x + gridDim.x * blockIdx.y, gridDim.x * gridDim.y);
@@ -262,22 +269,22 @@ __global__ __launch_bounds__(256) void mx_matmul_kernel(KPRE_PARAMS, MxArgs a) {
     const uint32_t wsh = (uint32_t)((uintptr_t)a.w & 15u);
     const __amdgpu_buffer_rsrc_t rb_rs = uniform_rsrc(a.w - wsh, a.wspan);
     const uint32_t rbytes = (uint32_t)a.row_bytes;
-    // Chunk slot q = tid + 256 u: chunk q % 18 of tile row q / 18 (rows past
+    // Chunk slot q = tid + 512 u: chunk q % 18 of tile row q / 18 (rows past
     // n repeat row n - 1 and are never stored).
     uint32_t boff[BU], bdst[BU];
 #pragma unroll
     for (int u = 0; u < BU; u++) {
-        const uint32_t q = tid + 256 * u, row = min(q / P::CH, (uint32_t)BN - 1), ch = q % P::CH;
+        const uint32_t q = tid + P::NTH * u, row = min(q / P::CH, (uint32_t)BN - 1), ch = q % P::CH;
         const bool live = q < (uint32_t)(BN * P::CH);
         boff[u] = live ? ((wsh + min(col0 + row, a.n - 1) * rbytes) & ~15u) + 16 * ch : 0u;
         bdst[u] = live ? row * P::RSTR + 16 * ch : ~0u;  // ~0: no slot (the last round's spare threads)
     }
-    // Realign slot r = tid + 256 u: block r / BN of tile row r % BN; its
+    // Realign slot r = tid + 512 u: block r / BN of tile row r % BN; its
     // scale byte sits at rsrc in the raw buffer, its payload right after.
     uint32_t rsrc[RU], rpay[RU], rscl[RU];
 #pragma unroll
     for (int u = 0; u < RU; u++) {
-        const uint32_t r = tid + 256 * u, row = r % BN, blk = r / BN;
+        const uint32_t r = tid + P::NTH * u, row = r % BN, blk = r / BN;
         const bool live = r < (uint32_t)(BN * 2 * OCT);
         rsrc[u] = row * P::RSTR + ((wsh + min(col0 + row, a.n - 1) * rbytes) & 15u) + 17 * blk;
         rpay[u] = live ? (blk * P::PROW + row) * 16 : ~0u;
@@ -299,22 +306,19 @@ __global__ __launch_bounds__(256) void mx_matmul_kernel(KPRE_PARAMS, MxArgs a) {
         }
         as[U] = __builtin_amdgcn_raw_buffer_load_b32(ra_rs, MX_DATA + lane * 4, so, 0);
     };
-    // B chunks of stage o (steps 8 o .. 8 o + 7) into register set V.
+    // B chunks of stage o (steps 8 o .. 8 o + 7).
     const uint32_t nst = (nsteps + OCT - 1) / OCT;
-    u32x4 bw[BU];  // the prologue's second set
-    auto load_b = [&](auto set, uint32_t o) {
-        u32x4 *v = decltype(set)::value ? bw : bv;
+    auto load_b = [&](uint32_t o) {
 #pragma unroll
-        for (int u = 0; u < BU; u++) v[u] = __builtin_amdgcn_raw_buffer_load_b128(rb_rs, boff[u], o * 272, 0);
+        for (int u = 0; u < BU; u++) bv[u] = __builtin_amdgcn_raw_buffer_load_b128(rb_rs, boff[u], o * 272, 0);
     };
-    auto store_b = [&](auto buf, auto set) {
+    auto store_b = [&](auto buf) {
         constexpr int S = decltype(buf)::value;
-        const u32x4 *v = decltype(set)::value ? bw : bv;
 #pragma unroll
         for (int u = 0; u < BU; u++) {
-            if ((BN * P::CH) % 256 == 0 || u + 1 < BU || bdst[u] != ~0u) {
-                *reinterpret_cast<u32x2 *>(raw + S * P::RAW + bdst[u]) = u32x2{v[u].x, v[u].y};
-                *reinterpret_cast<u32x2 *>(raw + S * P::RAW + bdst[u] + 8) = u32x2{v[u].z, v[u].w};
+            if ((BN * P::CH) % P::NTH == 0 || u + 1 < BU || bdst[u] != ~0u) {
+                *reinterpret_cast<u32x2 *>(raw + S * P::RAW + bdst[u]) = u32x2{bv[u].x, bv[u].y};
+                *reinterpret_cast<u32x2 *>(raw + S * P::RAW + bdst[u] + 8) = u32x2{bv[u].z, bv[u].w};
             }
         }
     };
@@ -323,7 +327,7 @@ __global__ __launch_bounds__(256) void mx_matmul_kernel(KPRE_PARAMS, MxArgs a) {
         constexpr int S = decltype(buf)::value;
 #pragma unroll
         for (int u = 0; u < RU; u++) {
-            if ((BN * 2 * OCT) % 256 == 0 || u + 1 < RU || rpay[u] != ~0u) {
+            if ((BN * 2 * OCT) % P::NTH == 0 || u + 1 < RU || rpay[u] != ~0u) {
                 const uint32_t o = S * P::RAW + rsrc[u], p = o + 1, sh = p & 3u;
                 const uint32_t *w = reinterpret_cast<const uint32_t *>(raw + (p & ~3u));
                 const uint32_t w0 = w[0], w1 = w[1], w2 = w[2], w3 = w[3], w4 = w[4];
@@ -343,8 +347,8 @@ __global__ __launch_bounds__(256) void mx_matmul_kernel(KPRE_PARAMS, MxArgs a) {
 
     // The stage's scale bytes of this lane's rows: 8 steps, byte L of word L / 4.
     u32x2 sw[CT];
-    // Fragments of step L of aligned buffer S: read one step ahead of their
-    // MFMAs, so the LDS latency hides behind the previous step's.
+    // Fragments of step L of aligned buffer S, read one own step (two steps)
+    // ahead of their MFMAs, into set (L / 2) & 1.
     i32x8 bf[2][CT];
     auto frag = [&](auto buf, auto local) {
         constexpr int S = decltype(buf)::value, L = decltype(local)::value;
@@ -352,13 +356,13 @@ __global__ __launch_bounds__(256) void mx_matmul_kernel(KPRE_PARAMS, MxArgs a) {
         for (int t = 0; t < CT; t++) {
             const u32x4 v = *reinterpret_cast<const u32x4 *>(aln + S * P::ALN +
                                                              ((2 * L + part) * P::PROW + wcol + t * 32 + c) * 16);
-            bf[L & 1][t] = i32x8{(int)v.x, (int)v.y, (int)v.z, (int)v.w, 0, 0, 0, 0};
+            bf[(L / 2) & 1][t] = i32x8{(int)v.x, (int)v.y, (int)v.z, (int)v.w, 0, 0, 0, 0};
         }
     };
-    // Step s = 8 o + L of stage o (aligned buffer S).
+    // Step s = 8 o + L of stage o (aligned buffer S), A ring slot (L / 2) % RA.
     auto step = [&](auto buf, auto local, uint32_t s) {
         constexpr int S = decltype(buf)::value, L = decltype(local)::value;
-        if constexpr (L + 1 < OCT) frag(buf, Int<L + 1>{});
+        if constexpr (L + 2 < OCT) frag(buf, Int<L + 2>{});
         if (s < nsteps) {
             // A block past K (odd block count, last step): its weight scale
             // byte may be E8M0 255 (NaN); the activations there are zero, so
@@ -367,68 +371,90 @@ __global__ __launch_bounds__(256) void mx_matmul_kernel(KPRE_PARAMS, MxArgs a) {
             uint32_t scl[CT];
 #pragma unroll
             for (int t = 0; t < CT; t++) scl[t] = dead ? 0x7f7f7f7fu : (L < 4 ? sw[t].x : sw[t].y);
-            constexpr int U = L % RA, B = L & 3;
+            constexpr int U = (L / 2) % RA, B = L & 3, F = (L / 2) & 1;
 #pragma unroll
             for (int t = 0; t < CT; t++)
-                acc[t] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av[U][0], bf[L & 1][t], acc[t], 2, 4, 0,
+                acc[t] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av[U][0], bf[F][t], acc[t], 2, 4, 0,
                                                                           (int)as[U], B, (int)scl[t]);
 #pragma unroll
             for (int t = 0; t < CT; t++)
-                acc[t] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av[U][1], bf[L & 1][t], acc[t], 2, 4, 1,
+                acc[t] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av[U][1], bf[F][t], acc[t], 2, 4, 1,
                                                                           (int)as[U], B, (int)scl[t]);
         }
         (void)S;
     };
-
+    // Stage o: realign raw stage o + 1; write stage o + 2's chunks to the
+    // other raw buffer; request stage o + 3's; then this wavefront's four
+    // steps of stage o (parity kw), each followed by the A request of the
+    // same step one stage ahead.
     auto body = [&](auto par, uint32_t o) {
         constexpr int S = decltype(par)::value;
         realign(Int<1 - S>{});
-        if (o + 2 < nst) store_b(Int<S>{}, Int<0>{});
+        if (o + 2 < nst) store_b(Int<S>{});
         // (no requests past the last stage: they would be HBM reads that
         // the kernel's tail waits behind)
-        if (o + 3 < nst) load_b(Int<0>{}, o + 3);
+        if (o + 3 < nst) load_b(o + 3);
 #pragma unroll
         for (int t = 0; t < CT; t++)
             sw[t] = *reinterpret_cast<const u32x2 *>(aln + S * P::ALN + P::PAY + (wcol + t * 32 + c) * 2 * OCT + part * OCT);
-        frag(Int<S>{}, Int<0>{});
-        static_for<OCT>([&](auto l) {
-            step(Int<S>{}, l, o * OCT + l.value);
-            load_a(Int<l.value % RA>{}, o * OCT + l.value + RA);
-        });
+        if (kw == 0) {
+            frag(Int<S>{}, Int<0>{});
+            static_for<OCT / 2>([&](auto i) {
+                step(Int<S>{}, Int<2 * i.value>{}, o * OCT + 2 * i.value);
+                load_a(Int<i.value % RA>{}, o * OCT + 2 * (i.value + RA));
+            });
+        } else {
+            frag(Int<S>{}, Int<1>{});
+            static_for<OCT / 2>([&](auto i) {
+                step(Int<S>{}, Int<2 * i.value + 1>{}, o * OCT + 2 * i.value + 1);
+                load_a(Int<i.value % RA>{}, o * OCT + 2 * (i.value + RA) + 1);
+            });
+        }
         __syncthreads();
     };
 
-    // Prologue: stages 0 and 1 requested together; stage 0 realigned,
-    // stage 1 raw in LDS, stage 2 in registers.
-    load_b(Int<0>{}, 0);
-    if (nst > 1) load_b(Int<1>{}, 1);
-    static_for<RA>([&](auto u) { load_a(u, u.value); });
-    store_b(Int<0>{}, Int<0>{});
-    if (nst > 2) load_b(Int<0>{}, 2);
+    // Prologue: stage 0 realigned, stage 1 raw in LDS, stage 2 in registers.
+    load_b(0);
+    static_for<RA>([&](auto u) { load_a(u, 2 * u.value + kw); });
+    store_b(Int<0>{});
+    if (nst > 1) load_b(1);
     __syncthreads();
     realign(Int<0>{});
-    if (nst > 1) store_b(Int<1>{}, Int<1>{});
+    if (nst > 1) store_b(Int<1>{});
+    if (nst > 2) load_b(2);
     __syncthreads();
     for (uint32_t o = 0; o < nst; o += 2) {
         body(Int<0>{}, o);
         if (o + 1 < nst) body(Int<1>{}, o + 1);
     }
 
-    // Output: the tile goes through LDS (f32, [row][column], the raw
-    // buffers are free after the loop's last barrier), then out as rows of
+    // The odd-step wavefronts hand their sums to the even-step ones, which
+    // put the tile in LDS (f32, [row][column]; the stage buffers are free
+    // after the loop's last barrier); then all threads store it as rows of
     // 4-column chunks -- contiguous 8- or 16-byte stores instead of one
     // 2-byte store per accumulator.
-    float *ot = reinterpret_cast<float *>(lds);
-    constexpr int OROW = BN + 4;  // floats per LDS row (pad: rows 4 banks apart)
+    float *red = reinterpret_cast<float *>(lds);
+    float *ot = reinterpret_cast<float *>(lds + P::RED);
+    constexpr int OROW = P::OROW;  // floats per LDS row (pad: rows 4 banks apart)
+    if (kw == 1) {
 #pragma unroll
-    for (int j = 0; j < CT; j++)
+        for (int j = 0; j < CT; j++)
 #pragma unroll
-        for (int v = 0; v < 16; v++)
-            ot[(wm * 32 + 8 * (v / 4) + 4 * part + (v % 4)) * OROW + wcol + j * 32 + c] = acc[j][v];
+            for (int v = 0; v < 16; v++) red[((w4 * CT + j) * 16 + v) * 64 + lane] = acc[j][v];
+    }
+    __syncthreads();
+    if (kw == 0) {
+#pragma unroll
+        for (int j = 0; j < CT; j++)
+#pragma unroll
+            for (int v = 0; v < 16; v++)
+                ot[(wm * 32 + 8 * (v / 4) + 4 * part + (v % 4)) * OROW + wcol + j * 32 + c] =
+                    acc[j][v] + red[((w4 * CT + j) * 16 + v) * 64 + lane];
+    }
     __syncthreads();
     constexpr int CPR = BN / 4;  // chunks per row
     const uint32_t rows = min((uint32_t)P::BM, a.m - min(a.m, by * P::BM));
-    for (uint32_t q = tid; q < rows * CPR; q += 256) {
+    for (uint32_t q = tid; q < rows * CPR; q += P::NTH) {
         const uint32_t r = q / CPR, cc = (q % CPR) * 4, col = col0 + cc;
         if (col >= a.n) continue;
         float v[4];
@@ -527,7 +553,7 @@ int mx_matmul_launch(const void *w, const void *x, void *y, bool y_bf16, const f
         return fail(OCO_ERR_UNSUPPORTED, "oco_matmul: MXFP4 weight of %llu bytes (4 GiB limit)",
                     (unsigned long long)wspan);
     a.wspan = (uint32_t)wspan;
-    hipLaunchKernelGGL(fn, dim3(plan.col_tiles, plan.groups), dim3(256), lds, stream, KPRE_ARGS(a), a);
+    hipLaunchKernelGGL(fn, dim3(plan.col_tiles, plan.groups), dim3(MxPlan<4, 3>::NTH), lds, stream, KPRE_ARGS(a), a);
     return launch_check("oco_matmul (mx)");
 }
 
