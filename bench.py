@@ -538,7 +538,8 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16 MFMA, f32 accumulation" if is_flops else "f32",
+        "dtype": ("fp6 x fp4 block-scaled MFMA (bf16 activations as two E2M3 terms), f32 accumulation"
+                  if is_flops and getattr(wl, "fmt", None) == 39 else "f16 MFMA, f32 accumulation" if is_flops else "f32"),
         "data": "synthetic (seeded GGUF-layout weights, N(0,1) activations)",
         "config": {"workload": wl.name, "format": getattr(wl, "fmt", None), "n": getattr(wl, "n", None),
                    "k": getattr(wl, "k", None), "batch": getattr(wl, "m", getattr(wl, "tokens", 1)),

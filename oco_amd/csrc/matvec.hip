@@ -184,6 +184,7 @@ struct DirectOk<OCO_Q5_K> {
     static constexpr bool value = true;
 };
 
+
 // DIRECT (Q4_K / Q5_K on a 16-byte aligned base, whose blocks are then all
 // 16-byte aligned): each lane loads its pieces' 16-byte chunks straight into
 // registers, with no LDS tile and no realignment.
@@ -256,7 +257,10 @@ __global__ __launch_bounds__(256) void stream_kernel(const uint8_t *w_, const vo
     typename T::Raw da[DIRECT ? NPL : 1], db[DIRECT ? NPL : 1], dc[DIRECT ? NPL : 1];
     __amdgpu_buffer_rsrc_t rall;
     if constexpr (DIRECT) {
-        const uint64_t bytes = (uint64_t)p.n * a.row_bytes;
+        // The range ends at a whole dword: a block's dword-aligned span may
+        // end up to three bytes past the tensor, and a dword that straddles
+        // the range end would read as zero (the same page holds it).
+        const uint64_t bytes = ((uint64_t)p.n * a.row_bytes + 3) & ~3ull;
         rall = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(ebase), 0,
                                                  (uint32_t)(bytes > 0xffffffffull ? 0xffffffffull : bytes), 0x00020000);
     }
