@@ -186,16 +186,6 @@ __device__ __forceinline__ void static_for(F &&f) {
 
 typedef void (*MxFn)(u32x4, u32x4, u32x4, u32x2, MxArgs);
 
-// A buffer resource the compiler keeps in SGPRs: every field goes through
-// readfirstlane (the values are uniform; without this a resource built next
-// to divergent code may land in VGPRs and every load becomes a waterfall loop).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void *p, uint32_t bytes) {
-    const uint64_t v = (uint64_t)(uintptr_t)p;
-    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-    return __builtin_amdgcn_make_buffer_rsrc((void *)(uintptr_t)(((uint64_t)hi << 32) | lo), 0,
-                                             __builtin_amdgcn_readfirstlane(bytes), 0x00020000);
-}
-
 // ---------------------------------------------------------------------------
 // Prefill tile: workgroup = four wavefronts, WM along the activation rows
 // and 4 / WM along the weight rows (output columns); each wavefront owns one
