@@ -416,9 +416,27 @@ uint64_t oco_experts_workspace(const oco_experts *w, uint32_t tokens) {
 // selected on the device (ids/probs are written): at one token inside the
 // routed gate/up kernel (expert_expand's selection), else inside the route
 // plan's launch.
+// The MXFP4 tiles at a small decode batch: every gate/up workgroup builds
+// the route plan itself (route.h), the input rows are split beside the
+// router logits, or by a launch of their own without a router.
+static bool mx_small_path(const oco_experts *w, uint32_t tokens) {
+    int32_t ov[4];
+    const uint32_t mx_tokens = plan_override(OCO_KNOB_MOE_MX_TOKENS, ov) ? (uint32_t)ov[0] : MOE_MX_TOKENS;
+    return w->format == OCO_MXFP4 && w->hidden % 32 == 0 && w->ffn % 32 == 0 && tokens >= mx_tokens &&
+           small_plan_fits(tokens, tokens * w->k, w->experts);
+}
+
+// The input rows' split records in the workspace (MXFP4 banks).
+static uint8_t *mx_xrec(const oco_experts *w, uint8_t *ws, uint32_t tokens) {
+    const uint32_t routes = tokens * w->k;
+    return ws + align256(oco_route_plan_words(routes, w->experts) * 4) + align256((uint64_t)routes * w->ffn * 4) +
+           align256((uint64_t)tokens * w->hidden * 2) + align256((uint64_t)routes * 4) +
+           align256((uint64_t)routes * w->hidden * 4);
+}
+
 static int experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype, uint32_t *ids, float *probs,
                          const float *logits, uint32_t tokens, uint16_t *out, float *routed, void *workspace,
-                         uint64_t workspace_bytes, hipStream_t s, const char *who) {
+                         uint64_t workspace_bytes, hipStream_t s, const char *who, bool split_done = false) {
     OCO_TRY(check_bank(w, true));
     if (!tokens) return OCO_OK;
     if (!x || !ids || !probs || !out || !workspace) return fail(OCO_ERR_INVALID, "%s: null pointer", who);
@@ -430,7 +448,8 @@ static int experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype,
     oco_stream stream = (oco_stream)s;
     // Selection inside the gate/up kernel covers one token over <= 64 experts;
     // otherwise it runs in the route plan's workgroup, before the plan.
-    const bool fused_select = logits && tokens == 1 && w->experts <= 64;
+    const bool small = mx_small_path(w, tokens);
+    const bool fused_select = logits && tokens == 1 && w->experts <= 64 && !small;
     PlanSide sel = {};
 #if defined(OCO_ABL) && OCO_ABL == 4
     if (logits && !fused_select) OCO_TRY(oco_route_select(logits, tokens, w->experts, w->k, ids, probs, stream));
@@ -451,7 +470,7 @@ static int experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype,
     uint32_t *rowmax = (uint32_t *)((uint8_t *)x16 + align256((uint64_t)tokens * w->hidden * 2));
     uint8_t *own_down = (uint8_t *)rowmax + align256((uint64_t)routes * 4);
     float *down = routed ? routed : (float *)own_down;
-    uint8_t *xrec = own_down + align256((uint64_t)routes * w->hidden * 4);  // MXFP4 only
+    uint8_t *xrec = mx_xrec(w, ws, tokens);  // MXFP4 only (just past the route outputs)
     uint8_t *arec = xrec + align256(mx_rows_bytes(tokens, w->hidden, 3));
     uint16_t *act16 = (uint16_t *)xrec;  // Q4_K only (in place of the MXFP4 splits)
 
@@ -469,15 +488,28 @@ static int experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype,
         // split by the gate/up tiles themselves.
         const int xterms = x_dtype == OCO_DT_BF16 ? 2 : 3;  // bf16 rows are exact in two terms
         uint32_t *desc = (uint32_t *)(arec + align256(mx_rows_bytes(routes, w->ffn, 3)));
-        PlanSide side = sel;
-        side.desc = desc;
-        side.x = x;
-        side.x_bf16 = x_dtype == OCO_DT_BF16 ? 1u : 0u;
-        side.rec = xrec;
-        side.rows = tokens;
-        side.k = w->hidden;
-        OCO_TRY(route_plan_launch(ids, routes, w->experts, tile_rows, 0, 0, plan, &side, s));
         MatmulArgs g = {};
+        if (small) {
+            if (!split_done)
+                OCO_TRY(router_logits_launch(x, x_dtype, nullptr, nullptr, tokens, w->hidden, w->experts, nullptr, xrec,
+                                             s));
+            g.small = 1;
+            g.logits = logits;
+            g.ids = ids;
+            g.ids_out = ids;
+            g.probs_out = probs;
+            g.desc_out = desc;
+            g.plan_out = plan;
+        } else {
+            PlanSide side = sel;
+            side.desc = desc;
+            side.x = x;
+            side.x_bf16 = x_dtype == OCO_DT_BF16 ? 1u : 0u;
+            side.rec = xrec;
+            side.rows = tokens;
+            side.k = w->hidden;
+            OCO_TRY(route_plan_launch(ids, routes, w->experts, tile_rows, 0, 0, plan, &side, s));
+        }
         g.desc = desc;
         g.w = (const uint8_t *)w->gate;
         g.w2 = (const uint8_t *)w->up;
@@ -497,6 +529,7 @@ static int experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype,
         g.up_one = w->up_bias_one;
         OCO_TRY(mx_experts_launch(MM_GATE_UP, g, xrec, xterms, tile_rows, s));
         MatmulArgs d = g;
+        d.small = 0;
         d.yrec = nullptr;
         d.w = (const uint8_t *)w->down;
         d.w2 = nullptr;
@@ -688,9 +721,12 @@ int oco_experts_forward(const oco_experts *w, const float *router_w, const float
     hipStream_t s = (hipStream_t)stream;
     float *logits = (float *)((uint8_t *)workspace + oco_experts_workspace(w, tokens) -
                               align256((uint64_t)tokens * w->experts * 4));
-    OCO_TRY(router_logits_launch(x, x_dtype, router_w, router_bias, tokens, w->hidden, w->experts, logits, s));
+    // the MXFP4 decode tiles' input split rides in the router's launch
+    const bool split = mx_small_path(w, tokens) && (x_dtype == OCO_DT_F32 || x_dtype == OCO_DT_BF16);
+    OCO_TRY(router_logits_launch(x, x_dtype, router_w, router_bias, tokens, w->hidden, w->experts, logits,
+                                 split ? mx_xrec(w, (uint8_t *)workspace, tokens) : nullptr, s));
     return experts_apply(w, x, x_dtype, ids, probs, logits, tokens, out, routed, workspace, workspace_bytes, s,
-                         "oco_experts_forward");
+                         "oco_experts_forward", split);
 }
 
 }  // extern "C"

@@ -25,6 +25,16 @@ struct MatmulArgs {
     uint32_t act, up_one;
     uint32_t *rowmax;      // [routes] max |activation| bits per expert-sorted row (gate/up writes, down reads)
     uint8_t *yrec;         // MXFP4 gate/up: the activations' E4M3 split records in place of f32 rows (or null)
+    // MXFP4 gate/up at small decode batches (route.h's in-workgroup plan):
+    // `small` set, the plan is built from `logits` (selection; ids_out and
+    // probs_out receive it) or from `ids`, and written to desc_out / plan_out
+    // for the down launch
+    uint32_t small;
+    const float *logits;
+    const uint32_t *ids;
+    uint32_t *ids_out;
+    float *probs_out;
+    uint32_t *desc_out, *plan_out;
 };
 
 // Power of two that brings a row with max |value| `bits` (f32 bits) into

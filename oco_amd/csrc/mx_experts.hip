@@ -53,20 +53,49 @@ __global__ __launch_bounds__(64 * NW) void mx_experts_kernel(KPRE_PARAMS, Matmul
     constexpr int ALD = (KS * TR * APR + 64 * NW - 1) / (64 * NW);  // A loads per lane per quad (TR rows per part)
     static_assert(NW % KS == 0 && (G == MM_DOWN || (NW / KS) % 2 == 0), "wavefronts split evenly into parts and tiles");
     static_assert((KS - 1) * (NW / KS) * 16 * 64 * 4 <= KS * TR * AROW, "the K-part sums fit the record region");
+    static_assert(4 * SMALL_PLAN_WORDS <= TR * AROW && TR <= 64, "the in-workgroup plan fits the record region");
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, c = lane & 31, part = lane >> 5;
     const int kh = wave / WPK, wsub = wave % WPK;  // K part, wavefront within it
     // The plan's tile count (word 1) spreads exactly the used tiles evenly
     // over the XCDs, each XCD a contiguous range of them (tile-major); then
     // the tile's descriptor: expert, rows, first sorted row, its route ids.
-    const uint32_t used = gridDim.x * min(a.plan[1], gridDim.y);
-    const uint32_t lin = xcd_order(blockIdx.x + gridDim.x * blockIdx.y, used);
-    if (lin >= used) return;  // uniform: a surplus workgroup
-    const uint32_t bx = lin % gridDim.x, y = lin / gridDim.x;
-    const uint32_t *dsc = a.desc + (uint64_t)y * (PLAN_DESC_HEAD + TR);
-    const uint4 head = *reinterpret_cast<const uint4 *>(dsc);
-    const uint32_t *rid = dsc + PLAN_DESC_HEAD;
-    const uint32_t expert = head.x, rows = head.y, sorted0 = head.z;
-    if (rows == 0) return;  // uniform: an unused tile slot
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    uint32_t expert, rows, sorted0, bx, y;
+    const uint32_t *rid;
+    if (G == MM_GATE_UP && a.small) {
+        // the plan built here (in the A region, free until the first quad)
+        uint32_t *psh = reinterpret_cast<uint32_t *>(lds);
+        const bool store = blockIdx.x == 0 && blockIdx.y == 0;  // this workgroup records the plan
+        const SmallPlan sp =
+            small_plan<64 * NW, TR>(a.logits, a.ids, a.routes / a.topk, a.experts, a.topk, psh, store);
+        if (store)
+            small_plan_store<TR>(sp, a.routes, a.desc_out, a.plan_out, psh, a.logits ? a.ids_out : nullptr,
+                                 a.probs_out);
+        const uint32_t used = gridDim.x * min(small_tiles(sp), gridDim.y);
+        const uint32_t lin = xcd_order(blockIdx.x + gridDim.x * blockIdx.y, used);
+        if (lin >= used) return;  // uniform: a surplus workgroup
+        bx = lin % gridDim.x;
+        y = lin / gridDim.x;
+        const SmallTile t = small_tile<TR>(sp, y, psh);
+        __syncthreads();  // the tile's route ids are in place
+        expert = t.expert;
+        rows = t.rows;
+        sorted0 = t.sorted0;
+        rid = sh_tile(psh);
+    } else {
+        const uint32_t used = gridDim.x * min(a.plan[1], gridDim.y);
+        const uint32_t lin = xcd_order(blockIdx.x + gridDim.x * blockIdx.y, used);
+        if (lin >= used) return;  // uniform: a surplus workgroup
+        bx = lin % gridDim.x;
+        y = lin / gridDim.x;
+        const uint32_t *dsc = a.desc + (uint64_t)y * (PLAN_DESC_HEAD + TR);
+        const uint4 head = *reinterpret_cast<const uint4 *>(dsc);
+        rid = dsc + PLAN_DESC_HEAD;
+        expert = head.x;
+        rows = head.y;
+        sorted0 = head.z;
+        if (rows == 0) return;  // uniform: an unused tile slot
+    }
     // Wavefronts past the last column still load (clamped rows) and join the
     // barriers; they store nothing.
     const bool upw = G == MM_GATE_UP && wsub >= CT;  // an up wavefront
@@ -76,7 +105,6 @@ __global__ __launch_bounds__(64 * NW) void mx_experts_kernel(KPRE_PARAMS, Matmul
     // the parity of their local quad index)
     const uint32_t qpart = KS == 1 ? quads : (quads + 2 * KS - 1) / (2 * KS) * 2, q0 = kh * qpart;
 
-    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     uint8_t *alds = lds;                                           // [KS][TR][AROW]
     uint8_t *wlds = lds + KS * TR * AROW + wave * (WROWS * WSLOT);  // [WROWS][WSLOT]
 

@@ -40,18 +40,32 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const XT *x, const f
 }
 
 // The same logits with the reduction spread over a workgroup: workgroup
-// (e, g) takes expert e and tokens 4g .. 4g + 3, each thread four columns per
+// g * experts + e takes expert e and tokens 4g .. 4g + 3, each thread four columns per
 // 1024-column chunk (16-byte weight loads, all of a thread's loads issued
 // before its first FMA), partial sums over DPP and then LDS.  Needs hidden %
-// 4 == 0 and 16-byte (f32) or 8-byte (bf16) aligned rows.
+// 4 == 0 and 16-byte (f32) or 8-byte (bf16) aligned rows.  Workgroups past
+// the logits' (`rec` set) split the rows into E4M3 records (mxsplit.h: bf16
+// rows in two terms, f32 rows in three), one split item per 32 lanes.
 constexpr int ROUTER_TOKENS = 4;
 template <typename XT>
 __global__ __launch_bounds__(256) void router_logits_wide_kernel(const XT *x, const float *w, const float *bias,
                                                                  uint32_t tokens, uint32_t hidden,
-                                                                 uint32_t experts, float *logits) {
+                                                                 uint32_t experts, float *logits, uint8_t *rec) {
     constexpr int TT = ROUTER_TOKENS, U = 4;  // tokens per workgroup, chunks in flight per thread
     __shared__ float part[4][TT];
-    const uint32_t e = blockIdx.x, t0 = blockIdx.y * TT, wave = threadIdx.x >> 6;
+    const uint32_t groups = (tokens + TT - 1) / TT;
+    if (blockIdx.x >= experts * groups) {  // the split job
+        const uint64_t item = ((uint64_t)(blockIdx.x - experts * groups) * 256 + threadIdx.x) / 32;
+        if (item < (uint64_t)tokens * ((hidden + 63) / 64) * 2)
+        {
+            if constexpr (sizeof(XT) == 4)
+                mx_split_item_lanes<float, 3>(reinterpret_cast<const float *>(x), rec, hidden, item);
+            else
+                mx_split_item_lanes<uint16_t, 2>(reinterpret_cast<const uint16_t *>(x), rec, hidden, item);
+        }
+        return;
+    }
+    const uint32_t e = blockIdx.x % experts, t0 = blockIdx.x / experts * TT, wave = threadIdx.x >> 6;
     const uint32_t nt = min((uint32_t)TT, tokens - t0), quads = hidden / 4;
     const float4 *wr = reinterpret_cast<const float4 *>(w + (uint64_t)e * hidden);
     float acc[TT];
@@ -505,9 +519,9 @@ int oco_router(const void *x, oco_dtype x_dtype, const float *w, const float *bi
         // Caller did not ask for the logits: keep them in a per-call allocation.
         OCO_TRY(hip_check(hipMallocAsync((void **)&l, (size_t)tokens * experts * 4, s), "hipMallocAsync"));
     }
-    int rc = router_logits_launch(x, x_dtype, w, bias, tokens, hidden, experts, l, s);
+    int rc = router_logits_launch(x, x_dtype, w, bias, tokens, hidden, experts, l, nullptr, s);
     if (rc == OCO_OK) rc = oco_route_select(l, tokens, experts, k, ids, probs, stream);
-    if (!logits) hipFreeAsync(l, s);
+    if (!logits) (void)hipFreeAsync(l, s);
     return rc;
 }
 
@@ -515,18 +529,29 @@ int oco_router(const void *x, oco_dtype x_dtype, const float *w, const float *bi
 
 namespace oco {
 int router_logits_launch(const void *x, oco_dtype x_dtype, const float *w, const float *bias, uint32_t tokens,
-                         uint32_t hidden, uint32_t experts, float *logits, hipStream_t s) {
+                         uint32_t hidden, uint32_t experts, float *logits, uint8_t *rec, hipStream_t s) {
     const uint32_t waves = tokens * experts;
     const uint32_t xal = x_dtype == OCO_DT_F32 ? 16 : 8;
-    if (hidden % 4 == 0 && ((uintptr_t)w & 15) == 0 && ((uintptr_t)x & (xal - 1)) == 0 &&
-        (x_dtype == OCO_DT_F32 || x_dtype == OCO_DT_BF16)) {
-        const dim3 grid(experts, (tokens + ROUTER_TOKENS - 1) / ROUTER_TOKENS);
+    const uint64_t split_blocks = rec ? ((uint64_t)tokens * ((hidden + 63) / 64) * 2 * 32 + 255) / 256 : 0;
+    const uint64_t router_blocks = (uint64_t)experts * ((tokens + ROUTER_TOKENS - 1) / ROUTER_TOKENS);
+    if (rec && hidden % 32) return fail(OCO_ERR_INVALID, "router: split rows need hidden %% 32 == 0 (hidden=%u)", hidden);
+    const bool wide = hidden % 4 == 0 && ((uintptr_t)w & 15) == 0 && ((uintptr_t)x & (xal - 1)) == 0 &&
+                      (x_dtype == OCO_DT_F32 || x_dtype == OCO_DT_BF16);
+    if (wide || (rec && !logits)) {
+        if (router_blocks + split_blocks >= 0x7fffffffull)
+            return fail(OCO_ERR_INVALID, "router: %u tokens x %u experts over one grid", tokens, experts);
+        // a split alone (no logits): no router workgroups
+        const uint32_t ex = logits ? experts : 0;
+        const dim3 grid((unsigned)((logits ? router_blocks : 0) + split_blocks));
+        if (grid.x == 0) return OCO_OK;
         if (x_dtype == OCO_DT_F32)
             hipLaunchKernelGGL(router_logits_wide_kernel<float>, grid, dim3(256), 0, s, (const float *)x, w, bias,
-                               tokens, hidden, experts, logits);
-        else
+                               tokens, hidden, ex, logits, rec);
+        else if (x_dtype == OCO_DT_BF16)
             hipLaunchKernelGGL(router_logits_wide_kernel<bf16_t>, grid, dim3(256), 0, s, (const bf16_t *)x, w, bias,
-                               tokens, hidden, experts, logits);
+                               tokens, hidden, ex, logits, rec);
+        else
+            return fail(OCO_ERR_UNSUPPORTED, "router: activations must be f32 or bf16");
         return launch_check("router logits");
     }
     if (x_dtype == OCO_DT_F32)
@@ -537,7 +562,9 @@ int router_logits_launch(const void *x, oco_dtype x_dtype, const float *w, const
                            (const bf16_t *)x, w, bias, tokens, hidden, experts, logits);
     else
         return fail(OCO_ERR_UNSUPPORTED, "router: activations must be f32 or bf16");
-    return launch_check("router logits");
+    OCO_TRY(launch_check("router logits"));
+    // the split apart when the rows did not suit the wide kernel
+    return rec ? router_logits_launch(x, x_dtype, w, bias, tokens, hidden, experts, nullptr, rec, s) : OCO_OK;
 }
 }  // namespace oco
 

@@ -477,3 +477,56 @@ def test_experts_forward_from_router(lib, fmt, tokens):
     say("relL2", err)
     bar = MX3_BAR if fmt == 39 and tokens >= 4 else 2e-3 if tokens >= 32 else 1e-5
     assert err < bar
+
+
+@pytest.mark.parametrize("tokens,case", [(4, "ties"), (16, "ties"), (16, "nonfinite"), (1, "plain"), (9, "plain")])
+def test_experts_forward_in_tile_plan(lib, tokens, case):
+    """MXFP4 decode batches (routes <= 64, experts <= 64): every gate/up
+    workgroup selects and plans by itself and the input split rides in the
+    router's launch.  Selection by rank must equal the repeated maximum of
+    oco_route_select bit for bit, ties to the lowest expert included (all
+    router weights zero, biases with repeated values) and non-finite logits
+    (a NaN input row: that token's probabilities are NaN); batch 1 is forced
+    onto the tiles through the MOE_MX_TOKENS knob."""
+    E, hidden, ffn, k = 32, 256, 128, 4
+    say("experts forward in-tile plan", tokens, case)
+    host, devs = bank(lib, 39, E, hidden, ffn, seed=150 + tokens)
+    g, u, d, gb, ub, db = host
+    rng = np.random.default_rng(151 + tokens)
+    x = rng.normal(size=(tokens, hidden)).astype(np.float32)
+    rw = (rng.normal(size=(E, hidden)) / np.sqrt(hidden)).astype(np.float32)
+    rb = (rng.normal(size=E) * 0.1).astype(np.float32)
+    if case == "ties":
+        rw[:] = 0
+        rb = np.array([0.5, 0.25, 0.5, 0.25] * (E // 4), np.float32)
+    if case == "nonfinite":
+        x[3, 7] = np.nan
+    resid = O.f32_to_bf16(rng.normal(size=(tokens, hidden)).astype(np.float32))
+    bk = lib.ExpertBank(39, hidden, ffn, E, k, *devs, activation=0, up_bias_one=True)
+    xb, rwb, rbb = dev(lib, x), dev(lib, rw), dev(lib, rb)
+    with lib.overridden(lib.Knob.MOE_MX_TOKENS, [1]):
+        out1, ids1, probs1 = dev(lib, resid), lib.DeviceBuffer(tokens * k * 4), lib.DeviceBuffer(tokens * k * 4)
+        routed1 = Guarded(lib, tokens * k * hidden * 4)
+        bk.forward(rwb, rbb, xb, lib.DType.F32, tokens, out1, ids1, probs1, routed=routed1.ptr)
+        logits = lib.DeviceBuffer(tokens * E * 4)
+        out2, ids2, probs2 = dev(lib, resid), lib.DeviceBuffer(tokens * k * 4), lib.DeviceBuffer(tokens * k * 4)
+        routed2 = Guarded(lib, tokens * k * hidden * 4)
+        lib.router(xb, lib.DType.F32, rwb, rbb, tokens, hidden, E, k, logits, ids2, probs2)
+        bk.apply(xb, lib.DType.F32, ids2, probs2, tokens, out2, routed=routed2.ptr)
+        lib.synchronize()
+    ids = ids1.download(np.uint32).reshape(tokens, k)
+    np.testing.assert_array_equal(ids, ids2.download(np.uint32).reshape(tokens, k))
+    np.testing.assert_array_equal(probs1.download(np.uint32), probs2.download(np.uint32))
+    np.testing.assert_array_equal(out1.download(np.uint16), out2.download(np.uint16))
+    p = probs1.download(np.float32).reshape(tokens, k)
+    if case == "ties":  # experts 0, 2, 4, 6 (bias 0.5, lowest indices first)
+        np.testing.assert_array_equal(ids, np.tile(np.array([0, 2, 4, 6], np.uint32), (tokens, 1)))
+        np.testing.assert_array_equal(p, np.full((tokens, k), 0.25, np.float32))
+    if case == "nonfinite":
+        assert np.isnan(p[3]).all() and not np.isnan(np.delete(p, 3, axis=0)).any()
+        return
+    np.testing.assert_array_equal(routed1.read(np.uint32), routed2.read(np.uint32))
+    want_ids, want_probs = O.select_experts(logits.download(np.float32).reshape(tokens, E), k)
+    np.testing.assert_array_equal(ids, want_ids)
+    ref = O.experts_reference(39, hidden, ffn, g, u, d, x, ids, p, resid, gb, ub, db, activation=0, up_one=True)
+    assert rel_l2(routed1.read(np.float32).reshape(-1, hidden), ref["down"]) < MX3_BAR
