@@ -202,8 +202,11 @@ __global__ __launch_bounds__(PLAN_THREADS) void route_plan_kernel(const uint32_t
     const bool one_pass = plan_one_pass(routes, experts);
     uint32_t ev[PLAN_ONEPASS_CHUNKS], rk[PLAN_ONEPASS_CHUNKS];
     if (one_pass) {
-        const uint32_t slots = nchunks * 16;
-        for (uint32_t t = tid; t < slots * experts; t += PLAN_THREADS) hist[t] = 0;
+        // counts of (chunk, wavefront) slot q of expert e at hist[e * HS + q]:
+        // an odd row stride keeps the scan's reads (threads of several
+        // experts, each over a run of slots) on distinct banks
+        const uint32_t slots = nchunks * 16, HS = slots + 1;
+        for (uint32_t t = tid; t < HS * experts; t += PLAN_THREADS) hist[t] = 0;
         const uint32_t id_bits = experts > 1 ? 32u - (uint32_t)__builtin_clz(experts - 1) : 0u;
 #pragma unroll
         for (uint32_t c = 0; c < PLAN_ONEPASS_CHUNKS; c++) {
@@ -226,7 +229,7 @@ __global__ __launch_bounds__(PLAN_THREADS) void route_plan_kernel(const uint32_t
                 peers &= ((e >> bit) & 1u) ? b : ~b;
             }
             rk[c] = (uint32_t)__popcll(peers & ((1ull << lane) - 1ull));
-            if (e < experts && (peers >> lane) == 1ull) hist[(c * 16 + wave) * experts + e] = rk[c] + 1;
+            if (e < experts && (peers >> lane) == 1ull) hist[e * HS + c * 16 + wave] = rk[c] + 1;
         }
         __syncthreads();
         // exclusive scan per expert over the slots (chunk, wavefront) in
@@ -237,7 +240,7 @@ __global__ __launch_bounds__(PLAN_THREADS) void route_plan_kernel(const uint32_t
         const uint32_t e = tid / G, j = tid % G, per = (slots + G - 1) / G;
         uint32_t local = 0;
         if (e < experts)
-            for (uint32_t q = j * per; q < min(slots, j * per + per); q++) local += hist[q * experts + e];
+            for (uint32_t q = j * per; q < min(slots, j * per + per); q++) local += hist[e * HS + q];
         uint32_t incl = local;
         for (uint32_t o = 1; o < G; o <<= 1) {
             const uint32_t v = (uint32_t)__shfl_up((int)incl, o, (int)G);
@@ -246,8 +249,8 @@ __global__ __launch_bounds__(PLAN_THREADS) void route_plan_kernel(const uint32_t
         if (e < experts) {
             uint32_t run_e = incl - local;
             for (uint32_t q = j * per; q < min(slots, j * per + per); q++) {
-                const uint32_t v = hist[q * experts + e];
-                hist[q * experts + e] = run_e;
+                const uint32_t v = hist[e * HS + q];
+                hist[e * HS + q] = run_e;
                 run_e += v;
             }
             if (j == G - 1) run[e] = incl;
@@ -342,7 +345,7 @@ __global__ __launch_bounds__(PLAN_THREADS) void route_plan_kernel(const uint32_t
             if (c >= nchunks) break;  // uniform
             const uint32_t e = ev[c], i = c * PLAN_THREADS + tid;
             if (e < experts) {
-                const uint32_t pos = hist[(c * 16 + wave) * experts + e] + rk[c];
+                const uint32_t pos = hist[e * (nchunks * 16 + 1) + c * 16 + wave] + rk[c];
                 plan[grouped + (uint64_t)e * (routes + 1) + 1 + pos] = i;
                 plan[sorted + experts + i] = offs[e] + pos;
                 if (side.desc)
@@ -479,7 +482,7 @@ int route_plan_launch(const uint32_t *ids, uint32_t routes, uint32_t experts, ui
     if (side_blocks >= 0x7fffffffu) return fail(OCO_ERR_INVALID, "oco_route_plan: side job of %llu elements", (unsigned long long)sj.n);
     hipLaunchKernelGGL(route_plan_kernel, dim3(1 + (unsigned)side_blocks), dim3(PLAN_THREADS),
                        (size_t)(PLAN_THREADS + 3 * experts +
-                                (plan_one_pass(routes, experts) ? std::max(16 * experts, (routes + 1023) / 1024 * 16 * experts)
+                                (plan_one_pass(routes, experts) ? std::max(16 * experts, ((routes + 1023) / 1024 * 16 + 1) * experts)
                                  : experts <= PLAN_HIST_EXPERTS  ? 16 * experts
                                                                  : 0)) * 4,
                        stream, ids, routes, experts, tile_rows, up_tiles, down_tiles, plan, sj);
