@@ -207,7 +207,7 @@ struct SmallPlan {
 // rows; every thread of the workgroup (NTH threads) calls it; the
 // probabilities only `with_probs`.  `sh` holds SMALL_PLAN_WORDS words of LDS.
 template <int NTH, int TR>
-__device__ SmallPlan small_plan(const float *logits, const uint32_t *ids, uint32_t tokens, uint32_t experts,
+__device__ __forceinline__ SmallPlan small_plan(const float *logits, const uint32_t *ids, uint32_t tokens, uint32_t experts,
                                 uint32_t k, uint32_t *sh, bool with_probs) {
     uint32_t *sid = sh_ids(sh), *nf = sh_nonfinite(sh);
     float *sch = sh_chosen(sh), *sprob = sh_probs(sh);
@@ -316,7 +316,7 @@ __device__ __forceinline__ SmallTile small_tile(const SmallPlan &sp, uint32_t y,
 // selection (ids/probs) when it was made here.  Threads 0-63 of one
 // workgroup.
 template <int TR>
-__device__ void small_plan_store(const SmallPlan &sp, uint32_t routes, uint32_t *desc, uint32_t *plan, uint32_t *sh,
+__device__ __forceinline__ void small_plan_store(const SmallPlan &sp, uint32_t routes, uint32_t *desc, uint32_t *plan, uint32_t *sh,
                                  uint32_t *ids_out, float *probs_out) {
     if (threadIdx.x >= 64) return;
     const uint32_t l = threadIdx.x, DW = PLAN_DESC_HEAD + TR;
