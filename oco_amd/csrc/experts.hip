@@ -399,12 +399,12 @@ uint64_t oco_experts_workspace(const oco_experts *w, uint32_t tokens) {
     const uint64_t routes = (uint64_t)tokens * w->k;
     // plan, f32 activations, f16 copy of f32 inputs and activation row maxima
     // (prefill), route outputs, f16 activations (Q4_K prefill); MXFP4 banks
-    // also the E4M3 splits of the inputs and of the activations
+    // also the E2M3 splits of the inputs and of the activations
     uint64_t bytes = align256(oco_route_plan_words((uint32_t)routes, w->experts) * 4) + align256(routes * w->ffn * 4) +
                      align256((uint64_t)tokens * w->hidden * 2) + align256(routes * 4) + align256(routes * w->hidden * 4);
     if (w->format == OCO_Q4_K) bytes += align256(routes * w->ffn * 2);
     if (w->format == OCO_MXFP4)  // ... and the plan's tile descriptors (tiles of up to 32 rows)
-        bytes += align256(mx_rows_bytes(tokens, w->hidden, 3)) + align256(mx_rows_bytes((uint32_t)routes, w->ffn, 3)) +
+        bytes += align256(mx_rows_bytes(tokens, w->hidden)) + align256(mx_rows_bytes((uint32_t)routes, w->ffn)) +
                  align256(plan_desc_words((uint32_t)routes, w->experts, 32) * 4);
     // router logits of oco_experts_forward, last
     return bytes + align256((uint64_t)tokens * w->experts * 4);
@@ -471,23 +471,22 @@ static int experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype,
     uint8_t *own_down = (uint8_t *)rowmax + align256((uint64_t)routes * 4);
     float *down = routed ? routed : (float *)own_down;
     uint8_t *xrec = mx_xrec(w, ws, tokens);  // MXFP4 only (just past the route outputs)
-    uint8_t *arec = xrec + align256(mx_rows_bytes(tokens, w->hidden, 3));
+    uint8_t *arec = xrec + align256(mx_rows_bytes(tokens, w->hidden));
     uint16_t *act16 = (uint16_t *)xrec;  // Q4_K only (in place of the MXFP4 splits)
 
     int32_t ov[4];
     const uint32_t mx_tokens = plan_override(OCO_KNOB_MOE_MX_TOKENS, ov) ? (uint32_t)ov[0] : MOE_MX_TOKENS;
-    // The MFMA tiles and the E4M3 row split read whole 32-element k groups
+    // The MFMA tiles and the E2M3 row split read whole 32-element k groups
     // and n tiles; other geometries take the routed matvec path below.
     const bool tiled = w->hidden % 32 == 0 && w->ffn % 32 == 0;
     if (tiled && w->format == OCO_MXFP4 && tokens >= mx_tokens) {
-        // MXFP4 banks: block-scaled FP8 x FP4 MFMA on the GGUF bytes (no
-        // weight decode); activations split per row into E4M3 terms.
+        // MXFP4 banks: block-scaled FP6 x FP4 MFMA on the GGUF bytes (no
+        // weight decode); activations split per row into three E2M3 terms.
         // Decode batches take 16-row tiles (half the staged activations).
         const uint32_t tile_rows = tokens <= 16 ? 16 : 32;
-        // The input rows' split runs beside the plan; the activations are
-        // split by the gate/up tiles themselves.
-        const int xterms = x_dtype == OCO_DT_BF16 ? 2 : 3;  // bf16 rows are exact in two terms
-        uint32_t *desc = (uint32_t *)(arec + align256(mx_rows_bytes(routes, w->ffn, 3)));
+        // The input rows' split runs beside the router or the plan; the
+        // activations are split by the gate/up tiles themselves.
+        uint32_t *desc = (uint32_t *)(arec + align256(mx_rows_bytes(routes, w->ffn)));
         MatmulArgs g = {};
         if (small) {
             if (!split_done)
@@ -527,7 +526,7 @@ static int experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype,
         g.topk = w->k;
         g.act = w->activation;
         g.up_one = w->up_bias_one;
-        OCO_TRY(mx_experts_launch(MM_GATE_UP, g, xrec, xterms, tile_rows, s));
+        OCO_TRY(mx_experts_launch(MM_GATE_UP, g, xrec, tile_rows, s));
         MatmulArgs d = g;
         d.small = 0;
         d.yrec = nullptr;
@@ -541,7 +540,7 @@ static int experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype,
         d.k = w->ffn;
         d.row_bytes = (uint32_t)oco_row_bytes(w->format, w->ffn);
         d.expert_bytes = (uint64_t)d.row_bytes * w->hidden;
-        OCO_TRY(mx_experts_launch(MM_DOWN, d, arec, 3, tile_rows, s));
+        OCO_TRY(mx_experts_launch(MM_DOWN, d, arec, tile_rows, s));
         return oco_moe_sum(down, routed ? OCO_DT_F32 : OCO_DT_BF16, probs, out, w->hidden, tokens, w->k, stream);
     }
 

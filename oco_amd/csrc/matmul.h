@@ -12,7 +12,7 @@ struct MatmulArgs {
     const uint32_t *plan;  // grouped (routed-expert) mode: route plan with tile_rows = BM
     const uint8_t *w;
     const uint8_t *w2;     // up weights (gate/up mode)
-    const void *x;         // activations (MXFP4 expert tiles: their E4M3 split records)
+    const void *x;         // activations (MXFP4 expert tiles: their E2M3 split records)
     uint32_t n, k;
     uint32_t row_bytes;    // bytes of one weight row (< 4 GiB)
     uint32_t routes, experts, topk;
@@ -24,7 +24,7 @@ struct MatmulArgs {
     const float *bias2;    // up bias (gate/up mode)
     uint32_t act, up_one;
     uint32_t *rowmax;      // [routes] max |activation| bits per expert-sorted row (gate/up writes, down reads)
-    uint8_t *yrec;         // MXFP4 gate/up: the activations' E4M3 split records in place of f32 rows (or null)
+    uint8_t *yrec;         // MXFP4 gate/up: the activations' E2M3 split records in place of f32 rows (or null)
     // MXFP4 gate/up at small decode batches (route.h's in-workgroup plan):
     // `small` set, the plan is built from `logits` (selection; ids_out and
     // probs_out receive it) or from `ids`, and written to desc_out / plan_out
@@ -77,12 +77,11 @@ int grouped_matmul_launch(int mode, uint32_t fmt, const MatmulArgs &a, uint32_t 
 // tile_rows = bm: 32, 48 or 64).
 int moe_q4k_launch(int mode, const MatmulArgs &a, uint32_t bm, hipStream_t stream);
 
-// MXFP4 banks on the block-scaled MFMA: activations split per row into E4M3
-// records (mxsplit.h; mx_rows_bytes each matrix) -- the inputs beside the
-// route plan, the activations by the gate/up tiles -- route plan with
-// tile_rows = 16 or 32.
-uint64_t mx_rows_bytes(uint32_t rows, uint32_t k, int terms);
-int mx_experts_launch(int mode, const MatmulArgs &a, const uint8_t *xrec, int terms, uint32_t tile_rows,
-                      hipStream_t stream);
+// MXFP4 banks on the block-scaled MFMA: activations split per row into three
+// E2M3 terms (mxsplit.h; mx_rows_bytes each matrix) -- the inputs beside the
+// router or the route plan, the activations by the gate/up tiles -- route
+// plan with tile_rows = 16 or 32.
+uint64_t mx_rows_bytes(uint32_t rows, uint32_t k);
+int mx_experts_launch(int mode, const MatmulArgs &a, const uint8_t *xrec, uint32_t tile_rows, hipStream_t stream);
 
 }  // namespace oco

@@ -1,4 +1,4 @@
-// Routed MXFP4 experts on the block-scaled FP8 x FP4 MFMA: the grouped
+// Routed MXFP4 experts on the block-scaled FP6 x FP4 MFMA: the grouped
 // expert GEMMs of expert_up_tensor / moe_activate / expert_down_tensor
 // (projections.metal:192-376, routing.metal:44-64) and, at decode, the
 // routed matvecs of expert_expand / matvec_mxfp4 (:78-182) -- with no weight
@@ -6,7 +6,8 @@
 // stored and its E8M0 byte the B scale (the operand layout is described in
 // mxmatmul.hip).
 //
-// Activations come split per row into TERMS E4M3 terms (mxsplit.h).
+// Activations come split per row into three E2M3 terms (mxsplit.h): the A
+// operand is FP6, which issues at the FP4 rate.
 #include "matmul.h"
 #include "mxsplit.h"
 #include "route.h"
@@ -17,9 +18,7 @@ namespace oco {
 typedef int mxe_i32x8 __attribute__((ext_vector_type(8)));
 typedef float mxe_f32x16 __attribute__((ext_vector_type(16)));
 
-uint64_t mx_rows_bytes(uint32_t rows, uint32_t k, int terms) {
-    return (uint64_t)rows * ((k + 63) / 64) * mxr_rec(terms);
-}
+uint64_t mx_rows_bytes(uint32_t rows, uint32_t k) { return (uint64_t)rows * ((k + 63) / 64) * MXR_REC; }
 
 // Tile: one route-plan tile of up to TR routes (16 or 32: the plan's tile
 // rows) and 32-column weight tiles, one per wavefront (gate/up: the first
@@ -36,7 +35,7 @@ uint64_t mx_rows_bytes(uint32_t rows, uint32_t k, int terms) {
 // Both are loaded one quad ahead into registers and written to LDS at the
 // top of the next quad, so one vmcnt(0) and two barriers per quad order
 // everything.
-template <int G, int NW, int TERMS, int TR, int KS>
+template <int G, int NW, int TR, int KS>
 __global__ __launch_bounds__(64 * NW) void mx_experts_kernel(KPRE_PARAMS, MatmulArgs a) {
     KPRE_APPLY(a);
     const uint8_t *xrec = reinterpret_cast<const uint8_t *>(a.x);
@@ -47,7 +46,7 @@ __global__ __launch_bounds__(64 * NW) void mx_experts_kernel(KPRE_PARAMS, Matmul
     constexpr int WPK = NW / KS;                   // wavefronts per K part (KS parts split the quads)
     constexpr int CT = G == MM_GATE_UP ? WPK / 2 : WPK;  // column tiles per workgroup
     constexpr uint32_t WSLOT = 176;                // LDS bytes per staged row (11 x 16)
-    constexpr uint32_t AREC = mxr_rec(TERMS);
+    constexpr uint32_t AREC = MXR_REC;
     constexpr uint32_t AROW = 4 * AREC + 16;       // LDS bytes per tile row of A (four records + pad)
     constexpr uint32_t APR = 4 * AREC / 16;        // 16-byte pieces per tile row and quad
     constexpr int ALD = (KS * TR * APR + 64 * NW - 1) / (64 * NW);  // A loads per lane per quad (TR rows per part)
@@ -129,7 +128,8 @@ __global__ __launch_bounds__(64 * NW) void mx_experts_kernel(KPRE_PARAMS, Matmul
     // row of C depends on its own row of A only, and those rows are never
     // stored).
     const uint32_t arow = (uint32_t)c < rows ? c : 0u;
-    const uint32_t afrag = (kh * TR + arow) * AROW + 32 * part, ascale = (kh * TR + arow) * AROW + mxr_data(TERMS) + 4 * part;
+    const uint32_t arow0 = (kh * TR + arow) * AROW;
+    const uint32_t a16 = arow0 + 16 * part, a8 = arow0 + MXR_CODES8 + 8 * part, ascale = arow0 + MXR_SCALES + 4 * part;
 
     // B: load i of a lane covers staged row f / 10, chunk f % 10 (f = lane +
     // 64 i); quad q's span of a row at byte R starts at
@@ -198,12 +198,14 @@ __global__ __launch_bounds__(64 * NW) void mx_experts_kernel(KPRE_PARAMS, Matmul
             if (step >= ksteps) break;  // uniform per wavefront
             // the lone last block's partner is zero with scale 1
             const bool live = 2 * step + part < nblk;
-            u32x4 av[TERMS][2];
+            // A: each term's 24 code bytes of this lane's block (16 + 8)
+            u32x4 av16[MX_TERMS];
+            u32x2 av8[MX_TERMS];
 #pragma unroll
-            for (int t = 0; t < TERMS; t++)
-#pragma unroll
-                for (int b = 0; b < 2; b++)
-                    av[t][b] = *reinterpret_cast<const u32x4 *>(alds + afrag + s * AREC + 64 * t + 16 * b);
+            for (int t = 0; t < MX_TERMS; t++) {
+                av16[t] = *reinterpret_cast<const u32x4 *>(alds + a16 + s * AREC + 32 * t);
+                av8[t] = *reinterpret_cast<const u32x2 *>(alds + a8 + s * AREC + 16 * t);
+            }
             const uint32_t sa = *reinterpret_cast<const uint32_t *>(alds + ascale + s * AREC);
 #pragma unroll
             for (int j = 0; j < NT; j++) {
@@ -219,19 +221,20 @@ __global__ __launch_bounds__(64 * NW) void mx_experts_kernel(KPRE_PARAMS, Matmul
                     live ? mxe_i32x8{(int)qd[0], (int)qd[1], (int)qd[2], (int)qd[3], 0, 0, 0, 0} : mxe_i32x8{};
                 const int sb = live ? (int)wlds[pay - 1] : 127;
 #if defined(OCO_ABL) && OCO_ABL == 1
-                acc[j][0] += __int_as_float(bv[0] ^ bv[3] ^ sb ^ (int)sa ^ (int)av[0][0].x ^ (int)av[TERMS - 1][1].w);
+                acc[j][0] += __int_as_float(bv[0] ^ bv[3] ^ sb ^ (int)sa ^ (int)av16[0].x ^ (int)av8[MX_TERMS - 1].y);
                 continue;
 #endif
 #pragma unroll
-                for (int t = 0; t < TERMS; t++) {
-                    const mxe_i32x8 avt{(int)av[t][0].x, (int)av[t][0].y, (int)av[t][0].z, (int)av[t][0].w,
-                                        (int)av[t][1].x, (int)av[t][1].y, (int)av[t][1].z, (int)av[t][1].w};
+                for (int t = 0; t < MX_TERMS; t++) {
+                    const mxe_i32x8 avt{(int)av16[t].x, (int)av16[t].y, (int)av16[t].z, (int)av16[t].w,
+                                        (int)av8[t].x,  (int)av8[t].y,  0,                0};
+                    // cbsz 2: A in E2M3; blgp 4: B in E2M1; op_sel picks term t's scale byte
                     if (t == 0)
-                        acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(avt, bv, acc[j], 0, 4, 0, (int)sa, 0, sb);
+                        acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(avt, bv, acc[j], 2, 4, 0, (int)sa, 0, sb);
                     else if (t == 1)
-                        acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(avt, bv, acc[j], 0, 4, 1, (int)sa, 0, sb);
+                        acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(avt, bv, acc[j], 2, 4, 1, (int)sa, 0, sb);
                     else
-                        acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(avt, bv, acc[j], 0, 4, 2, (int)sa, 0, sb);
+                        acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(avt, bv, acc[j], 2, 4, 2, (int)sa, 0, sb);
                 }
             }
         }
@@ -282,20 +285,36 @@ __global__ __launch_bounds__(64 * NW) void mx_experts_kernel(KPRE_PARAMS, Matmul
             }
             return;
         }
-        // The 32 columns are one block of each activation row (n % 32 == 0):
-        // each half wavefront splits its rows' blocks into the down
-        // projection's records (and, for a lone last block, zeros the partner).
-        const uint32_t blk = col0 / 32, dsteps = (a.n + 63) / 64;
-        const bool lone = !(blk & 1) && blk + 1 == a.n / 32;
+        // The 32 columns are one block of each activation row (n % 32 == 0).
+        // The block goes through this wavefront's weight staging region (free
+        // now), transposed so that lane r holds row r's 32 values, and each
+        // live row's lane splits it into the down projection's record (and,
+        // for a lone last block, zeros the partner).
+        constexpr uint32_t TRS = 36;  // floats per transposed row (16-byte aligned rows)
+        static_assert(16 * TRS * 4 <= WROWS * WSLOT, "the transposed block fits the staging region");
+        float *tr = reinterpret_cast<float *>(wlds);
 #pragma unroll
         for (int v = 0; v < 16; v++) {
-            const uint32_t r = 8 * (v / 4) + 4 * part + (v % 4);  // uniform per half wavefront
-            if (r < rows) {
-                uint8_t *rec = a.yrec + ((uint64_t)(sorted0 + r) * dsteps + blk / 2) * mxr_rec(3);
-                mx_split_lanes<3>(expert_activation(a.act, acc[0][v] + bg, hand[(wsub * 16 + v) * 64 + lane] + bu), rec,
-                                  blk & 1);
-                if (lone) mx_split_lanes<3>(0.f, rec, 1);
+            const uint32_t r = 8 * (v / 4) + 4 * part + (v % 4);
+            tr[r * TRS + c] = expert_activation(a.act, acc[0][v] + bg, hand[(wsub * 16 + v) * 64 + lane] + bu);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if ((uint32_t)lane < rows) {
+            const uint32_t blk = col0 / 32, dsteps = (a.n + 63) / 64;
+            float v[32];
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const float4 f = *reinterpret_cast<const float4 *>(tr + lane * TRS + 4 * q);
+                v[4 * q] = f.x;
+                v[4 * q + 1] = f.y;
+                v[4 * q + 2] = f.z;
+                v[4 * q + 3] = f.w;
             }
+            uint8_t *rec = a.yrec + ((uint64_t)(sorted0 + lane) * dsteps + blk / 2) * MXR_REC;
+            mx6_split_block(v, rec, blk & 1);
+            if (!(blk & 1) && blk + 1 == a.n / 32) mx6_zero_block(rec, 1);  // a lone last block
         }
     } else {
         if (col >= a.n) return;
@@ -316,11 +335,11 @@ __global__ __launch_bounds__(64 * NW) void mx_experts_kernel(KPRE_PARAMS, Matmul
 
 constexpr int MXE_NW = 4;
 
-template <int G, int TERMS, int TR, int KS>
+template <int G, int TR, int KS>
 static int mx_experts_go(const MatmulArgs &a, const uint8_t *xrec, hipStream_t stream) {
-    const size_t lds = KS * TR * (4 * mxr_rec(TERMS) + 16) + (size_t)MXE_NW * 32 * 176;
-    static_assert(TR * (4 * mxr_rec(2) + 16) >= MXE_NW / 2 * 16 * 64 * 4, "the up hand-over fits the A region");
-    auto fn = mx_experts_kernel<G, MXE_NW, TERMS, TR, KS>;
+    const size_t lds = KS * TR * (4 * MXR_REC + 16) + (size_t)MXE_NW * 32 * 176;
+    static_assert(TR * (4 * MXR_REC + 16) >= MXE_NW / 2 * 16 * 64 * 4, "the up hand-over fits the A region");
+    auto fn = mx_experts_kernel<G, MXE_NW, TR, KS>;
     OCO_TRY(hip_check(hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
                       "hipFuncSetAttribute"));
     const uint32_t cols = 32 * (G == MM_GATE_UP ? MXE_NW / 2 : MXE_NW) / KS;
@@ -333,9 +352,9 @@ static int mx_experts_go(const MatmulArgs &a, const uint8_t *xrec, hipStream_t s
 
 constexpr uint32_t MXE_CUS = 256;
 
-template <int G, int TERMS>
+template <int G>
 static int mx_experts_go_tr(const MatmulArgs &a, const uint8_t *xrec, uint32_t tile_rows, hipStream_t stream) {
-    if (tile_rows == 32) return mx_experts_go<G, TERMS, 32, 1>(a, xrec, stream);
+    if (tile_rows == 32) return mx_experts_go<G, 32, 1>(a, xrec, stream);
     if constexpr (G == MM_DOWN) {
         // Few tiles (small decode batches): split each tile's K over two
         // halves of the workgroup when twice the grid still fits one round
@@ -349,22 +368,19 @@ static int mx_experts_go_tr(const MatmulArgs &a, const uint8_t *xrec, uint32_t t
         // Under four quads the second part would hold little or no real work.
         const uint32_t quads = ((a.k + 63) / 64 + 3) / 4;
         const int ks = plan_override(OCO_KNOB_MX_EXPERTS_KS, ov) ? ov[0] : 2 * wgs <= 3 * MXE_CUS && quads >= 4 ? 2 : 1;
-        if (ks == 2) return mx_experts_go<G, TERMS, 16, 2>(a, xrec, stream);
+        if (ks == 2) return mx_experts_go<G, 16, 2>(a, xrec, stream);
     }
-    return mx_experts_go<G, TERMS, 16, 1>(a, xrec, stream);
+    return mx_experts_go<G, 16, 1>(a, xrec, stream);
 }
 
-int mx_experts_launch(int mode, const MatmulArgs &a, const uint8_t *xrec, int terms, uint32_t tile_rows,
-                      hipStream_t stream) {
+int mx_experts_launch(int mode, const MatmulArgs &a, const uint8_t *xrec, uint32_t tile_rows, hipStream_t stream) {
     if (a.k % 32) return fail(OCO_ERR_INVALID, "experts: MXFP4 rows need k %% 32 == 0 (k=%u)", a.k);
     if (tile_rows != 16 && tile_rows != 32) return fail(OCO_ERR_INVALID, "experts: MXFP4 plan tiles of %u rows", tile_rows);
     // Kernel offsets are 32-bit: the split rows and one expert's matrix each stay under 4 GiB.
-    if (mx_rows_bytes(a.routes, a.k, terms) > 0xffffffffull || a.expert_bytes + 4 > 0xffffffffull)
+    if (mx_rows_bytes(a.routes, a.k) > 0xffffffffull || a.expert_bytes + 4 > 0xffffffffull)
         return fail(OCO_ERR_UNSUPPORTED, "experts: MXFP4 operands over 4 GiB (routes=%u k=%u)", a.routes, a.k);
-    const int rc = mode == MM_GATE_UP ? (terms == 2 ? mx_experts_go_tr<MM_GATE_UP, 2>(a, xrec, tile_rows, stream)
-                                                    : mx_experts_go_tr<MM_GATE_UP, 3>(a, xrec, tile_rows, stream))
-                                      : (terms == 2 ? mx_experts_go_tr<MM_DOWN, 2>(a, xrec, tile_rows, stream)
-                                                    : mx_experts_go_tr<MM_DOWN, 3>(a, xrec, tile_rows, stream));
+    const int rc = mode == MM_GATE_UP ? mx_experts_go_tr<MM_GATE_UP>(a, xrec, tile_rows, stream)
+                                      : mx_experts_go_tr<MM_DOWN>(a, xrec, tile_rows, stream);
     OCO_TRY(rc);
     return launch_check("experts MXFP4 grouped matmul");
 }

@@ -31,6 +31,7 @@
 
 #include <algorithm>
 
+#include "mxsplit.h"
 #include "stream.h"
 
 namespace oco {
@@ -44,50 +45,14 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 // (byte t = term t).  Lane l = row l % 32, block l / 32 of the step.
 constexpr uint32_t MX_LO = 2 * 64 * 16, MX_DATA = 2 * 64 * 24, MX_REC = MX_DATA + 64 * 4;
 
-typedef float f32x32 __attribute__((ext_vector_type(32)));
-typedef int i32x6 __attribute__((ext_vector_type(6)));
+typedef mx_f32x32 f32x32;
+typedef mx_i32x6 i32x6;
 
 struct MxSplitArgs {
     const uint16_t *x;
     uint8_t *frag;
     uint32_t m, k, ksteps, records;
 };
-
-// Smallest E with amax <= 7.5 * 2^E (7.5 = 1.875 * 2^2, the largest E2M3
-// value), as E; 128 (the NaN byte) for a non-finite block, -127 at least.
-__device__ __forceinline__ int mx6_scale_exp(uint32_t amax_bits) {
-    if (amax_bits >= 0x7f800000u) return 128;
-    if (amax_bits == 0) return -127;
-    int e;
-    uint32_t mant;
-    if (amax_bits >> 23) {
-        e = (int)(amax_bits >> 23) - 127;
-        mant = amax_bits & 0x7fffffu;
-    } else {  // subnormal amax: normalise
-        const int lz = __builtin_clz(amax_bits) - 8;
-        e = -126 - lz;
-        mant = (amax_bits << lz) & 0x7fffffu;
-    }
-    const int E = mant <= 0x700000u ? e - 2 : e - 1;  // m <= 1.875 <=> m * 2^e <= 7.5 * 2^(e - 2)
-    return E < -127 ? -127 : E;
-}
-
-// E2M3 codes of 32 values: position 2i takes lo[i], 2i + 1 hi[i] (measured
-// on gfx950).  The asm statement keeps the sources live until the result
-// exists: hipcc otherwise may give the result registers that overlap the
-// sources, and the instruction then reads inputs it has already overwritten
-// (seen: v_cvt_scalef32_2xpk16_fp6_f32 v[34:39], v[32:47], v[0:15]).
-__device__ __forceinline__ i32x6 fp6_pack(const f32x16 &lo, const f32x16 &hi) {
-    i32x6 c = __builtin_amdgcn_cvt_scalef32_2xpk16_fp6_f32(lo, hi, 1.0f);
-    asm volatile("" ::"v"(lo), "v"(hi), "v"(c));
-    return c;
-}
-// The 32 values of E2M3 codes, in position order (same register rule).
-__device__ __forceinline__ f32x32 fp6_unpack(const i32x6 &c) {
-    f32x32 d = __builtin_amdgcn_cvt_scalef32_pk32_f32_fp6(c, 1.0f);
-    asm volatile("" ::"v"(c), "v"(d));
-    return d;
-}
 
 // One wavefront (workgroup) per record, so the records spread over every CU;
 // lane l = (row l % 32, block l / 32), each lane

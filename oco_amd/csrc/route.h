@@ -7,8 +7,8 @@ namespace oco {
 // A job run beside the route plan, in the same launch (workgroups 1..):
 // activation rows to f16 (the reference's half(x)) from bf16 or f32, four
 // elements per thread, and `nzero` words of `zero` cleared; or, with `rec`
-// set, the rows' E4M3 split records (mxsplit.h: bf16 rows in two terms, f32
-// rows in three) in place of the f16 copy.
+// set, the rows' split records (mxsplit.h: three E2M3 terms) in place of the
+// f16 copy.
 //
 // Also optional, in the plan's own workgroup: the expert selection itself
 // (`logits` set: top-`topk` of each of `tokens` rows of `experts` logits, as
@@ -39,8 +39,8 @@ __host__ __device__ inline uint64_t plan_desc_words(uint32_t routes, uint32_t ex
 }
 
 // Router logits [tokens, experts] (routing.metal:96-146) into `logits` (or
-// none: null), and with `rec` set, in the same launch, the rows' E4M3 split
-// records (mxsplit.h: bf16 rows in two terms, f32 rows in three).
+// none: null), and with `rec` set, in the same launch, the rows' split
+// records (mxsplit.h: three E2M3 terms).
 int router_logits_launch(const void *x, oco_dtype x_dtype, const float *w, const float *bias, uint32_t tokens,
                          uint32_t hidden, uint32_t experts, float *logits, uint8_t *rec, hipStream_t stream);
 // oco_route_plan with an optional side job (null: none).

@@ -44,8 +44,8 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const XT *x, const f
 // 1024-column chunk (16-byte weight loads, all of a thread's loads issued
 // before its first FMA), partial sums over DPP and then LDS.  Needs hidden %
 // 4 == 0 and 16-byte (f32) or 8-byte (bf16) aligned rows.  Workgroups past
-// the logits' (`rec` set) split the rows into E4M3 records (mxsplit.h: bf16
-// rows in two terms, f32 rows in three), one split item per 32 lanes.
+// the logits' (`rec` set) split the rows into records of three E2M3 terms
+// (mxsplit.h), one split item (row, K step, block) per thread.
 constexpr int ROUTER_TOKENS = 4;
 template <typename XT>
 __global__ __launch_bounds__(256) void router_logits_wide_kernel(const XT *x, const float *w, const float *bias,
@@ -55,13 +55,12 @@ __global__ __launch_bounds__(256) void router_logits_wide_kernel(const XT *x, co
     __shared__ float part[4][TT];
     const uint32_t groups = (tokens + TT - 1) / TT;
     if (blockIdx.x >= experts * groups) {  // the split job
-        const uint64_t item = ((uint64_t)(blockIdx.x - experts * groups) * 256 + threadIdx.x) / 32;
-        if (item < (uint64_t)tokens * ((hidden + 63) / 64) * 2)
-        {
+        const uint64_t item = (uint64_t)(blockIdx.x - experts * groups) * 256 + threadIdx.x;
+        if (item < (uint64_t)tokens * ((hidden + 63) / 64) * 2) {
             if constexpr (sizeof(XT) == 4)
-                mx_split_item_lanes<float, 3>(reinterpret_cast<const float *>(x), rec, hidden, item);
+                mx6_split_item<float>(reinterpret_cast<const float *>(x), rec, hidden, item);
             else
-                mx_split_item_lanes<uint16_t, 2>(reinterpret_cast<const uint16_t *>(x), rec, hidden, item);
+                mx6_split_item<uint16_t>(reinterpret_cast<const uint16_t *>(x), rec, hidden, item);
         }
         return;
     }
@@ -143,13 +142,13 @@ __global__ __launch_bounds__(PLAN_THREADS) void route_plan_kernel(const uint32_t
     if (blockIdx.x > 0) {  // the side job: four elements (or one split item) and one cleared word per thread
         const uint64_t t = (uint64_t)(blockIdx.x - 1) * PLAN_THREADS + threadIdx.x;
         if (t < side.nzero) side.zero[t] = 0;
-        if (side.rec) {  // one split item per 32 lanes (uniform per half wavefront)
-            const uint64_t item = t / 32;
+        if (side.rec) {  // one split item (row, K step, block) per thread
+            const uint64_t item = t;
             if (item < (uint64_t)side.rows * ((side.k + 63) / 64) * 2) {
                 if (side.x_bf16)
-                    mx_split_item_lanes<uint16_t, 2>(reinterpret_cast<const uint16_t *>(side.x), side.rec, side.k, item);
+                    mx6_split_item<uint16_t>(reinterpret_cast<const uint16_t *>(side.x), side.rec, side.k, item);
                 else
-                    mx_split_item_lanes<float, 3>(reinterpret_cast<const float *>(side.x), side.rec, side.k, item);
+                    mx6_split_item<float>(reinterpret_cast<const float *>(side.x), side.rec, side.k, item);
             }
             return;
         }
@@ -476,7 +475,7 @@ int route_plan_launch(const uint32_t *ids, uint32_t routes, uint32_t experts, ui
                     "experts tiles)");
     PlanSide sj = side ? *side : PlanSide{};
     if (sj.rec && sj.k % 32) return fail(OCO_ERR_INVALID, "oco_route_plan: split rows need k %% 32 == 0 (k=%u)", sj.k);
-    const uint64_t side_items = sj.rec ? (uint64_t)sj.rows * ((sj.k + 63) / 64) * 2 * 32 : (sj.n + 3) / 4;  // threads
+    const uint64_t side_items = sj.rec ? (uint64_t)sj.rows * ((sj.k + 63) / 64) * 2 : (sj.n + 3) / 4;  // threads
     const uint64_t side_blocks =
         std::max<uint64_t>((side_items + PLAN_THREADS - 1) / PLAN_THREADS, (sj.nzero + PLAN_THREADS - 1) / PLAN_THREADS);
     if (side_blocks >= 0x7fffffffu) return fail(OCO_ERR_INVALID, "oco_route_plan: side job of %llu elements", (unsigned long long)sj.n);
@@ -535,7 +534,7 @@ int router_logits_launch(const void *x, oco_dtype x_dtype, const float *w, const
                          uint32_t hidden, uint32_t experts, float *logits, uint8_t *rec, hipStream_t s) {
     const uint32_t waves = tokens * experts;
     const uint32_t xal = x_dtype == OCO_DT_F32 ? 16 : 8;
-    const uint64_t split_blocks = rec ? ((uint64_t)tokens * ((hidden + 63) / 64) * 2 * 32 + 255) / 256 : 0;
+    const uint64_t split_blocks = rec ? ((uint64_t)tokens * ((hidden + 63) / 64) * 2 + 255) / 256 : 0;
     const uint64_t router_blocks = (uint64_t)experts * ((tokens + ROUTER_TOKENS - 1) / ROUTER_TOKENS);
     if (rec && hidden % 32) return fail(OCO_ERR_INVALID, "router: split rows need hidden %% 32 == 0 (hidden=%u)", hidden);
     const bool wide = hidden % 4 == 0 && ((uintptr_t)w & 15) == 0 && ((uintptr_t)x & (xal - 1)) == 0 &&
