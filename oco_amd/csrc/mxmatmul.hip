@@ -407,8 +407,30 @@ __global__ __launch_bounds__(512) void mx_matmul_kernel(KPRE_PARAMS, MxArgs a) {
                     acc[j][v] + red[((w4 * CT + j) * 16 + v) * 64 + lane];
     }
     __syncthreads();
-    constexpr int CPR = BN / 4;  // chunks per row
     const uint32_t rows = min((uint32_t)P::BM, a.m - min(a.m, by * P::BM));
+    if (a.y_bf16 && col0 + BN <= a.n && (a.n & 7) == 0 && ((uintptr_t)a.y & 15) == 0) {
+        // bf16 rows of whole 8-column chunks: one 16-byte store each
+        constexpr int CPR8 = BN / 8;
+        for (uint32_t q = tid; q < rows * CPR8; q += P::NTH) {
+            const uint32_t r = q / CPR8, cc = (q % CPR8) * 8, col = col0 + cc;
+            const float4 f0 = *reinterpret_cast<const float4 *>(ot + r * OROW + cc);
+            const float4 f1 = *reinterpret_cast<const float4 *>(ot + r * OROW + cc + 4);
+            float v[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
+            if (a.bias) {
+#pragma unroll
+                for (int e = 0; e < 8; e++) v[e] += round_bf16(gp(a.bias)[col + e]);
+            }
+            uint32_t w[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                w[e] = (uint32_t)f32_to_bf16_bits(v[2 * e]) | ((uint32_t)f32_to_bf16_bits(v[2 * e + 1]) << 16);
+            const uint64_t o = (uint64_t)(by * P::BM + r) * a.n + col;
+            *reinterpret_cast<__attribute__((address_space(1))) u32x4 *>(gp(reinterpret_cast<uint16_t *>(a.y) + o)) =
+                u32x4{w[0], w[1], w[2], w[3]};
+        }
+        return;
+    }
+    constexpr int CPR = BN / 4;  // chunks per row
     for (uint32_t q = tid; q < rows * CPR; q += P::NTH) {
         const uint32_t r = q / CPR, cc = (q % CPR) * 4, col = col0 + cc;
         if (col >= a.n) continue;
