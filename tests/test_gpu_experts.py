@@ -487,17 +487,19 @@ def test_experts_forward_from_router(lib, fmt, tokens):
     assert err < bar
 
 
-@pytest.mark.parametrize("tokens,case", [(4, "ties"), (16, "ties"), (16, "nonfinite"), (1, "plain"), (9, "plain")])
-def test_experts_forward_in_tile_plan(lib, tokens, case):
+@pytest.mark.parametrize("tokens,case,E", [(4, "ties", 32), (16, "ties", 32), (16, "nonfinite", 32), (1, "plain", 32),
+                                          (9, "plain", 32), (8, "plain", 64), (5, "ties", 48), (8, "nonfinite", 64)])
+def test_experts_forward_in_tile_plan(lib, tokens, case, E):
     """MXFP4 decode batches (routes <= 64, experts <= 64): every gate/up
     workgroup selects and plans by itself and the input split rides in the
     router's launch.  Selection by rank must equal the repeated maximum of
     oco_route_select bit for bit, ties to the lowest expert included (all
     router weights zero, biases with repeated values) and non-finite logits
     (a NaN input row: that token's probabilities are NaN); batch 1 is forced
-    onto the tiles through the MOE_MX_TOKENS knob."""
-    E, hidden, ffn, k = 32, 256, 128, 4
-    say("experts forward in-tile plan", tokens, case)
+    onto the tiles through the MOE_MX_TOKENS knob.  32 experts take the
+    32-wide rank rows, 48 and 64 the 64-wide ones (at most 8 tokens)."""
+    hidden, ffn, k = 256, 128, 4
+    say("experts forward in-tile plan", tokens, case, E)
     host, devs = bank(lib, 39, E, hidden, ffn, seed=150 + tokens)
     g, u, d, gb, ub, db = host
     rng = np.random.default_rng(151 + tokens)
@@ -508,7 +510,7 @@ def test_experts_forward_in_tile_plan(lib, tokens, case):
         rw[:] = 0
         rb = np.array([0.5, 0.25, 0.5, 0.25] * (E // 4), np.float32)
     if case == "nonfinite":
-        x[3, 7] = np.nan
+        x[3, 7] = np.nan  # token 3: every logit NaN
     resid = O.f32_to_bf16(rng.normal(size=(tokens, hidden)).astype(np.float32))
     bk = lib.ExpertBank(39, hidden, ffn, E, k, *devs, activation=0, up_bias_one=True)
     xb, rwb, rbb = dev(lib, x), dev(lib, rw), dev(lib, rb)
