@@ -17,6 +17,7 @@ namespace oco {
 
 typedef int mxe_i32x8 __attribute__((ext_vector_type(8)));
 typedef float mxe_f32x16 __attribute__((ext_vector_type(16)));
+typedef float mxe_f32x4 __attribute__((ext_vector_type(4)));
 
 uint64_t mx_rows_bytes(uint32_t rows, uint32_t k) { return (uint64_t)rows * ((k + 63) / 64) * MXR_REC; }
 
@@ -165,6 +166,22 @@ __global__ __launch_bounds__(64 * NW) void mx_experts_kernel(KPRE_PARAMS, Matmul
 #pragma unroll
         for (int p = 0; p < 2; p++) fpay[j][p] = (j * 32 + c) * WSLOT + ((r + 8 * p) & 15u) + 17 * part + 1;
     }
+    // Tiles of 16 rows run v_mfma_scale_f32_16x16x128_f8f6f4 (16 rows, half
+    // the MFMA of the 32-row shape): lane l takes row / column l % 16 and
+    // block g = l / 16 of each 128-K chunk (K steps 2h + g / 2 of the quad,
+    // block g % 2 of the step), the wavefront's 32 columns as two column
+    // tiles ct; C holds column l % 16, rows 4 (l / 16) + v.
+    constexpr bool S16 = TR == 16;
+    const uint32_t l16 = lane & 15, g16 = lane >> 4;
+    const uint32_t arow16 = l16 < rows ? l16 : 0u;
+    const uint32_t a16b = (kh * TR + arow16) * AROW + (g16 >> 1) * AREC;  // + 2 h AREC per chunk
+    uint32_t fpay16[2][2];  // [column tile][parity]: lds offset of the payload of chunk 0
+#pragma unroll
+    for (int ct = 0; ct < 2; ct++) {
+        const uint32_t r = rsh[0] + min(col0 + 16 * ct + l16, a.n - 1) * (uint32_t)a.row_bytes;
+#pragma unroll
+        for (int p = 0; p < 2; p++) fpay16[ct][p] = (16 * ct + l16) * WSLOT + ((r + 8 * p) & 15u) + 17 * g16 + 1;
+    }
 
     u32x4 wreg[WLD], areg[ALD];
     auto issue = [&](uint32_t q, int par) __attribute__((always_inline)) {
@@ -183,6 +200,7 @@ __global__ __launch_bounds__(64 * NW) void mx_experts_kernel(KPRE_PARAMS, Matmul
     mxe_f32x16 acc[NT];
 #pragma unroll
     for (int j = 0; j < NT; j++) acc[j] = mxe_f32x16{};
+    mxe_f32x4 acc16[2] = {mxe_f32x4{}, mxe_f32x4{}};
     auto quad = [&](uint32_t q, int par) __attribute__((always_inline)) {
         __syncthreads();  // every wavefront is done with the previous quad's A
 #pragma unroll
@@ -192,6 +210,53 @@ __global__ __launch_bounds__(64 * NW) void mx_experts_kernel(KPRE_PARAMS, Matmul
             if (threadIdx.x + 64 * NW * i < pieces) *reinterpret_cast<u32x4 *>(alds + adst[i]) = areg[i];
         __syncthreads();  // this quad's A is in place
         if (q + 1 < qpart) issue(q + 1, par ^ 1);
+        if constexpr (S16) {
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                if (4 * (q0 + q) + 2 * h >= ksteps) break;  // uniform per wavefront
+                // this lane's block: global block 2 (its step) + g % 2; a dead
+                // block (past k, or the lone last block's partner) multiplies
+                // zeros at scale 1 on both sides
+                const uint32_t gstep = 4 * (q0 + q) + 2 * h + (g16 >> 1);
+                const bool live = 2 * gstep + (g16 & 1) < nblk;
+                const uint32_t ab = a16b + 2 * h * AREC;
+                u32x4 av16[MX_TERMS];
+                u32x2 av8[MX_TERMS];
+#pragma unroll
+                for (int t = 0; t < MX_TERMS; t++) {
+                    av16[t] = *reinterpret_cast<const u32x4 *>(alds + ab + 32 * t + 16 * (g16 & 1));
+                    av8[t] = *reinterpret_cast<const u32x2 *>(alds + ab + MXR_CODES8 + 16 * t + 8 * (g16 & 1));
+                }
+                const uint32_t sa = live ? *reinterpret_cast<const uint32_t *>(alds + ab + MXR_SCALES + 4 * (g16 & 1))
+                                         : 0x7f7f7f7fu;
+#pragma unroll
+                for (int ct = 0; ct < 2; ct++) {
+                    const uint32_t pay = fpay16[ct][par] + 68 * h;
+                    const uint32_t *pw = reinterpret_cast<const uint32_t *>(wlds + (pay & ~3u));
+                    uint32_t w[5];
+#pragma unroll
+                    for (int i = 0; i < 5; i++) w[i] = pw[i];
+                    uint32_t qd[4];
+#pragma unroll
+                    for (int i = 0; i < 4; i++) qd[i] = __builtin_amdgcn_alignbyte(w[i + 1], w[i], pay);
+                    const mxe_i32x8 bv =
+                        live ? mxe_i32x8{(int)qd[0], (int)qd[1], (int)qd[2], (int)qd[3], 0, 0, 0, 0} : mxe_i32x8{};
+                    const int sb = live ? (int)wlds[pay - 1] : 127;
+#pragma unroll
+                    for (int t = 0; t < MX_TERMS; t++) {
+                        const mxe_i32x8 avt{(int)av16[t].x, (int)av16[t].y, (int)av16[t].z, (int)av16[t].w,
+                                            (int)av8[t].x,  (int)av8[t].y,  0,                0};
+                        if (t == 0)
+                            acc16[ct] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(avt, bv, acc16[ct], 2, 4, 0, (int)sa, 0, sb);
+                        else if (t == 1)
+                            acc16[ct] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(avt, bv, acc16[ct], 2, 4, 1, (int)sa, 0, sb);
+                        else
+                            acc16[ct] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(avt, bv, acc16[ct], 2, 4, 2, (int)sa, 0, sb);
+                    }
+                }
+            }
+            return;
+        }
 #pragma unroll
         for (int s = 0; s < 4; s++) {
             const uint32_t step = 4 * (q0 + q) + s;
@@ -244,44 +309,63 @@ __global__ __launch_bounds__(64 * NW) void mx_experts_kernel(KPRE_PARAMS, Matmul
         quad(q, 0);
         if (q + 1 < qpart) quad(q + 1, 1);
     }
+    // The lane's results as (row, column from col0, value): the 32x32 shape
+    // holds column l % 32, rows 8 (v / 4) + 4 (l / 32) + v % 4; the 16x16
+    // shape column 16 ct + l % 16, rows 4 (l / 16) + v.
+    constexpr int NV = S16 ? 8 : 16;
+    float accv[NV];
+    uint32_t rowv[NV], colv[NV];
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        if constexpr (S16) {
+            accv[i] = acc16[i / 4][i % 4];
+            rowv[i] = 4 * g16 + i % 4;
+            colv[i] = 16 * (i / 4) + l16;
+        } else {
+            accv[i] = acc[0][i];
+            rowv[i] = 8 * (i / 4) + 4 * part + (i % 4);
+            colv[i] = c;
+        }
+    }
     if constexpr (KS > 1) {
         // the other K parts' sums to part 0 (the A region is free now)
-        float *red = reinterpret_cast<float *>(lds);  // [KS - 1][WPK][16][64]
+        float *red = reinterpret_cast<float *>(lds);  // [KS - 1][WPK][NV][64]
         __syncthreads();
         if (kh > 0) {
 #pragma unroll
-            for (int v = 0; v < 16; v++) red[(((kh - 1) * WPK + wsub) * 16 + v) * 64 + lane] = acc[0][v];
+            for (int i = 0; i < NV; i++) red[(((kh - 1) * WPK + wsub) * NV + i) * 64 + lane] = accv[i];
         }
         __syncthreads();
         if (kh > 0) return;
 #pragma unroll
         for (int k2 = 0; k2 < KS - 1; k2++)
 #pragma unroll
-            for (int v = 0; v < 16; v++) acc[0][v] += red[((k2 * WPK + wsub) * 16 + v) * 64 + lane];
+            for (int i = 0; i < NV; i++) accv[i] += red[((k2 * WPK + wsub) * NV + i) * 64 + lane];
     }
 
-    // C: lane l holds column l % 32, rows 8 (v / 4) + 4 (l / 32) + v % 4.
-    const uint32_t col = col0 + c;
-    const uint64_t bi = (uint64_t)expert * a.n + min(col, a.n - 1);
     if constexpr (G == MM_GATE_UP) {
         // up sums to the gate wavefront of the same columns (the A region is free now)
-        float *hand = reinterpret_cast<float *>(lds);  // [CT][16][64]
+        float *hand = reinterpret_cast<float *>(lds);  // [CT][NV][64]
         __syncthreads();
         if (upw) {
 #pragma unroll
-            for (int v = 0; v < 16; v++) hand[((wsub - CT) * 16 + v) * 64 + lane] = acc[0][v];
+            for (int i = 0; i < NV; i++) hand[((wsub - CT) * NV + i) * 64 + lane] = accv[i];
         }
         __syncthreads();
         if (upw || col0 >= a.n) return;  // uniform per wavefront
-        const float bg = a.bias ? round_bf16(a.bias[bi]) : 0.f;
-        const float bu = a.bias2 ? round_bf16(a.bias2[bi] + (a.up_one ? 1.0f : 0.0f)) : (a.up_one ? 1.0f : 0.0f);
+        float actv[NV];
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const uint64_t bi = (uint64_t)expert * a.n + min(col0 + colv[i], a.n - 1);
+            const float bg = a.bias ? round_bf16(a.bias[bi]) : 0.f;
+            const float bu = a.bias2 ? round_bf16(a.bias2[bi] + (a.up_one ? 1.0f : 0.0f)) : (a.up_one ? 1.0f : 0.0f);
+            actv[i] = expert_activation(a.act, accv[i] + bg, hand[(wsub * NV + i) * 64 + lane] + bu);
+        }
         if (!a.yrec) {
 #pragma unroll
-            for (int v = 0; v < 16; v++) {
-                const uint32_t r = 8 * (v / 4) + 4 * part + (v % 4);
-                if (r < rows && col < a.n)
-                    reinterpret_cast<float *>(a.y)[(uint64_t)(sorted0 + r) * a.n + col] =
-                        expert_activation(a.act, acc[0][v] + bg, hand[(wsub * 16 + v) * 64 + lane] + bu);
+            for (int i = 0; i < NV; i++) {
+                const uint32_t r = rowv[i], col = col0 + colv[i];
+                if (r < rows && col < a.n) reinterpret_cast<float *>(a.y)[(uint64_t)(sorted0 + r) * a.n + col] = actv[i];
             }
             return;
         }
@@ -291,13 +375,10 @@ __global__ __launch_bounds__(64 * NW) void mx_experts_kernel(KPRE_PARAMS, Matmul
         // live row's lane splits it into the down projection's record (and,
         // for a lone last block, zeros the partner).
         constexpr uint32_t TRS = 36;  // floats per transposed row (16-byte aligned rows)
-        static_assert(16 * TRS * 4 <= WROWS * WSLOT, "the transposed block fits the staging region");
+        static_assert(32 * TRS * 4 <= WROWS * WSLOT, "the transposed block fits the staging region");
         float *tr = reinterpret_cast<float *>(wlds);
 #pragma unroll
-        for (int v = 0; v < 16; v++) {
-            const uint32_t r = 8 * (v / 4) + 4 * part + (v % 4);
-            tr[r * TRS + c] = expert_activation(a.act, acc[0][v] + bg, hand[(wsub * 16 + v) * 64 + lane] + bu);
-        }
+        for (int i = 0; i < NV; i++) tr[rowv[i] * TRS + colv[i]] = actv[i];
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -317,13 +398,11 @@ __global__ __launch_bounds__(64 * NW) void mx_experts_kernel(KPRE_PARAMS, Matmul
             if (!(blk & 1) && blk + 1 == a.n / 32) mx6_zero_block(rec, 1);  // a lone last block
         }
     } else {
-        if (col >= a.n) return;
-        const float b = a.bias ? round_bf16(a.bias[bi]) : 0.f;
 #pragma unroll
-        for (int v = 0; v < 16; v++) {
-            const uint32_t r = 8 * (v / 4) + 4 * part + (v % 4);
-            if (r >= rows) continue;
-            const float val = acc[0][v] + b;
+        for (int i = 0; i < NV; i++) {
+            const uint32_t r = rowv[i], col = col0 + colv[i];
+            if (r >= rows || col >= a.n) continue;
+            const float val = accv[i] + (a.bias ? round_bf16(a.bias[(uint64_t)expert * a.n + col]) : 0.f);
             const uint64_t o = (uint64_t)rid[r] * a.n + col;
             if (a.y_bf16)
                 reinterpret_cast<uint16_t *>(a.y)[o] = f32_to_bf16_bits(val);
