@@ -334,6 +334,7 @@ int oco_expert_expand(const oco_experts *w, const void *x, oco_dtype x_dtype,
 /* Weighted combine with residual: out = bf16(out + bf16(sum_r route_r p_r)).
  * routes: [tokens*k, hidden] of routes_dtype (bf16 in the reference; f32
  * route values are rounded to bf16 before weighting, as stored there).
+ * k <= 8 (the expert banks' limit); OCO_ERR_INVALID beyond.
  * Replaces moe_sum (routing.metal:157-168). */
 int oco_moe_sum(const void *routes, oco_dtype routes_dtype, const float *probs, uint16_t *out,
                 uint32_t hidden, uint32_t tokens, uint32_t k, oco_stream stream);

@@ -419,14 +419,22 @@ __global__ __launch_bounds__(256) void moe_sum_kernel(const RT *routes, const fl
     const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= (uint64_t)hidden * tokens) return;
     const uint64_t t = i / hidden, d = i % hidden;
-    float s = 0.f;
-    for (uint32_t r = 0; r < k; r++) {
-        float v;
+    // all k (<= 8) route values requested before the first FMA
+    float v[8], p[8];
+#pragma unroll
+    for (uint32_t r = 0; r < 8; r++) {
+        if (r >= k) break;
         if constexpr (sizeof(RT) == 4)
-            v = round_bf16(routes[(t * k + r) * hidden + d]);
+            v[r] = round_bf16(routes[(t * k + r) * hidden + d]);
         else
-            v = bf16_bits_to_f32(routes[(t * k + r) * hidden + d].bits);
-        s = fmaf(v, probs[t * k + r], s);
+            v[r] = bf16_bits_to_f32(routes[(t * k + r) * hidden + d].bits);
+        p[r] = probs[t * k + r];
+    }
+    float s = 0.f;
+#pragma unroll
+    for (uint32_t r = 0; r < 8; r++) {
+        if (r >= k) break;
+        s = fmaf(v[r], p[r], s);
     }
     out[i] = f32_to_bf16_bits(bf16_bits_to_f32(out[i]) + round_bf16(s));
 }
@@ -439,14 +447,23 @@ __global__ __launch_bounds__(256) void moe_sum8_kernel(const uint16_t *routes, c
     if (i8 * 8 >= (uint64_t)hidden * tokens) return;
     const uint64_t i = i8 * 8, t = i / hidden, d = i % hidden;
     float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (uint32_t r = 0; r < k; r++) {
-        const uint4 v = *reinterpret_cast<const uint4 *>(routes + (t * k + r) * hidden + d);
-        const float p = probs[t * k + r];
-        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    // all k (<= 8) routes' words requested before the first FMA
+    uint4 rv[8];
+    float pv[8];
+#pragma unroll
+    for (uint32_t r = 0; r < 8; r++) {
+        if (r >= k) break;
+        rv[r] = *reinterpret_cast<const uint4 *>(routes + (t * k + r) * hidden + d);
+        pv[r] = probs[t * k + r];
+    }
+#pragma unroll
+    for (uint32_t r = 0; r < 8; r++) {
+        if (r >= k) break;
+        const uint32_t w[4] = {rv[r].x, rv[r].y, rv[r].z, rv[r].w};
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            s[2 * j] = fmaf(__uint_as_float(w[j] << 16), p, s[2 * j]);
-            s[2 * j + 1] = fmaf(__uint_as_float(w[j] & 0xffff0000u), p, s[2 * j + 1]);
+            s[2 * j] = fmaf(__uint_as_float(w[j] << 16), pv[r], s[2 * j]);
+            s[2 * j + 1] = fmaf(__uint_as_float(w[j] & 0xffff0000u), pv[r], s[2 * j + 1]);
         }
     }
     uint4 o = *reinterpret_cast<const uint4 *>(out + i);
@@ -590,6 +607,7 @@ int oco_moe_sum(const void *routes, oco_dtype routes_dtype, const float *probs, 
     uint64_t n = (uint64_t)hidden * tokens;
     if (!n) return OCO_OK;
     if (!routes || !probs || !out) return fail(OCO_ERR_INVALID, "oco_moe_sum: null pointer");
+    if (k > 8) return fail(OCO_ERR_INVALID, "oco_moe_sum: k=%u routes per token, at most 8", k);
     hipStream_t s = (hipStream_t)stream;
     unsigned grid = (unsigned)((n + 255) / 256);
     if (routes_dtype == OCO_DT_F32)

@@ -69,3 +69,9 @@ def test_argument_validation_without_gpu():
     assert lib.oco_matmul_ws(39, fake, fake, 1, fake, 0, None, ctypes.byref(p), fake, need - 1, None) == 1
     assert b"workspace" in lib.oco_last_error()
     assert lib.oco_route_plan(fake, 64, 32, 8, 0, 0, fake, None) == 1  # tile_rows < 16
+    assert lib.oco_moe_sum(fake, 0, fake, fake, 64, 2, 9, None) == 1  # at most 8 routes per token
+    assert b"at most 8" in lib.oco_last_error()
+    # MXFP4 expert records: 160 bytes per (row, K step of 64) -- three E2M3
+    # terms of 24 bytes per block (two blocks) and the scale words, padded
+    mx = oco_amd.ExpertsDesc(39, 2880, 2880, 32, 4, 0, 1, fake, fake, fake, None, None, None)
+    assert lib.oco_experts_workspace(ctypes.byref(mx), 16) > 16 * 45 * 160 + 64 * 45 * 160

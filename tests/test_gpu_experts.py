@@ -126,10 +126,11 @@ def test_route_plan_bit_exact(lib, batch, experts, tile):
     np.testing.assert_array_equal(got[defined], want[defined])
 
 
-@pytest.mark.parametrize("hidden", [2880, 2884])
-def test_moe_sum(lib, hidden):
-    """hidden % 8 == 0 takes the eight-wide kernel, else the scalar one."""
-    tokens, k = 16, 4
+@pytest.mark.parametrize("hidden,k", [(2880, 4), (2884, 4), (2880, 8), (2884, 1), (2880, 3)])
+def test_moe_sum(lib, hidden, k):
+    """hidden % 8 == 0 takes the eight-wide kernel, else the scalar one; k
+    from 1 to the limit of 8."""
+    tokens = 16
     rng = np.random.default_rng(5)
     routes = O.f32_to_bf16(rng.normal(size=(tokens * k, hidden)).astype(np.float32))
     probs = O.bf16_round(rng.dirichlet(np.ones(k), size=tokens)).astype(np.float32)
