@@ -75,3 +75,8 @@ def test_argument_validation_without_gpu():
     # terms of 24 bytes per block (two blocks) and the scale words, padded
     mx = oco_amd.ExpertsDesc(39, 2880, 2880, 32, 4, 0, 1, fake, fake, fake, None, None, None)
     assert lib.oco_experts_workspace(ctypes.byref(mx), 16) > 16 * 45 * 160 + 64 * 45 * 160
+    # the allocation-free entry point takes what fits its 8 MiB array and
+    # rejects more before any GPU work
+    assert lib.oco_experts_workspace(ctypes.byref(mx), 62) <= 8 << 20 < lib.oco_experts_workspace(ctypes.byref(mx), 63)
+    rc = lib.oco_experts_forward_static(ctypes.byref(mx), fake, None, fake, 0, 63, fake, fake, fake, None, None)
+    assert rc == 1 and b"scratch" in lib.oco_last_error()
