@@ -451,9 +451,6 @@ static int experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype,
     const bool small = mx_small_path(w, tokens);
     const bool fused_select = logits && tokens == 1 && w->experts <= 64 && !small;
     PlanSide sel = {};
-#if defined(OCO_ABL) && OCO_ABL == 4
-    if (logits && !fused_select) OCO_TRY(oco_route_select(logits, tokens, w->experts, w->k, ids, probs, stream));
-#else
     if (logits && !fused_select) {
         sel.logits = logits;
         sel.tokens = tokens;
@@ -461,7 +458,6 @@ static int experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype,
         sel.ids_out = ids;
         sel.probs_out = probs;
     }
-#endif
     const uint32_t routes = tokens * w->k;
     uint8_t *ws = (uint8_t *)workspace;
     uint32_t *plan = (uint32_t *)ws;

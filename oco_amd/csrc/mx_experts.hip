@@ -188,11 +188,7 @@ __global__ __launch_bounds__(64 * NW) void mx_experts_kernel(KPRE_PARAMS, Matmul
         const uint32_t qg = q0 + q, sw = 136 * qg - 8 * (qg & 1), sa = 4 * q * AREC;  // q: this part's quad
 #pragma unroll
         for (int i = 0; i < WLD; i++)
-#if defined(OCO_ABL) && OCO_ABL == 2
-            wreg[i] = u32x4{boff[i][par], sw, (uint32_t)i, 7u};
-#else
             wreg[i] = __builtin_amdgcn_raw_buffer_load_b128(rw[(lane + 64 * i) / 10 / 32], boff[i][par], sw, 0);
-#endif
 #pragma unroll
         for (int i = 0; i < ALD; i++)
             if (threadIdx.x + 64 * NW * i < pieces) areg[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, asrc[i], sa, 0);
@@ -285,10 +281,6 @@ __global__ __launch_bounds__(64 * NW) void mx_experts_kernel(KPRE_PARAMS, Matmul
                 const mxe_i32x8 bv =
                     live ? mxe_i32x8{(int)qd[0], (int)qd[1], (int)qd[2], (int)qd[3], 0, 0, 0, 0} : mxe_i32x8{};
                 const int sb = live ? (int)wlds[pay - 1] : 127;
-#if defined(OCO_ABL) && OCO_ABL == 1
-                acc[j][0] += __int_as_float(bv[0] ^ bv[3] ^ sb ^ (int)sa ^ (int)av16[0].x ^ (int)av8[MX_TERMS - 1].y);
-                continue;
-#endif
 #pragma unroll
                 for (int t = 0; t < MX_TERMS; t++) {
                     const mxe_i32x8 avt{(int)av16[t].x, (int)av16[t].y, (int)av16[t].z, (int)av16[t].w,
