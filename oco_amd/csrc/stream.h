@@ -146,6 +146,23 @@ struct Tile<OCO_Q8_0> {
     }
 };
 
+// (scale, min) of sub-blocks 2g and 2g + 1 of a Q4_K / Q5_K super-block
+// (get_scale_min_k4, weights.metal:67-77) as the bytes [sc0, sc1, mn0, mn1]
+// of one word, from scales[12] = hdr.y (bytes 0..3), hdr.z (4..7), hdr.w
+// (8..11).  Sub-block j < 4 has sc = scales[j] & 63, mn = scales[j + 4] & 63;
+// j >= 4 has sc = (scales[j + 4] & 15) | (scales[j - 4] >> 6) << 4 and mn =
+// (scales[j + 4] >> 4) | (scales[j] >> 6) << 4.  Both forms read bytes b,
+// b + 1 (b = 2 (g & 1)) of hdr.y and hdr.z, the second also of hdr.w, so two
+// byte permutes gather them (the byte conversions v_cvt_f32_ubyte0..3 then
+// take each value straight from the word).
+__device__ __forceinline__ uint32_t k_scale_min(const uint4 &hdr, uint32_t g) {
+    const uint32_t b = 2u * (g & 1u);
+    const uint32_t sel = b | ((b + 1) << 8) | ((b + 4) << 16) | ((b + 5) << 24);
+    const uint32_t yz = __builtin_amdgcn_perm(hdr.z, hdr.y, sel);  // y_b, y_b1, z_b, z_b1
+    const uint32_t ww = __builtin_amdgcn_perm(hdr.w, hdr.w, (sel & 0xffffu) | ((sel & 0xffffu) << 16));  // w_b, w_b1, w_b, w_b1
+    return g < 2 ? yz & 0x3f3f3f3fu : (ww & 0x00000f0fu) | ((ww >> 4) & 0x0f0f0000u) | ((yz >> 2) & 0x30303030u);
+}
+
 // Q4_K: piece c of a super-block = qs bytes 16c..16c+15; low nibbles are
 // columns 64g + 16(c&1) + i of sub-block 2g, high nibbles columns
 // 64g + 32 + 16(c&1) + i of sub-block 2g+1 (g = c/2).  The 16-byte header
@@ -195,22 +212,8 @@ struct Tile<OCO_Q4_K> {
     }
     __device__ __forceinline__ static float dot(const Raw &r, const float *x, const float *s, int c) {
         const uint32_t g = (uint32_t)c >> 1;
-        // (scale, min) of sub-blocks 2g and 2g+1 (weights.metal:70-71) from
-        // scales[12] = hdr.y (bytes 0..3), hdr.z (4..7), hdr.w (8..11):
-        // runtime bit offsets, one select between the j < 4 and j >= 4
-        // forms (a runtime index into a byte array costs a compare/select
-        // chain per byte).
-        uint32_t scm[2][2];
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const uint32_t t = 8 * ((2 * g + h) & 3);
-            const uint32_t sc_lo = __builtin_amdgcn_ubfe(r.hdr.y, t, 6), mn_lo = __builtin_amdgcn_ubfe(r.hdr.z, t, 6);
-            const uint32_t sc_hi = __builtin_amdgcn_ubfe(r.hdr.w, t, 4) | (__builtin_amdgcn_ubfe(r.hdr.y, t + 6, 2) << 4);
-            const uint32_t mn_hi = __builtin_amdgcn_ubfe(r.hdr.w, t + 4, 4) | (__builtin_amdgcn_ubfe(r.hdr.z, t + 6, 2) << 4);
-            scm[h][0] = g < 2 ? sc_lo : sc_hi;
-            scm[h][1] = g < 2 ? mn_lo : mn_hi;
-        }
-        const uint32_t sc0 = scm[0][0], mn0 = scm[0][1], sc1 = scm[1][0], mn1 = scm[1][1];
+        const uint32_t scm = k_scale_min(r.hdr, g);
+        const float sc0 = ub(scm, 0), sc1 = ub(scm, 1), mn0 = ub(scm, 2), mn1 = ub(scm, 3);
         const uint32_t w[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
         const float d = half_bits_to_f32(r.hdr.x & 0xffffu), dmin = half_bits_to_f32(r.hdr.x >> 16);
         float a0 = 0.f, a1 = 0.f;
@@ -228,8 +231,8 @@ struct Tile<OCO_Q4_K> {
             a0 = fmaf(l1.y, x[4 * j + 3], a0);
             a1 = fmaf(h1.y, x[16 + 4 * j + 3], a1);
         }
-        const float v = fmaf(d * (float)sc0, a0, -(dmin * (float)mn0) * s[0]);
-        return fmaf(d * (float)sc1, a1, fmaf(-(dmin * (float)mn1), s[1], v));
+        const float v = fmaf(d * sc0, a0, -(dmin * mn0) * s[0]);
+        return fmaf(d * sc1, a1, fmaf(-(dmin * mn1), s[1], v));
     }
 };
 
@@ -411,16 +414,7 @@ struct Tile<OCO_Q5_K> {
     }
     __device__ __forceinline__ static float dot(const Raw &r, const float *x, const float *s, int c) {
         const uint32_t g = (uint32_t)c >> 1;
-        uint32_t scm[2][2];
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const uint32_t t = 8 * ((2 * g + h) & 3);
-            const uint32_t sc_lo = __builtin_amdgcn_ubfe(r.hdr.y, t, 6), mn_lo = __builtin_amdgcn_ubfe(r.hdr.z, t, 6);
-            const uint32_t sc_hi = __builtin_amdgcn_ubfe(r.hdr.w, t, 4) | (__builtin_amdgcn_ubfe(r.hdr.y, t + 6, 2) << 4);
-            const uint32_t mn_hi = __builtin_amdgcn_ubfe(r.hdr.w, t + 4, 4) | (__builtin_amdgcn_ubfe(r.hdr.z, t + 6, 2) << 4);
-            scm[h][0] = g < 2 ? sc_lo : sc_hi;
-            scm[h][1] = g < 2 ? mn_lo : mn_hi;
-        }
+        const uint32_t scm = k_scale_min(r.hdr, g);
         const uint32_t w[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
         const uint32_t hb[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
         float a0 = 0.f, a1 = 0.f;
@@ -435,8 +429,8 @@ struct Tile<OCO_Q5_K> {
             }
         }
         const float d = half_bits_to_f32(r.hdr.x & 0xffffu), dmin = half_bits_to_f32(r.hdr.x >> 16);
-        const float v = fmaf(d * (float)scm[0][0], a0, -(dmin * (float)scm[0][1]) * s[0]);
-        return fmaf(d * (float)scm[1][0], a1, fmaf(-(dmin * (float)scm[1][1]), s[1], v));
+        const float v = fmaf(d * ub(scm, 0), a0, -(dmin * ub(scm, 2)) * s[0]);
+        return fmaf(d * ub(scm, 1), a1, fmaf(-(dmin * ub(scm, 3)), s[1], v));
     }
 };
 
