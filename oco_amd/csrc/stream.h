@@ -100,11 +100,12 @@ struct Tile<OCO_MXFP4> {
     }
 };
 
-// Q8_0: piece = block {f16 d, int8 q[32]}.  Codes enter as unsigned bytes
-// q + 128 (exact), corrected by 128 * sum(x).
+// Q8_0: piece = block {f16 d, int8 q[32]}.  Each code converts straight
+// from its sign-extended byte (v_cvt_f32_i32 with a byte select), so the
+// block needs no activation sum.
 template <>
 struct Tile<OCO_Q8_0> {
-    static constexpr int BLOCK = 32, BYTES = 34, P = 1, NSUM = 1;
+    static constexpr int BLOCK = 32, BYTES = 34, P = 1, NSUM = 0;
     struct Raw {
         uint4 a, b;
         uint32_t d;
@@ -115,12 +116,7 @@ struct Tile<OCO_Q8_0> {
     }
     // float4 index of run t of piece p (the inverse of map)
     __device__ __forceinline__ static uint32_t unmap(uint32_t p, uint32_t t) { return p * 8 + t; }
-    __device__ __forceinline__ static void sums(const float *x, float *s) {
-        float a = 0.f;
-#pragma unroll
-        for (int i = 0; i < 32; i++) a += x[i];
-        s[0] = a;
-    }
+    __device__ __forceinline__ static void sums(const float *, float *) {}
     __device__ __forceinline__ static Raw load(const uint8_t *blk, int) {
         Raw r;
         r.d = lds_u16(blk);
@@ -130,19 +126,18 @@ struct Tile<OCO_Q8_0> {
         r.b = make_uint4(o[4], o[5], o[6], o[7]);
         return r;
     }
-    __device__ __forceinline__ static float dot(const Raw &r, const float *x, const float *s) {
+    __device__ __forceinline__ static float dot(const Raw &r, const float *x, const float *) {
         const uint32_t w[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
         float a0 = 0.f, a1 = 0.f;
 #pragma unroll
         for (int j = 0; j < 8; j += 2) {
-            uint32_t u0 = w[j] ^ 0x80808080u, u1 = w[j + 1] ^ 0x80808080u;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                a0 = fmaf(ub(u0, i), x[4 * j + i], a0);
-                a1 = fmaf(ub(u1, i), x[4 * j + 4 + i], a1);
+                a0 = fmaf((float)(int8_t)(w[j] >> (8 * i)), x[4 * j + i], a0);
+                a1 = fmaf((float)(int8_t)(w[j + 1] >> (8 * i)), x[4 * j + 4 + i], a1);
             }
         }
-        return half_bits_to_f32(r.d) * fmaf(-128.f, s[0], a0 + a1);
+        return half_bits_to_f32(r.d) * (a0 + a1);
     }
 };
 
