@@ -101,25 +101,22 @@ struct Piece<OCO_Q8_0> {
     static constexpr int BLOCK = 32, BYTES = 34, P = 4, E = 8;
     struct X {
         float v[8];
-        float sum;
     };
     template <typename XT>
     __device__ __forceinline__ static void load_x(const XT *xr, uint32_t block, int piece, X &x) {
         XLoad<XT>::template run<8>(xr + block * 32 + piece * 8, x.v);
-        x.sum = ((x.v[0] + x.v[1]) + (x.v[2] + x.v[3])) + ((x.v[4] + x.v[5]) + (x.v[6] + x.v[7]));
     }
     __device__ __forceinline__ static float dot(const WSrc &w, uint32_t b, int piece, const X &x) {
         uint2 q = w.u64(b + 2 + piece * 8);
         float d = half_bits_to_f32(w.u16(b));
-        // Signed codes as unsigned bytes q + 128: sum q x = sum (q+128) x - 128 sum x.
-        uint32_t u0 = q.x ^ 0x80808080u, u1 = q.y ^ 0x80808080u;
+        // each code straight from its sign-extended byte
         float s0 = 0.f, s1 = 0.f;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            s0 = fmaf(ub(u0, i), x.v[i], s0);
-            s1 = fmaf(ub(u1, i), x.v[4 + i], s1);
+            s0 = fmaf((float)(int8_t)(q.x >> (8 * i)), x.v[i], s0);
+            s1 = fmaf((float)(int8_t)(q.y >> (8 * i)), x.v[4 + i], s1);
         }
-        return d * fmaf(-128.f, x.sum, s0 + s1);
+        return d * (s0 + s1);
     }
 };
 

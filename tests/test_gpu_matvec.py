@@ -216,6 +216,14 @@ def test_matvec_stream_x_source(lib, direct, xreg):
         _stream_plan_cases(lib, f"direct {direct} xreg {xreg}")
 
 
+def test_matvec_plain_kernel(lib):
+    """The plain (non-streaming) matvec, which quantized formats take when
+    the activations are not vector-aligned, forced on every format with the
+    MATVEC_PLAIN knob."""
+    with lib.overridden(lib.Knob.MATVEC_PLAIN, [1]):
+        _stream_plan_cases(lib, "plain")
+
+
 def _stream_plan_cases(lib, plan):
     from oco_amd import synth
     for fmt, n, k in [(O.MXFP4, 131, 2880), (P.Q8_0, 77, 4096), (P.Q4_K, 257, 2048), (P.Q6_K, 300, 4096),
