@@ -339,17 +339,31 @@ __global__ __launch_bounds__(PLAN_THREADS) void route_plan_kernel(const uint32_t
     }
     if (one_pass) {
         __syncthreads();  // offs[] is complete
+        // Every route's place goes to an expert-sorted array in LDS first,
+        // (expert << 16) | route, and the lists and descriptors are written
+        // from it in sorted order: consecutive threads then store consecutive
+        // words, where storing from each route's own thread scatters every
+        // wavefront instruction over 64 lines through this one CU's address
+        // unit.
+        uint32_t *srt = hist + max(16 * experts, (nchunks * 16 + 1) * experts);
 #pragma unroll
         for (uint32_t c = 0; c < PLAN_ONEPASS_CHUNKS; c++) {
             if (c >= nchunks) break;  // uniform
             const uint32_t e = ev[c], i = c * PLAN_THREADS + tid;
             if (e < experts) {
                 const uint32_t pos = hist[e * (nchunks * 16 + 1) + c * 16 + wave] + rk[c];
-                plan[grouped + (uint64_t)e * (routes + 1) + 1 + pos] = i;
+                srt[offs[e] + pos] = (e << 16) | i;
                 plan[sorted + experts + i] = offs[e] + pos;
-                if (side.desc)
-                    side.desc[(uint64_t)(tbase[e] + pos / tile_rows) * DW + PLAN_DESC_HEAD + pos % tile_rows] = i;
             }
+        }
+        uint32_t placed = 0;  // routes with a valid expert: the per-wavefront count sums of step 2
+        for (uint32_t w = 0; w < 16; w++) placed += wsum[w];
+        __syncthreads();
+        for (uint32_t j = tid; j < placed; j += PLAN_THREADS) {
+            const uint32_t v = srt[j], e = v >> 16, i = v & 0xffffu, pos = j - offs[e];
+            plan[grouped + (uint64_t)e * (routes + 1) + 1 + pos] = i;
+            if (side.desc)
+                side.desc[(uint64_t)(tbase[e] + pos / tile_rows) * DW + PLAN_DESC_HEAD + pos % tile_rows] = i;
         }
         return;
     }
@@ -496,12 +510,18 @@ int route_plan_launch(const uint32_t *ids, uint32_t routes, uint32_t experts, ui
     const uint64_t side_blocks =
         std::max<uint64_t>((side_items + PLAN_THREADS - 1) / PLAN_THREADS, (sj.nzero + PLAN_THREADS - 1) / PLAN_THREADS);
     if (side_blocks >= 0x7fffffffu) return fail(OCO_ERR_INVALID, "oco_route_plan: side job of %llu elements", (unsigned long long)sj.n);
-    hipLaunchKernelGGL(route_plan_kernel, dim3(1 + (unsigned)side_blocks), dim3(PLAN_THREADS),
-                       (size_t)(PLAN_THREADS + 3 * experts +
-                                (plan_one_pass(routes, experts) ? std::max(16 * experts, ((routes + 1023) / 1024 * 16 + 1) * experts)
-                                 : experts <= PLAN_HIST_EXPERTS  ? 16 * experts
-                                                                 : 0)) * 4,
-                       stream, ids, routes, experts, tile_rows, up_tiles, down_tiles, plan, sj);
+    // LDS words: chunk ids, run / tile base / offset per expert, then the
+    // histograms and (one pass) the expert-sorted routes.
+    const size_t lds = (size_t)(PLAN_THREADS + 3 * experts +
+                                (plan_one_pass(routes, experts)
+                                     ? std::max(16 * experts, ((routes + 1023) / 1024 * 16 + 1) * experts) + routes
+                                 : experts <= PLAN_HIST_EXPERTS ? 16 * experts
+                                                                : 0)) * 4;
+    if (lds > 64 * 1024)
+        OCO_TRY(hip_check(hipFuncSetAttribute((const void *)route_plan_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+                          "hipFuncSetAttribute"));
+    hipLaunchKernelGGL(route_plan_kernel, dim3(1 + (unsigned)side_blocks), dim3(PLAN_THREADS), lds, stream, ids, routes,
+                       experts, tile_rows, up_tiles, down_tiles, plan, sj);
     return launch_check("oco_route_plan");
 }
 
