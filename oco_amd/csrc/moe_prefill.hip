@@ -44,6 +44,11 @@ typedef float q4f32x4 __attribute__((ext_vector_type(4)));
 struct Q4Raw {  // one lane's bytes of one super-block: header and its 32 qs bytes
     uint4 hdr, q0, q1;
 };
+// A wavefront's weights of one step as loaded: its 32 rows' super-blocks
+// (144 bytes each), 288 16-byte chunks, chunk lane + 64 i in c[i].
+struct Q4Set {
+    uint4 c[5];
+};
 
 // Scales of sub-block pair q: a = d sc, m = dmin mn for the low (0) and high
 // (1) nibbles (get_scale_min_k4, weights.metal:67-77).
@@ -177,7 +182,7 @@ __global__ __launch_bounds__(64 * NW) void moe_q4k_kernel(KPRE_PARAMS, MatmulArg
     constexpr int XL = ROWS / (2 * NW);  // activation loads per lane per step (16 bytes each)
     constexpr int STAGE = ROWS * 512;    // one super-block of f16 rows
     constexpr int COLS = G == MM_GATE_UP ? 16 : 32;
-    constexpr int LOADS = XL + 6;        // vector loads per lane per step
+    constexpr int LOADS = XL + 5;        // vector loads per lane per step
     static_assert(ROWS % (2 * NW) == 0, "whole 16-byte runs per lane");
     static_assert(Q4_TILES * ROWS <= 64 * NW, "one thread per (tile, row) in the prologue");
     // Three separate arrays, so the compiler can tell an LDS load of one stage
@@ -188,6 +193,9 @@ __global__ __launch_bounds__(64 * NW) void moe_q4k_kernel(KPRE_PARAMS, MatmulArg
     __shared__ __attribute__((aligned(16))) float t_inv[G == MM_DOWN ? Q4_TILES : 1][ROWS];
     __shared__ __attribute__((aligned(16))) uint32_t t_info[Q4_TILES][4];  // expert, rows, first sorted row
     __shared__ float u_bias[Q4_UNITS][2 * 16 * NW];  // gate/up: gate then up biases; down: biases
+    // Each wavefront's weights of the step it computes, [row][144 bytes]
+    // (320 chunk slots: the loads past the 288 land in the tail).
+    __shared__ __attribute__((aligned(16))) uint8_t wst[NW * 5120];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c16 = lane & 15, q = lane >> 4;
     const uint32_t grid = gridDim.x, lg = xcd_order(blockIdx.x, grid);
@@ -247,7 +255,7 @@ __global__ __launch_bounds__(64 * NW) void moe_q4k_kernel(KPRE_PARAMS, MatmulArg
     // Prefetch cursor: unit pu, super-block psb; per-lane source offsets.
     uint32_t pu = lo, psb = 0;
     uint32_t xoff[XL];
-    gbytes wrow[2];
+    gbytes cptr[5];
     auto set_unit = [&](uint32_t u) __attribute__((always_inline)) {
         const uint32_t y = u / chunks, ch = u - y * chunks, ti = y - y0;
         const uint32_t expert = __builtin_amdgcn_readfirstlane(t_info[ti][0]);
@@ -259,29 +267,31 @@ __global__ __launch_bounds__(64 * NW) void moe_q4k_kernel(KPRE_PARAMS, MatmulArg
             const uint32_t src = G == MM_GATE_UP ? t_route[ti][r] / a.topk : sorted0 + min(r, rows - 1);
             xoff[i] = (uint32_t)(src * xrow) + 16 * j;
         }
+        // Weight chunk j = lane + 64 i: row j / 9 of the wavefront's 32
+        // (fragment f = row / 16), 16-byte piece j % 9 of its super-block.
+        const uint64_t eoff = (uint64_t)expert * a.expert_bytes;
+        const gbytes bank0 = gp(a.w) + eoff, bank1 = gp(G == MM_GATE_UP ? a.w2 : a.w) + eoff;
 #pragma unroll
-        for (int f = 0; f < 2; f++) {
-            const uint32_t col = ch * (NW * COLS) + wave * COLS + (G == MM_GATE_UP ? 0 : 16 * f) + c16;
-            const gbytes base = gp((G == MM_GATE_UP && f == 1 ? a.w2 : a.w) + (uint64_t)expert * a.expert_bytes);
-            wrow[f] = base + (uint64_t)min(col, a.n - 1) * a.row_bytes;
+        for (int i = 0; i < 5; i++) {
+            const uint32_t j = min(lane + 64u * i, 287u), r = j / 9, p = j - 9 * r, f = r >> 4;
+            const uint32_t col = ch * (NW * COLS) + wave * COLS + (G == MM_GATE_UP ? 0 : 16 * f) + (r & 15);
+            const uint64_t off = (uint64_t)min(col, a.n - 1) * a.row_bytes + 16 * p;
+            cptr[i] = (G == MM_GATE_UP && f ? bank1 : bank0) + off;
         }
     };
     // Refill of stage nst / register set wn for the cursor's step, as
-    // LOADS items: 0..5 the weight loads (fragment k / 3: header, then the
-    // two halves of the lane's qs bytes), 6.. the activation rows.  The
+    // LOADS items: 0..4 the weight chunks (whole lines per instruction:
+    // each row's super-block is nine consecutive chunks), 5.. the activation
+    // rows.  The
     // items are spread over the eight MFMA chunks of a step: issued all at
     // once, every wavefront's loads queued behind each other's at the
     // address units.
-    auto load_item = [&](auto kk, int nst, Q4Raw *wn) __attribute__((always_inline)) {
+    auto load_item = [&](auto kk, int nst, Q4Set *wn) __attribute__((always_inline)) {
         constexpr int K = decltype(kk)::value;
-        if constexpr (K < 6) {
-            constexpr int f = K / 3, part = K % 3;
-            const gbytes blk = wrow[f] + psb * 144;
-            if constexpr (part == 0) wn[f].hdr = ld_u128(blk);
-            if constexpr (part == 1) wn[f].q0 = ld_u128(blk + 16 + 32 * q);
-            if constexpr (part == 2) wn[f].q1 = ld_u128(blk + 32 + 32 * q);
+        if constexpr (K < 5) {
+            wn->c[K] = ld_u128(cptr[K] + psb * 144);
         } else {
-            constexpr int i = K - 6;
+            constexpr int i = K - 5;
             uint8_t *stage = nst == 0 ? xs0 : nst == 1 ? xs1 : xs2;
             q4_load_lds16(x8 + xoff[i] + psb * 512, stage + (wave + NW * i) * 1024);
         }
@@ -300,7 +310,33 @@ __global__ __launch_bounds__(64 * NW) void moe_q4k_kernel(KPRE_PARAMS, MatmulArg
 
     // One step: eight MFMA chunks of 32 k, each issuing its share of the
     // refill for step t + 2.
-    auto compute = [&](int st, const Q4Raw *r, int nst, Q4Raw *wn) __attribute__((always_inline)) {
+    auto compute = [&](int st, const Q4Set *wc, int nst, Q4Set *wn) __attribute__((always_inline)) {
+        // The step's chunks through the wavefront's LDS region to the lanes
+        // that decode them: lane (c16, q) takes fragment f's row 16 f + c16,
+        // its header and its pair q of qs halves.
+        uint8_t *ws = wst + wave * 5120;
+#pragma unroll
+        for (int i = 0; i < 5; i++) *reinterpret_cast<uint4 *>(ws + 16 * (lane + 64 * i)) = wc->c[i];
+        // (Reads as inline asm, with their own wait: the compiler cannot tell
+        // this region from the ring's stages and would wait for every
+        // global->LDS load in flight.)
+        asm volatile("" ::: "memory");  // the writes stay above the reads
+        q4u32x4 v[6];
+#pragma unroll
+        for (int f = 0; f < 2; f++) {
+            const uint8_t *blk = ws + (16 * f + c16) * 144;
+            v[3 * f] = q4_lds_b128(blk);
+            v[3 * f + 1] = q4_lds_b128(blk + 16 + 32 * q);
+            v[3 * f + 2] = q4_lds_b128(blk + 32 + 32 * q);
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]));
+        Q4Raw r[2];
+#pragma unroll
+        for (int f = 0; f < 2; f++) {
+            __builtin_memcpy(&r[f].hdr, &v[3 * f], 16);
+            __builtin_memcpy(&r[f].q0, &v[3 * f + 1], 16);
+            __builtin_memcpy(&r[f].q1, &v[3 * f + 2], 16);
+        }
         const uint8_t *xb = (st == 0 ? xs0 : st == 1 ? xs1 : xs2) + c16 * 512;
         const Q4Scales s0 = q4_scales(r[0].hdr, q), s1 = q4_scales(r[1].hdr, q);
         auto chunk = [&](auto cc) __attribute__((always_inline)) {
@@ -404,27 +440,23 @@ __global__ __launch_bounds__(64 * NW) void moe_q4k_kernel(KPRE_PARAMS, MatmulArg
     // Step t computes stage t % 3 with register set t % 3 and refills stage
     // and set (t + 2) % 3, consumed at step t - 1; past the last step the
     // refills repeat the last unit's first super-block, never consumed.
-    Q4Raw w0[2], w1[2], w2[2];
+    Q4Set w0, w1, w2;
     set_unit(lo);
     // Steps 0 and 1's loads.
-    q4_static_for<0, LOADS>([&](auto kk) { load_item(kk, 0, w0); });
+    q4_static_for<0, LOADS>([&](auto kk) { load_item(kk, 0, &w0); });
     advance();
-    q4_static_for<0, LOADS>([&](auto kk) { load_item(kk, 1, w1); });
+    q4_static_for<0, LOADS>([&](auto kk) { load_item(kk, 1, &w1); });
     advance();
     uint32_t cu = lo, csb = 0;
     bool pend = false;  // unit cu - 1's results are in acc, not yet stored
     // Start of step t (compute register set wc): its loads landed in every
     // wavefront, a finished unit's stores go out, and wc is marked in use
     // (the compiler's own wait for it then sits here, where it has landed).
-    auto start = [&](int t, const Q4Raw *wc) __attribute__((always_inline)) {
+    auto start = [&](int t, const Q4Set *wc) __attribute__((always_inline)) {
         q4_vm_wait<LOADS>();                      // step t's loads (step t + 1's may be in flight)
         asm volatile("s_barrier" ::: "memory");  // every wavefront's LDS loads landed; stage (t + 2) % 3 is free
 #pragma unroll
-        for (int f = 0; f < 2; f++) {
-            q4_touch(wc[f].hdr);
-            q4_touch(wc[f].q0);
-            q4_touch(wc[f].q1);
-        }
+        for (int i = 0; i < 5; i++) q4_touch(wc->c[i]);
         // A finished unit's stores go out before this step's loads, so that
         // reusing their registers later waits only as far as those loads.
         if (pend) {
@@ -432,7 +464,7 @@ __global__ __launch_bounds__(64 * NW) void moe_q4k_kernel(KPRE_PARAMS, MatmulArg
             pend = false;
         }
     };
-    auto body = [&](int st, int t, const Q4Raw *wc, Q4Raw *wn) __attribute__((always_inline)) {
+    auto body = [&](int st, int t, const Q4Set *wc, Q4Set *wn) __attribute__((always_inline)) {
         compute(st, wc, (st + 2) % 3, wn);  // issues step t + 2's loads on the way
         if (++csb == nsb) {
             csb = 0;
@@ -443,17 +475,17 @@ __global__ __launch_bounds__(64 * NW) void moe_q4k_kernel(KPRE_PARAMS, MatmulArg
     // The loop starts with step t's compute (its start is the previous
     // iteration's last act, or the prologue's), so that its entry and its
     // back edge hold the same loads in flight.
-    start(0, w0);
+    start(0, &w0);
     for (int t = 0;; t += 3) {
-        body(0, t, w0, w2);
+        body(0, t, &w0, &w2);
         if (t + 1 >= (int)T) break;
-        start(t + 1, w1);
-        body(1, t + 1, w1, w0);
+        start(t + 1, &w1);
+        body(1, t + 1, &w1, &w0);
         if (t + 2 >= (int)T) break;
-        start(t + 2, w2);
-        body(2, t + 2, w2, w1);
+        start(t + 2, &w2);
+        body(2, t + 2, &w2, &w1);
         if (t + 3 >= (int)T) break;
-        start(t + 3, w0);
+        start(t + 3, &w0);
     }
     epilogue(cu - 1);  // the last unit ends on the last step
     q4_vm_wait<0>();  // no LDS load may land after the workgroup exits
