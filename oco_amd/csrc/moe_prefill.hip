@@ -14,7 +14,8 @@
 // -- for the weights, byte 32 q + 8 (c % 4) + e, nibble c / 4; for the
 // activations, a contiguous 16-byte run of the staged row.  A lane decodes
 // exactly the weights it multiplies (half(d sc q - dmin mn), as the
-// reference's half tiles: tile.metal:35-52); no weight goes through LDS.
+// reference's half tiles: tile.metal:35-52); weights pass through LDS as raw
+// bytes only, never decoded.
 //
 // Work: a unit is (route-plan tile of 16 MI rows, column chunk of NW x 16
 // gate/up columns or NW x 32 down columns).  The grid is persistent: each
@@ -24,7 +25,10 @@
 //   - activations of the step two ahead go straight from global memory into
 //     a three-stage LDS ring (global_load_lds_dwordx4, no registers), rows
 //     swizzled so that the MFMA A reads are conflict-free;
-//   - weights of the step two ahead load into a three-set register ring;
+//   - weights of the step two ahead load into a three-set register ring as
+//     whole-line chunks (each row's 144-byte super-block is nine consecutive
+//     16-byte chunks), and at the step pass through a per-wavefront LDS
+//     region to the lanes that decode them;
 //   - the wavefront decodes and multiplies its two 16-row fragments
 //     (gate/up: the 16 gate rows and the same 16 up rows, so the activation
 //     is fused in-lane; down: two groups of 16 rows).
