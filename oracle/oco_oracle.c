@@ -173,7 +173,7 @@ static float decode(uint32_t fmt, const uint8_t *b, uint32_t j) {
         uint32_t s = j / 32;
         const uint8_t *sc = b + 4;
         uint32_t scale = s < 4 ? (sc[s] & 63u) : ((sc[s + 4] & 15u) | ((sc[s - 4] >> 6) << 4));
-        uint32_t mn = s < 4 ? (sc[s + 4] & 63u) : ((sc[s + 4] >> 4) | ((sc[s] >> 6) << 4));
+        uint32_t mn = s < 4 ? (sc[s + 4] & 63u) : ((uint32_t)(sc[s + 4] >> 4) | ((uint32_t)(sc[s] >> 6) << 4));
         uint32_t q = (b[(fmt == OO_Q4_K ? 16 : 48) + j / 64 * 32 + j % 32] >> (s % 2 * 4)) & 15u;
         if (fmt == OO_Q5_K)
             q |= ((b[16 + j % 32] >> s) & 1u) << 4;
