@@ -96,16 +96,24 @@ def test_router_logits(lib, tokens, hidden, experts, dtype, offset):
     np.testing.assert_array_equal(ib.download(np.uint32).reshape(tokens, k), want_ids)
 
 
-@pytest.mark.parametrize("batch,experts,tile", [(1, 32, 16), (17, 32, 64), (257, 32, 64), (512, 128, 16),
-                                                (600, 128, 32), (2048, 128, 64), (300, 256, 16)])
-def test_route_plan_bit_exact(lib, batch, experts, tile):
-    say("route_plan", batch, experts, tile)
+@pytest.mark.parametrize("batch,experts,tile,invalid", [(1, 32, 16, 0), (17, 32, 64, 0), (257, 32, 64, 0),
+                                                        (512, 128, 16, 0), (600, 128, 32, 0), (2048, 128, 64, 0),
+                                                        (300, 256, 16, 0), (700, 64, 16, 1), (3000, 64, 32, 1)])
+def test_route_plan_bit_exact(lib, batch, experts, tile, invalid):
+    """The one-pass plan (up to 8 chunks of 1024 routes) and the chunked one
+    (3000 x 8 routes); `invalid`: about 5% of the ids are >= experts, which
+    the plan leaves out (routing.metal:4-39 skips them too)."""
+    say("route_plan", batch, experts, tile, invalid)
     if experts == 32 and batch > 1:
         ids = P.expert_ids(batch)
     elif batch == 1:
         ids = np.array([3, 0, 2, 1], np.uint32)
     else:
-        ids = np.random.default_rng(3).integers(0, experts, batch * 8).astype(np.uint32)
+        rng = np.random.default_rng(3)
+        ids = rng.integers(0, experts, batch * 8).astype(np.uint32)
+        if invalid:
+            bad = rng.random(ids.size) < 0.05
+            ids[bad] = experts + rng.integers(0, 1000, int(bad.sum())).astype(np.uint32)
     routes = ids.size
     words = lib.route_plan_words(routes, experts)
     assert words == O.route_plan_words(routes, experts)
@@ -123,6 +131,8 @@ def test_route_plan_bit_exact(lib, batch, experts, tile):
         base = grouped + e * (routes + 1)
         defined[base:base + 1 + want[base]] = True
     defined[grouped + experts * (routes + 1):] = True
+    # a left-out route has no row (the reference never writes it)
+    defined[grouped + experts * (routes + 1) + experts + np.nonzero(ids >= experts)[0]] = False
     np.testing.assert_array_equal(got[defined], want[defined])
 
 
