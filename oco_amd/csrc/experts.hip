@@ -373,19 +373,27 @@ constexpr uint32_t MOE_MX_TOKENS = 4;  // measured (gpt-oss): B=4 on these tiles
 // multiplies the gain back out, also exactly.  Four elements per thread
 // (cols % 4 == 0).
 __global__ __launch_bounds__(256) void act_f16_kernel(const float *x, const uint32_t *rowmax, uint16_t *y,
-                                                      uint32_t cols, uint64_t n) {
-    const uint64_t i = ((uint64_t)blockIdx.x * 256 + threadIdx.x) * 4;
-    if (i >= n) return;
-    const float g = row_gain(rowmax[i / cols]);
-    const float4 v = *reinterpret_cast<const float4 *>(x + i);
-    const float e[4] = {v.x * g, v.y * g, v.z * g, v.w * g};
-    uint16_t b[4];
+                                                      uint32_t cols8, uint32_t n8) {
+    // Eight values per thread (cols % 8 == 0: one row each), 32-byte loads,
+    // one 16-byte store.
+    const uint32_t i8 = blockIdx.x * 256 + threadIdx.x;
+    if (i8 >= n8) return;
+    const float g = row_gain(gp(rowmax)[i8 / cols8]);
+    const auto src = gp(reinterpret_cast<const u32x4 *>(x) + 2 * (uint64_t)i8);
+    const u32x4 v0 = src[0], v1 = src[1];
+    const uint32_t vb[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    float e[8];
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
+    for (int j = 0; j < 8; j++) e[j] = __uint_as_float(vb[j]) * g;
+    uint32_t b[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
         const _Float16 h = (_Float16)e[j];
-        __builtin_memcpy(&b[j], &h, 2);
+        uint16_t u;
+        __builtin_memcpy(&u, &h, 2);
+        b[j] = u;
     }
-    *reinterpret_cast<uint2 *>(y + i) = make_uint2(b[0] | ((uint32_t)b[1] << 16), b[2] | ((uint32_t)b[3] << 16));
+    gp(reinterpret_cast<u32x4 *>(y))[i8] = u32x4{b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16)};
 }
 
 }  // namespace oco
@@ -592,9 +600,11 @@ static int experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype,
         d.x = act;
         d.x_f16 = 1;
         if (q4) {
-            const uint64_t na = (uint64_t)routes * w->ffn;
-            hipLaunchKernelGGL(act_f16_kernel, dim3((unsigned)((na / 4 + 255) / 256)), dim3(256), 0, s, act, rowmax,
-                               act16, w->ffn, na);
+            const uint64_t n8 = (uint64_t)routes * w->ffn / 8;  // ffn % 256 == 0 (Q4_K rows)
+            if (n8 > 0xffffffffull - 255)
+                return fail(OCO_ERR_INVALID, "experts: %llu activations", (unsigned long long)n8 * 8);
+            hipLaunchKernelGGL(act_f16_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, s, act, rowmax,
+                               act16, w->ffn / 8, (uint32_t)n8);
             OCO_TRY(launch_check("experts f16 activations"));
             d.x = act16;
         }
