@@ -286,10 +286,9 @@ __global__ __launch_bounds__(64 * NW) void moe_q4k_kernel(KPRE_PARAMS, MatmulArg
     // Refill of stage nst / register set wn for the cursor's step, as
     // LOADS items: 0..4 the weight chunks (whole lines per instruction:
     // each row's super-block is nine consecutive chunks), 5.. the activation
-    // rows.  The
-    // items are spread over the eight MFMA chunks of a step: issued all at
-    // once, every wavefront's loads queued behind each other's at the
-    // address units.
+    // rows.  The items are spread over the eight MFMA chunks of a step:
+    // issued all at once, every wavefront's loads queued behind each other's
+    // at the address units.
     auto load_item = [&](auto kk, int nst, Q4Set *wn) __attribute__((always_inline)) {
         constexpr int K = decltype(kk)::value;
         if constexpr (K < 5) {
