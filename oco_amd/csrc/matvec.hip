@@ -580,6 +580,12 @@ static StreamPlan stream_plan(uint32_t fmt, uint32_t k, uint32_t n, uint32_t m) 
     if (plan_override(OCO_KNOB_STREAM_PLAN, ov) == 3 && ov[0] > 0) return {ov[0], ov[1], ov[2]};
     uint64_t row_bytes = oco_row_bytes(fmt, k);
     int ks = row_bytes > 6144 ? 4 : row_bytes > 3072 ? 2 : 1;
+    // Q8_0 decodes at one conversion and one FMA per weight, so one
+    // wavefront per row set holds up while its pieces fit a lane (k <= 4096;
+    // measured, 4096 x 4096: 7.28 -> 6.55 us against a K split of 2).  The
+    // K-quants lose without the split (lm_head 111 -> 148 us, Q4_K
+    // 12288 x 4096 10.9 -> 14.5 us).
+    if (fmt == OCO_Q8_0 && k / 32 <= 128) ks = 1;
     (void)m;
     // Three workgroups per CU only pay off on long streams (measured: the
     // 510 MB Q6_K lm_head 3.6 -> 4.2 TB/s; 8-41 MB matrices lose with it).
