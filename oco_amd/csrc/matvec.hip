@@ -587,9 +587,13 @@ static StreamPlan stream_plan(uint32_t fmt, uint32_t k, uint32_t n, uint32_t m) 
     // 12288 x 4096 10.9 -> 14.5 us).
     if (fmt == OCO_Q8_0 && k / 32 <= 128) ks = 1;
     (void)m;
-    // Three workgroups per CU only pay off on long streams (measured: the
-    // 510 MB Q6_K lm_head 3.6 -> 4.2 TB/s; 8-41 MB matrices lose with it).
-    const int wg = (uint64_t)n * row_bytes > (128ull << 20) ? 3 : 2;
+    // Workgroups per CU, measured: three pay off on long streams (the 510 MB
+    // Q6_K lm_head 3.6 -> 4.2 TB/s) and for MXFP4 and Q4_K at every measured
+    // size (the headline 5760 x 2880 5.30 -> 5.17 us, its 720 row groups one
+    // per workgroup; Q4_K 12288 x 4096 10.86 -> 10.66 us); mid-size Q5_K and
+    // Q6_K lose with three (12288 x 4096 13.6 -> 16.0 us, 4096 x 12288
+    // 14.3 -> 15.7 us), and Q8_0 4096 x 4096 is level.
+    const int wg = (uint64_t)n * row_bytes > (128ull << 20) || fmt == OCO_MXFP4 || fmt == OCO_Q4_K ? 3 : 2;
     return {1, ks, wg};
 }
 
