@@ -575,7 +575,7 @@ struct StreamPlan {
 // Geometry for the streaming kernel: R rows per half-wavefront, KS
 // wavefronts per K range, workgroups per CU (the analogue of
 // Builder::vector_kernel's table, pipelines.rs:227-265).
-static StreamPlan stream_plan(uint32_t fmt, uint32_t k, uint32_t n, uint32_t m) {
+static StreamPlan stream_plan(uint32_t fmt, uint32_t k, uint32_t n, uint32_t m, bool fused_norm) {
     int32_t ov[4];
     if (plan_override(OCO_KNOB_STREAM_PLAN, ov) == 3 && ov[0] > 0) return {ov[0], ov[1], ov[2]};
     uint64_t row_bytes = oco_row_bytes(fmt, k);
@@ -592,8 +592,11 @@ static StreamPlan stream_plan(uint32_t fmt, uint32_t k, uint32_t n, uint32_t m) 
     // size (the headline 5760 x 2880 5.30 -> 5.17 us, its 720 row groups one
     // per workgroup; Q4_K 12288 x 4096 10.86 -> 10.66 us); mid-size Q5_K and
     // Q6_K lose with three (12288 x 4096 13.6 -> 16.0 us, 4096 x 12288
-    // 14.3 -> 15.7 us), and Q8_0 4096 x 4096 is level.
-    const int wg = (uint64_t)n * row_bytes > (128ull << 20) || fmt == OCO_MXFP4 || fmt == OCO_Q4_K ? 3 : 2;
+    // 14.3 -> 15.7 us), and Q8_0 4096 x 4096 is level.  A fused norm, which
+    // every workgroup repeats while staging, keeps two (Qwen3-8B's norm +
+    // ffn_up + ffn_gate: 24.60 -> 24.17 us against three).
+    const bool long_stream = (uint64_t)n * row_bytes > (128ull << 20);
+    const int wg = long_stream || (!fused_norm && (fmt == OCO_MXFP4 || fmt == OCO_Q4_K)) ? 3 : 2;
     return {1, ks, wg};
 }
 
@@ -703,7 +706,7 @@ static int matvec_impl(uint32_t format, const void *w, const void *x, oco_dtype 
         oco_block_layout(format, &be, &bbytes);
         const uint32_t P = (format == OCO_Q4_K || format == OCO_Q5_K || format == OCO_Q6_K) ? 8 : 1;
         const uint32_t nblocks = p->k / be;
-        StreamPlan sp = stream_plan(format, p->k, p->n, p->m);
+        StreamPlan sp = stream_plan(format, p->k, p->n, p->m, norm != nullptr);
         if (sp.ks != 1 && sp.ks != 2 && sp.ks != 4) sp.ks = 1;
         uint32_t slice_blocks = (nblocks + sp.ks - 1) / sp.ks;
         int npl = (int)((slice_blocks * P + 31) / 32);
