@@ -134,15 +134,20 @@ int oco_buffer_copy(void *dst, const void *src, size_t bytes, oco_stream stream)
  * dispatch_tests.rs:12-13); safe inside captured graphs. */
 int oco_buffer_fill32(void *dst, uint32_t pattern, size_t words, oco_stream stream);
 
-/* XOR of `words` 32-bit words at src (16-byte aligned, words a multiple of
- * 4, under 4 GiB) into OCO_XOR32_SLOTS words of device memory at out: the
- * XOR of out[0 .. OCO_XOR32_SLOTS - 1] is the XOR of the words (each
- * workgroup stores its share; all slots are written).  No
- * counterpart in the reference: an integrity check of weights made
- * resident, and the plain HBM read stream the matvec kernels are compared
- * against (the bench's read-floor workload). */
+/* Diagnostic exports: no counterpart in the reference and not part of the
+ * matrix path.  oco_buffer_xor32 XORs `words` 32-bit words at src (16-byte
+ * aligned, words a multiple of 4, at most OCO_XOR32_MAX_BYTES bytes) into
+ * OCO_XOR32_SLOTS words of device memory at out: the XOR of
+ * out[0 .. OCO_XOR32_SLOTS - 1] is the XOR of the words (each workgroup
+ * stores its share; all slots are written).  It is an integrity check of
+ * weights made resident, and the plain HBM read stream that the matvec
+ * kernels are measured against.  oco_buffer_xor32_geometry reports the
+ * launch it would make (16 KiB rounds; workgroups), or OCO_ERR_INVALID past
+ * the size limit, without touching a device. */
 #define OCO_XOR32_SLOTS 1024u
+#define OCO_XOR32_MAX_BYTES (0xffffffffull - 32768ull)
 int oco_buffer_xor32(const void *src, size_t words, uint32_t *out, oco_stream stream);
+int oco_buffer_xor32_geometry(uint64_t words, uint64_t *rounds, uint64_t *workgroups);
 
 /* One queue per session (src/weights/compute.rs:36-55). */
 int oco_stream_create(oco_stream *out);
@@ -173,6 +178,18 @@ int oco_graph_destroy(oco_graph graph);
  * Q8_0, Q6_K, Q4_0, MXFP4, F16, BF16 are exact; Q4_K/Q5_K/Q4_1 round once.
  * MXFP4 exponent 255 decodes to NaN (projections.metal:19-23). */
 int oco_dequant(uint32_t format, const void *w, uint64_t count, float *out, oco_stream stream);
+
+/* Token embedding rows: out[r] = bf16 of row ids[r] of a GGUF tensor of
+ * `vocabulary` rows of `k` coefficients, decoded as oco_dequant does (native
+ * BF16 rows are copied as bits).  Ids >= vocabulary take row (id -
+ * vocabulary) of `features` (bf16 [feature_rows, k], may be NULL when
+ * feature_rows == 0): the spliced audio feature rows of the reference.  Ids
+ * past those rows too get a NaN row (the reference reads them unchecked).
+ * out: bf16 [rows, k].  Replaces `embed` (shaders/matrix/weights.metal:90-109,
+ * pipeline Builder::embedding, src/weights/pipelines.rs:180-193, dispatched
+ * by Compute::embed, src/weights/compute/matrix.rs:487-516). */
+int oco_embed(uint32_t format, const void *w, uint32_t k, uint32_t vocabulary, const uint32_t *ids, uint32_t rows,
+              const uint16_t *features, uint32_t feature_rows, uint16_t *out, oco_stream stream);
 
 /* ---- decode matvec ------------------------------------------------------ */
 

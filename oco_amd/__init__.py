@@ -142,6 +142,7 @@ SIGNATURES = {
     "oco_buffer_copy": (_i32, [_vp, _vp, _sz, _vp]),
     "oco_buffer_fill32": (_i32, [_vp, _u32, _sz, _vp]),
     "oco_buffer_xor32": (_i32, [_vp, _sz, _vp, _vp]),
+    "oco_buffer_xor32_geometry": (_i32, [_u64, ctypes.POINTER(_u64), ctypes.POINTER(_u64)]),
     "oco_stream_create": (_i32, [ctypes.POINTER(_vp)]),
     "oco_stream_sync": (_i32, [_vp]),
     "oco_stream_destroy": (_i32, [_vp]),
@@ -154,6 +155,7 @@ SIGNATURES = {
     "oco_graph_launch": (_i32, [_vp, _vp]),
     "oco_graph_destroy": (_i32, [_vp]),
     "oco_dequant": (_i32, [_u32, _vp, _u64, _vp, _vp]),
+    "oco_embed": (_i32, [_u32, _vp, _u32, _u32, _vp, _u32, _vp, _u32, _vp, _vp]),
     "oco_matvec": (_i32, [_u32, _vp, _vp, _i32, _vp, _i32, _vp, _vp, _MP, _vp]),
     "oco_matmul": (_i32, [_u32, _vp, _vp, _i32, _vp, _i32, _vp, _MP, _vp]),
     "oco_matmul_workspace": (_u64, [_u32, _i32, _MP]),
@@ -403,6 +405,25 @@ def synchronize(stream=None):
 
 def dequant(fmt: int, w, count: int, out, stream=None):
     _check(load_library().oco_dequant(int(fmt), _addr(w), count, _addr(out), _stream(stream)))
+
+
+def embed(fmt: int, w, k: int, vocabulary: int, ids, rows: int, out, features=None, feature_rows: int = 0,
+          stream=None):
+    """Token rows to bf16 (embed, weights.metal:90-109): ids >= vocabulary take feature rows."""
+    _check(load_library().oco_embed(int(fmt), _addr(w), k, vocabulary, _addr(ids), rows, _addr(features),
+                                    feature_rows, _addr(out), _stream(stream)))
+
+
+class Embedding:
+    """Embedding operand (src/weights/operands.rs Embedding; Builder::embedding,
+    pipelines.rs:180-193): a GGUF tensor [width, vocabulary] and its lookup."""
+
+    def __init__(self, fmt: int, values, width: int, vocabulary: int):
+        self.format, self.values, self.width, self.vocabulary = int(fmt), values, width, vocabulary
+
+    def embed(self, ids, rows: int, out, features=None, feature_rows: int = 0, stream=None):
+        """Compute::embed (compute/matrix.rs:487-516)."""
+        embed(self.format, self.values, self.width, self.vocabulary, ids, rows, out, features, feature_rows, stream)
 
 
 def matvec(fmt: int, w, x, y, p: Matrix, x_dtype=DType.F32, y_dtype=DType.F32, bias=None,

@@ -19,6 +19,7 @@
 #include "route.h"
 #include "stream.h"
 
+#include <atomic>
 #include <mutex>
 
 namespace oco {
@@ -745,7 +746,7 @@ int oco_experts_forward(const oco_experts *w, const float *router_w, const float
 // and only that address is handed to kernels.
 static __device__ __align__(256) uint8_t scratch[OCO_EXPERTS_SCRATCH_BYTES];
 constexpr int SCRATCH_DEVICES = 64;
-static void *g_scratch[SCRATCH_DEVICES];
+static std::atomic<void *> g_scratch[SCRATCH_DEVICES];
 static std::mutex g_scratch_lock;
 
 namespace oco {
@@ -753,11 +754,11 @@ int experts_scratch_init(int device) {
     if (device < 0 || device >= SCRATCH_DEVICES)
         return fail(OCO_ERR_UNSUPPORTED, "experts scratch: device %d beyond %d", device, SCRATCH_DEVICES);
     std::lock_guard<std::mutex> hold(g_scratch_lock);
-    if (g_scratch[device]) return OCO_OK;
+    if (g_scratch[device].load(std::memory_order_acquire)) return OCO_OK;
     void *p = nullptr;
     OCO_TRY(hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)"));
     if (!p) return fail(OCO_ERR_HIP, "hipGetSymbolAddress(scratch): null address");
-    g_scratch[device] = p;
+    g_scratch[device].store(p, std::memory_order_release);
     return OCO_OK;
 }
 }  // namespace oco
@@ -777,9 +778,10 @@ int oco_experts_forward_static(const oco_experts *w, const float *router_w, cons
                     tokens, (unsigned long long)need, (unsigned long long)OCO_EXPERTS_SCRATCH_BYTES);
     int dev = 0;
     OCO_TRY(hip_check(hipGetDevice(&dev), "hipGetDevice"));
-    if (dev < 0 || dev >= SCRATCH_DEVICES || !g_scratch[dev]) OCO_TRY(experts_scratch_init(dev));
-    return oco_experts_forward(w, router_w, router_bias, x, x_dtype, tokens, out, ids, probs, routed, g_scratch[dev],
-                               need, stream);
+    if (dev < 0 || dev >= SCRATCH_DEVICES || !g_scratch[dev].load(std::memory_order_acquire))
+        OCO_TRY(experts_scratch_init(dev));
+    return oco_experts_forward(w, router_w, router_bias, x, x_dtype, tokens, out, ids, probs, routed,
+                               g_scratch[dev].load(std::memory_order_acquire), need, stream);
 }
 
 int oco_expert_expand(const oco_experts *w, const void *x, oco_dtype x_dtype, const float *logits, uint32_t *ids,

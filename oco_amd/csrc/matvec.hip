@@ -20,21 +20,6 @@
 #include "stream.h"
 #include "norm.h"
 
-// Timeline probes for tuning builds only (-DOCO_TIMELINE): per workgroup,
-// wave 0 stamps s_memrealtime at entry and s_memtime at each marked point.
-#ifdef OCO_TIMELINE
-__device__ unsigned long long g_tl[8192 * 8];
-#define TL_STAMP(i)                                                                                      \
-    do {                                                                                                 \
-        if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < 8192)                                    \
-            g_tl[blockIdx.x * 8 + (i)] = (i) == 0 ? __builtin_amdgcn_s_memrealtime() : __builtin_amdgcn_s_memtime(); \
-    } while (0)
-#else
-#define TL_STAMP(i) \
-    do {            \
-    } while (0)
-#endif
-
 namespace oco {
 
 struct MatvecArgs {
@@ -210,8 +195,6 @@ __global__ __launch_bounds__(256) void stream_kernel(const uint8_t *w_, const vo
     a.p.experts = experts_;
     a.p.routes = routes_ & 0x7fffffffu;
     a.p.route_major = routes_ >> 31;
-    TL_STAMP(0);
-    TL_STAMP(1);
     using T = Tile<FMT>;
     constexpr int LPR = StreamShape<FMT, NPL>::LPR;
     constexpr int ROWS = 2;                     // tile rows per wavefront (one per half-wavefront)
@@ -360,7 +343,6 @@ __global__ __launch_bounds__(256) void stream_kernel(const uint8_t *w_, const vo
         if (g0 < a.ngroups) issue(g0, ra);
         if (g0 + G < a.ngroups) issue(g0 + G, rb);
     }
-    TL_STAMP(2);
 
     // Staged: x (f32) to LDS in piece-major order, then the per-piece sums.  With a
     // fused norm, x is the bf16 row before normalisation: every workgroup
@@ -444,7 +426,6 @@ __global__ __launch_bounds__(256) void stream_kernel(const uint8_t *w_, const vo
             for (int j = 0; j < T::NSUM; j++) sv[s][j] = xsum[j * PT + pg];
         }
     }
-    TL_STAMP(3);
 
     uint8_t *tile = tiles + (size_t)wave * TILE;
     // One row group: its registers to this wavefront's LDS tile, the loads of
@@ -461,7 +442,6 @@ __global__ __launch_bounds__(256) void stream_kernel(const uint8_t *w_, const vo
         } else {
 #pragma unroll
             for (int i = 0; i < ROWS * LPR; i++) reinterpret_cast<u32x4 *>(tile)[i * 64 + lane] = regs[i];
-            if (g == blockIdx.x) TL_STAMP(4);
             const uint32_t rbase = half * LPR * 1024 + (row_offset(g, half) & 15u);
             if (g + 2 * G < a.ngroups) issue(g + 2 * G, regs);
 #pragma unroll
@@ -475,7 +455,6 @@ __global__ __launch_bounds__(256) void stream_kernel(const uint8_t *w_, const vo
             }
         }
         acc = half_sum(acc);
-        if (g == blockIdx.x) TL_STAMP(5);
 
         const uint32_t row = g * rows_per_group + set * ROWS + half;
         if (ks > 1) {
@@ -510,7 +489,6 @@ __global__ __launch_bounds__(256) void stream_kernel(const uint8_t *w_, const vo
             if (g + G < a.ngroups) group(g + G, rb, db);
         }
     }
-    TL_STAMP(6);
 }
 
 typedef void (*StreamFn)(const uint8_t *, const void *, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t,
@@ -813,11 +791,6 @@ static int matvec_impl(uint32_t format, const void *w, const void *x, oco_dtype 
     return launch_check("oco_matvec");
 }
 
-#ifdef OCO_TIMELINE
-extern "C" int oco_timeline_read(void *host, size_t bytes) {
-    return hip_check(hipMemcpyFromSymbol(host, HIP_SYMBOL(g_tl), bytes), "timeline");
-}
-#endif
 
 extern "C" int oco_matvec(uint32_t format, const void *w, const void *x, oco_dtype x_dtype, void *y,
                           oco_dtype y_dtype, const float *bias, const uint32_t *ids,

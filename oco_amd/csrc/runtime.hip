@@ -42,11 +42,15 @@ int plan_override(uint32_t knob, int32_t *vals) {
 // its XOR to out[b] (an atomic per workgroup into one word costs
 // microseconds of contention), workgroup 0 zeroes the slots no workgroup
 // owns.  XOR is order-independent: exact.
-__global__ __launch_bounds__(256) void xor32_kernel(const uint8_t *src, uint32_t bytes, uint32_t *out) {
+// The round count is precomputed on the host, so the loop ends after
+// `rounds` rounds whatever the size; offsets stay below 2^32 because the
+// host caps bytes at XOR32_MAX_BYTES.
+__global__ __launch_bounds__(256) void xor32_kernel(const uint8_t *src, uint32_t bytes, uint32_t rounds, uint32_t *out) {
     const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(src), 0, bytes, 0x00020000);
     constexpr int U = 4;
     uint32_t acc = 0;
-    for (uint32_t base = blockIdx.x * 256u * U * 16u; base < bytes; base += gridDim.x * 256u * U * 16u) {
+    for (uint32_t round = blockIdx.x; round < rounds; round += gridDim.x) {
+        const uint32_t base = round * 256u * U * 16u;
         u32x4 v[U];
 #pragma unroll
         for (int u = 0; u < U; u++) v[u] = __builtin_amdgcn_raw_buffer_load_b128(r, base + (u * 256 + threadIdx.x) * 16, 0, 2);
@@ -60,6 +64,18 @@ __global__ __launch_bounds__(256) void xor32_kernel(const uint8_t *src, uint32_t
     if (threadIdx.x == 0) out[blockIdx.x] = part[0] ^ part[1] ^ part[2] ^ part[3];
     if (blockIdx.x == 0)
         for (uint32_t i = gridDim.x + threadIdx.x; i < OCO_XOR32_SLOTS; i += 256) out[i] = 0;
+}
+
+// Size limit and launch geometry of xor32_kernel: 16 KiB per workgroup
+// round, one workgroup per round up to OCO_XOR32_SLOTS.  The last round
+// starts below XOR32_MAX_BYTES and reads at most 16 KiB past its start, so
+// every buffer offset fits 32 bits.
+constexpr uint64_t XOR32_MAX_BYTES = OCO_XOR32_MAX_BYTES;
+bool xor32_geometry(uint64_t words, uint64_t *rounds, uint64_t *grid) {
+    if (words > XOR32_MAX_BYTES / 4) return false;
+    *rounds = (words * 4 + 16383u) / 16384u;
+    *grid = *rounds < OCO_XOR32_SLOTS ? *rounds : OCO_XOR32_SLOTS;
+    return true;
 }
 
 __global__ void fill32_kernel(uint32_t *dst, uint32_t pattern, size_t words) {
@@ -117,7 +133,10 @@ int oco_device_open(int ordinal, int *compute_units) {
     if (ordinal < 0 || ordinal >= count)
         return fail(OCO_ERR_INVALID, "device %d out of range (%d devices)", ordinal, count);
     OCO_TRY(hip_check(hipSetDevice(ordinal), "hipSetDevice"));
-    OCO_TRY(experts_scratch_init(ordinal));
+    // The static experts scratch is resolved here when the ordinal has a
+    // slot; devices beyond the table still open (the static entry point
+    // then reports them), and a failure here is retried on its first call.
+    if (ordinal < 64) (void)experts_scratch_init(ordinal);
     if (compute_units) {
         int cu = 0;
         OCO_TRY(hip_check(hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, ordinal),
@@ -162,12 +181,20 @@ int oco_buffer_xor32(const void *src, size_t words, uint32_t *out, oco_stream st
     if (!words) return OCO_OK;
     if (!src || !out) return fail(OCO_ERR_INVALID, "oco_buffer_xor32: null pointer");
     if (((uintptr_t)src & 15u) || words % 4) return fail(OCO_ERR_INVALID, "oco_buffer_xor32: needs 16-byte aligned whole chunks");
-    if (words > 0x3fffffffull) return fail(OCO_ERR_INVALID, "oco_buffer_xor32: over 4 GiB");
-    const uint32_t bytes = (uint32_t)(words * 4);
-    const uint32_t rounds = (bytes + 16383u) / 16384u;  // 16 KiB per workgroup round
-    const uint32_t grid = rounds < OCO_XOR32_SLOTS ? rounds : OCO_XOR32_SLOTS;
-    hipLaunchKernelGGL(xor32_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, (const uint8_t *)src, bytes, out);
+    uint64_t rounds64 = 0, grid64 = 0;
+    if (!xor32_geometry(words, &rounds64, &grid64))
+        return fail(OCO_ERR_INVALID, "oco_buffer_xor32: %zu words is over the %llu-byte limit", words,
+                    (unsigned long long)XOR32_MAX_BYTES);
+    hipLaunchKernelGGL(xor32_kernel, dim3((uint32_t)grid64), dim3(256), 0, (hipStream_t)stream, (const uint8_t *)src,
+                       (uint32_t)(words * 4), (uint32_t)rounds64, out);
     return launch_check("xor32");
+}
+
+int oco_buffer_xor32_geometry(uint64_t words, uint64_t *rounds, uint64_t *workgroups) {
+    if (!rounds || !workgroups) return fail(OCO_ERR_INVALID, "oco_buffer_xor32_geometry: null pointer");
+    if (!xor32_geometry(words, rounds, workgroups))
+        return fail(OCO_ERR_INVALID, "oco_buffer_xor32_geometry: over the size limit");
+    return OCO_OK;
 }
 
 int oco_stream_create(oco_stream *out) {

@@ -207,6 +207,35 @@ int oo_dequant(uint32_t fmt, const uint8_t *w, uint64_t count, float *out) {
     return 0;
 }
 
+/* Token rows (embed, weights.metal:90-109): row r is bf16 of the decoded
+ * row ids[r] of a [vocab][k] tensor; native BF16 copies the stored bits;
+ * ids >= vocab splice feature row (id - vocab), and ids past the
+ * feature_rows give a row of quiet NaN (0x7fc0), this build's rule for the
+ * case the reference leaves unchecked. */
+int oo_embed(uint32_t fmt, const uint8_t *w, uint32_t k, uint32_t vocab, const uint32_t *ids, uint32_t rows,
+             const uint16_t *features, uint32_t feature_rows, uint16_t *out) {
+    uint32_t be, bb;
+    if (oo_block_layout(fmt, &be, &bb) || k % be) return -1;
+    const uint64_t row_bytes = (uint64_t)(k / be) * bb;
+    for (uint32_t r = 0; r < rows; r++) {
+        const uint32_t id = ids[r];
+        uint16_t *o = out + (uint64_t)r * k;
+        for (uint32_t c = 0; c < k; c++) {
+            if (id >= vocab) {
+                o[c] = features && id - vocab < feature_rows ? features[(uint64_t)(id - vocab) * k + c] : 0x7fc0;
+                continue;
+            }
+            const uint8_t *blk = w + (uint64_t)id * row_bytes + (uint64_t)(c / be) * bb;
+            if (fmt == 30) {
+                o[c] = (uint16_t)(blk[0] | (blk[1] << 8));
+            } else {
+                o[c] = oo_f32_to_bf16(decode(fmt, blk, c % be));
+            }
+        }
+    }
+    return 0;
+}
+
 static double load_x(const void *x, int dt, uint64_t i) {
     if (dt == OO_DT_F32) return ((const float *)x)[i];
     if (dt == OO_DT_BF16) return oo_bf16(((const uint16_t *)x)[i]);

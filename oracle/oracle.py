@@ -49,6 +49,7 @@ def lib():
         L.oo_f32_to_f16.argtypes = [ctypes.c_float]
         L.oo_f32_to_f16.restype = ctypes.c_uint16
         L.oo_dequant.argtypes = [u32, vp, u64, vp]
+        L.oo_embed.argtypes = [u32, vp, u32, u32, vp, u32, vp, u32, vp]
         L.oo_matvec_f64.argtypes = [u32, vp, vp, i32, vp, vp, ctypes.POINTER(Matrix), vp, vp]
         L.oo_matvec_f32.argtypes = [u32, vp, vp, i32, vp, vp, ctypes.POINTER(Matrix), vp, i32, i32]
         L.oo_select_experts.argtypes = [vp, u32, u32, vp, vp]
@@ -84,6 +85,20 @@ def dequant(fmt: int, w: np.ndarray, count: int) -> np.ndarray:
     rc = lib().oo_dequant(fmt, _p(w), count, _p(out))
     if rc:
         raise ValueError(f"oo_dequant failed: {rc}")
+    return out
+
+
+def embed(fmt: int, w: np.ndarray, k: int, vocab: int, ids, features=None) -> np.ndarray:
+    """bf16 token rows (weights.metal:90-109) of a [vocab][k] GGUF tensor."""
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    ids = np.ascontiguousarray(ids, np.uint32)
+    out = np.empty((ids.size, k), np.uint16)
+    feats = None if features is None else np.ascontiguousarray(features, np.uint16)
+    nf = 0 if feats is None else feats.size // k
+    rc = lib().oo_embed(fmt, _p(w), k, vocab, _p(ids), ids.size, _p(feats) if feats is not None else None, nf,
+                        _p(out))
+    if rc:
+        raise ValueError(f"oo_embed failed: {rc}")
     return out
 
 
@@ -209,16 +224,38 @@ def bf16_round(x) -> np.ndarray:
     return bf16_to_f32(f32_to_bf16(np.asarray(x, np.float32))).astype(np.float64)
 
 
+def _nonfinite_to_nan(g, u, act):
+    """The activations' rule for invalid operands: any non-finite gate or up
+    value gives NaN (projections.metal:5-8, routing.metal:53-58,
+    elementwise.metal:76-80), checked before any clipping."""
+    bad = ~(np.isfinite(g) & np.isfinite(u))
+    return np.where(bad, np.nan, act)
+
+
 def swiglu_clipped_f64(g, u):
-    """projections.metal:4-13 in fp64: sigmoid(1.702 g') g' u', g' = min(g, 7), u' = clamp(u, -6, 8)."""
-    g = np.minimum(g, 7.0)
-    u = np.clip(u, -6.0, 8.0)
-    return g / (1.0 + np.exp(-1.702 * g)) * u
+    """projections.metal:4-13 in fp64: sigmoid(1.702 g') g' u', g' = min(g, 7),
+    u' = clamp(u, -6, 8); NaN for a non-finite g or u."""
+    g = np.asarray(g, np.float64)
+    u = np.asarray(u, np.float64)
+    with np.errstate(over="ignore", invalid="ignore"):
+        gc = np.minimum(np.where(np.isfinite(g), g, 0.0), 7.0)
+        uc = np.clip(np.where(np.isfinite(u), u, 0.0), -6.0, 8.0)
+        act = gc / (1.0 + np.exp(-1.702 * gc)) * uc
+    return _nonfinite_to_nan(g, u, act)
 
 
 def swiglu_f64(g, u):
-    """silu(g) * u (elementwise.metal:70-88 without its bf16 storage)."""
-    return g / (1.0 + np.exp(-g)) * u
+    """silu(g) * u (elementwise.metal:70-88 without its bf16 storage); NaN
+    for a non-finite g or u."""
+    g = np.asarray(g, np.float64)
+    u = np.asarray(u, np.float64)
+    with np.errstate(over="ignore", invalid="ignore"):
+        gf = np.where(np.isfinite(g), g, 0.0)
+        # sigmoid from exp(-|g|), as the kernels take it, so large |g| does not overflow
+        e = np.exp(-np.abs(gf))
+        sig = np.where(gf < 0, e, 1.0) / (1.0 + e)
+        act = sig * gf * np.where(np.isfinite(u), u, 0.0)
+    return _nonfinite_to_nan(g, u, act)
 
 
 def experts_reference(fmt, hidden, ffn, gate, up, down, x, ids, probs, residual_bf16,

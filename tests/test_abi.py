@@ -80,3 +80,20 @@ def test_argument_validation_without_gpu():
     assert lib.oco_experts_workspace(ctypes.byref(mx), 62) <= 8 << 20 < lib.oco_experts_workspace(ctypes.byref(mx), 63)
     rc = lib.oco_experts_forward_static(ctypes.byref(mx), fake, None, fake, 0, 63, fake, fake, fake, None, None)
     assert rc == 1 and b"scratch" in lib.oco_last_error()
+
+
+def test_xor32_geometry_at_the_size_limit():
+    """The read stream's rounds and grid stay finite and in 32-bit offsets up
+    to its limit, and sizes past it are refused before any launch."""
+    lib = oco_amd.load_library()
+    rounds, grid = ctypes.c_uint64(), ctypes.c_uint64()
+    limit = 0xffffffff - 32768
+    for words, want_rounds in [(4, 1), (4096, 1), (4100, 2), (2203200, 538), (limit // 4, (limit // 4 * 4 + 16383) // 16384)]:
+        assert lib.oco_buffer_xor32_geometry(words, ctypes.byref(rounds), ctypes.byref(grid)) == 0
+        assert rounds.value == want_rounds
+        assert grid.value == min(rounds.value, 1024)
+        # the last round's reads end inside 32-bit offsets
+        assert (rounds.value - 1) * 16384 + 16384 <= 1 << 32
+    for words in [limit // 4 + 1, (1 << 30), (1 << 32)]:
+        assert lib.oco_buffer_xor32_geometry(words, ctypes.byref(rounds), ctypes.byref(grid)) == 1
+        assert b"limit" in lib.oco_last_error()

@@ -330,6 +330,74 @@ def test_experts_full_shape(lib, tokens):
     diff = np.abs(O.bf16_to_f32(outb.download(np.uint16).reshape(tokens, hidden)).astype(np.float64) - want)
     assert np.all(diff <= out_bound(want, ref["down"], k))
 
+    # The timed path: oco_experts_forward from the router weights (at 4 and 16
+    # tokens the selection and route plan run inside every gate/up
+    # workgroup; at one token inside the routed kernel) equals oco_router
+    # followed by oco_experts_apply bit for bit at this shape.
+    rw = (rng.normal(size=(E, hidden)) / np.sqrt(hidden)).astype(np.float32)
+    rb = (rng.normal(size=E) * 0.1).astype(np.float32)
+    xb, rwb, rbb = dev(lib, x), dev(lib, rw), dev(lib, rb)
+    out1, ids1, probs1 = dev(lib, resid), lib.DeviceBuffer(tokens * k * 4), lib.DeviceBuffer(tokens * k * 4)
+    routed1 = Guarded(lib, tokens * k * hidden * 4)
+    bk.forward(rwb, rbb, xb, lib.DType.F32, tokens, out1, ids1, probs1, routed=routed1.ptr)
+    logits = lib.DeviceBuffer(tokens * E * 4)
+    out2, ids2, probs2 = dev(lib, resid), lib.DeviceBuffer(tokens * k * 4), lib.DeviceBuffer(tokens * k * 4)
+    routed2 = Guarded(lib, tokens * k * hidden * 4)
+    lib.router(xb, lib.DType.F32, rwb, rbb, tokens, hidden, E, k, logits, ids2, probs2)
+    bk.apply(xb, lib.DType.F32, ids2, probs2, tokens, out2, routed=routed2.ptr)
+    lib.synchronize()
+    np.testing.assert_array_equal(ids1.download(np.uint32), ids2.download(np.uint32))
+    np.testing.assert_array_equal(probs1.download(np.uint32), probs2.download(np.uint32))
+    np.testing.assert_array_equal(routed1.read(np.uint32), routed2.read(np.uint32))
+    np.testing.assert_array_equal(out1.download(np.uint16), out2.download(np.uint16))
+    want_ids, _ = O.select_experts(logits.download(np.float32).reshape(tokens, E), k)
+    np.testing.assert_array_equal(ids1.download(np.uint32).reshape(tokens, k), want_ids)
+
+
+@pytest.mark.parametrize("tokens", [1, 4, 40])
+def test_experts_nonfinite_gate_and_up(lib, tokens):
+    """One gate row and one up row of expert 0 carry a block whose E8M0
+    scale is 2^127 with a code of 6 (6 * 2^127 overflows f32): those gate and
+    up values are non-finite, the activation rule turns them into NaN
+    (projections.metal:5-8), and every route through expert 0 comes out NaN
+    in every column, as in the oracle; routes through other experts stay
+    finite and within their bar.  Batch 1 runs the routed kernel, 4 the
+    block-scaled MFMA tiles, 40 the prefill tiles."""
+    E, hidden, ffn, k = 8, 256, 128, 2
+    say("experts nonfinite gate/up", tokens)
+    host, _ = bank(lib, 39, E, hidden, ffn, seed=210 + tokens)
+    g, u, d, gb, ub, db = [a.copy() for a in host]
+    rb = hidden // 32 * 17
+    for arr, row in ((g, 5), (u, 77)):  # expert 0: gate row 5, up row 77, second block
+        blk = row * rb + 17
+        arr[blk] = 254
+        arr[blk + 1:blk + 17] = 0
+        arr[blk + 1] = 0x7  # code 7 = 6.0 in column 0 of the block
+    rng = np.random.default_rng(211)
+    x = np.abs(rng.normal(size=(tokens, hidden))).astype(np.float32) + 0.5
+    logits = rng.normal(size=(tokens, E)).astype(np.float32)
+    logits[:, 0] += 10.0  # every token routes through expert 0 ...
+    logits[0, 0] -= 20.0  # ... except token 0
+    ids, probs = O.select_experts(logits, k)
+    resid = O.f32_to_bf16(rng.normal(size=(tokens, hidden)).astype(np.float32))
+    bk = lib.ExpertBank(39, hidden, ffn, E, k, *[dev(lib, a) for a in (g, u, d, gb, ub, db)])
+    outb = dev(lib, resid)
+    routed = Guarded(lib, tokens * k * hidden * 4)
+    bk.apply(dev(lib, x), lib.DType.F32, dev(lib, ids), dev(lib, probs), tokens, outb, routed=routed.ptr)
+    lib.synchronize()
+    ref = O.experts_reference(39, hidden, ffn, g, u, d, x, ids, probs, resid, gb, ub, db)
+    assert np.isnan(ref["act"][ids.reshape(-1) == 0][:, [5, 77]]).all()
+    got = routed.read(np.float32).reshape(-1, hidden)
+    bad = np.isnan(ref["down"]).any(axis=1)
+    assert bad.sum() == tokens - 1 and not bad[:k].any()
+    np.testing.assert_array_equal(bad, ids.reshape(-1) == 0)
+    assert np.isnan(got[bad]).all()
+    assert np.isfinite(got[~bad]).all()
+    bar = 1e-5 if tokens == 1 else MX3_BAR if tokens < 32 else 2e-3
+    assert rel_l2(got[~bad], ref["down"][~bad]) < bar
+    out = O.bf16_to_f32(outb.download(np.uint16).reshape(tokens, hidden))
+    np.testing.assert_array_equal(np.isnan(out), np.isnan(O.bf16_to_f32(ref["out"])))
+
 
 @pytest.mark.parametrize("ks", [1, 2])
 @pytest.mark.parametrize("ffn", [512, 640])
@@ -413,6 +481,51 @@ def test_experts_prefill_qwen3_shape(lib):
     say("experts prefill qwen3 shape")
     got, _, ref = _prefill_case(lib, 12, E, hidden, ffn, k, tokens, "bf16", 91, False)
     assert rel_l2(got, ref["down"]) < 2e-3
+
+
+def test_experts_prefill_qwen3_30b_a3b_geometry(lib):
+    """BASELINE cfg 5b at its own geometry: 128 experts of hidden 2048 / ffn
+    768, Q4_K, SwiGLU without biases, top-8 of N(0,1) logits over 512 tokens
+    (4,096 routes, 32 per expert on average).  The plan then takes 48-row
+    tiles over all 128 experts; experts past 48 routes spill into overflow
+    tiles (more than 128 tiles in all), which hand some persistent
+    workgroups an extra unit.  This is the layer the bench times."""
+    E, hidden, ffn, k, tokens = 128, 2048, 768, 8, 512
+    say("experts prefill qwen3-30b-a3b geometry")
+    host, devs = bank(lib, 12, E, hidden, ffn, seed=95)
+    g, u, d = host[:3]
+    rng = np.random.default_rng(95)
+    x = rng.normal(size=(tokens, hidden)).astype(np.float32)
+    ids, probs = O.select_experts(rng.normal(size=(tokens, E)).astype(np.float32), k)
+    counts = np.bincount(ids.reshape(-1), minlength=E)
+    tiles = int(np.sum((counts + 47) // 48))
+    say("routes per expert", counts.min(), counts.max(), "tiles of 48:", tiles)
+    assert (counts > 0).all() and counts.max() > 48 and tiles > E
+    resid = O.f32_to_bf16(rng.normal(size=(tokens, hidden)).astype(np.float32))
+    bk = lib.ExpertBank(12, hidden, ffn, E, k, devs[0], devs[1], devs[2], activation=1, up_bias_one=False)
+    xin = O.f32_to_bf16(x)
+    outb = dev(lib, resid)
+    routed = Guarded(lib, tokens * k * hidden * 4)
+    bk.apply(dev(lib, xin), lib.DType.BF16, dev(lib, ids), dev(lib, probs), tokens, outb, routed=routed.ptr)
+    lib.synchronize()
+    ref = O.experts_reference(12, hidden, ffn, g, u, d, O.bf16_to_f32(xin), ids, probs, resid,
+                              activation=1, up_one=False)
+    got = routed.read(np.float32).reshape(tokens * k, hidden)
+    err = rel_l2(got, ref["down"])
+    say("relL2", err)
+    assert err < 2e-3
+    want = O.bf16_to_f32(ref["out"])
+    diff = np.abs(O.bf16_to_f32(outb.download(np.uint16).reshape(tokens, hidden)).astype(np.float64) - want)
+    mag = np.abs(ref["down"]).reshape(tokens, k, hidden).sum(axis=1)
+    assert np.all(diff <= 2 ** -6 * np.abs(want) + (2 * k * 2 ** -9 + 2e-3) * mag + 2e-2)
+    # forced 64-row tiles (every expert in one tile) give the same routes
+    # within the bar: the tile choice only regroups rows
+    with lib.overridden(lib.Knob.MOE_Q4_ROWS, [64]):
+        routed64 = Guarded(lib, tokens * k * hidden * 4)
+        bk.apply(dev(lib, xin), lib.DType.BF16, dev(lib, ids), dev(lib, probs), tokens, dev(lib, resid),
+                 routed=routed64.ptr)
+        lib.synchronize()
+    assert rel_l2(routed64.read(np.float32).reshape(tokens * k, hidden), ref["down"]) < 2e-3
 
 
 def test_experts_prefill_q4k_ranges_over_tiles(lib):

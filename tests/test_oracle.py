@@ -36,6 +36,46 @@ def test_dequant_reproduces_reference_packer(fmt):
     np.testing.assert_array_equal(got, want.astype(np.float32))
 
 
+@pytest.mark.parametrize("fmt", FORMATS + [O.MXFP4])
+def test_embed_rows_from_reference_packer(fmt):
+    """embed (weights.metal:90-109): row ids[r] of the packed tensor equals
+    the packer's recorded coefficients rounded to bf16 (numpy rounding of the
+    exact values), ids >= vocabulary splice the feature rows, and ids past
+    them give NaN rows; native BF16 rows keep their stored bits, so a NaN
+    payload that a float round trip would quieten (0x7f81 -> 0x7fc1)
+    survives."""
+    k, n = 512, 33
+    if fmt == O.MXFP4:
+        data, values = P.mxfp4_expert_weights(k, n, salt=3, experts=1)
+        w = np.frombuffer(data, np.uint8)[P.WEIGHT_OFFSET:]
+        coeffs = np.asarray(values, np.float64).reshape(n, k)
+    else:
+        data, cs = P.dense_weights(fmt, n, k)
+        w = np.frombuffer(data, np.uint8).copy()
+        coeffs = np.array([c for c, _ in cs], np.float64).reshape(n, k)
+        if fmt == P.BF16:
+            w.view(np.uint16)[3 * k + 5] = 0x7f81
+            coeffs[3, 5] = np.nan
+    feats = O.f32_to_bf16(np.random.default_rng(1).normal(size=(2, k)).astype(np.float32))
+    ids = np.array([0, 3, n - 1, n, n + 1, n + 2, 7, 3], np.uint32)
+    got = O.embed(fmt, w, k, n, ids, feats)
+    for r, i in enumerate(ids):
+        if i < n:
+            want = coeffs[i].astype(np.float32)
+            rounded = ((want.view(np.uint32).astype(np.uint64) + 0x7FFF + ((want.view(np.uint32) >> 16) & 1)) >> 16)
+            finite = np.isfinite(want)
+            # as values: the MXFP4 packer records code 8 (-0) as +0
+            np.testing.assert_array_equal(O.bf16_to_f32(got[r])[finite],
+                                          O.bf16_to_f32(rounded.astype(np.uint16))[finite])
+        elif i - n < 2:
+            np.testing.assert_array_equal(got[r], feats[i - n])
+        else:
+            assert (got[r] == 0x7fc0).all()
+    if fmt == P.BF16:
+        assert got[1][5] == 0x7f81
+    assert (O.embed(fmt, w, k, n, ids[:3]) == got[:3]).all()
+
+
 def test_mxfp4_decode_reproduces_reference_packer():
     """mxfp4.rs:46-81 at the reference's K=2880, with the unaligned start."""
     k, n = 2880, 5
@@ -269,6 +309,37 @@ def test_swiglu_clipped_closed_form():
         assert abs(O.swiglu_clipped(g, u) - want) <= 1e-6 * max(1.0, abs(want))
     assert math.isnan(O.swiglu_clipped(float("inf"), 1.0))
     assert math.isnan(O.swiglu_clipped(1.0, float("nan")))
+
+
+def test_layer_activations_follow_the_nonfinite_rule():
+    """The fp64 layer activations agree with the C oracle's f32 clipped
+    SwiGLU on finite inputs (including ones far past the clipping points and
+    where exp overflows), and give NaN for every non-finite gate or up, as
+    projections.metal:5-8 and elementwise.metal:76-80 do -- without numpy
+    overflow warnings."""
+    import warnings
+    rng = np.random.default_rng(4)
+    g = np.concatenate([rng.normal(0, 3, 200), [1e30, -1e30, 500.0, -500.0, 7.0, -6.0, 0.0]])
+    u = np.concatenate([rng.normal(0, 5, 200), [1.0, 2.0, -1e30, 1e30, 8.5, -6.5, 3.0]])
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        got = O.swiglu_clipped_f64(g, u)
+        silu = O.swiglu_f64(g, u)
+    want = np.array([O.swiglu_clipped(float(a), float(b)) for a, b in zip(g, u)], np.float64)
+    assert np.all(np.abs(got - want) <= 1e-6 * np.maximum(1.0, np.abs(want)))
+    # silu(g) u: closed form where exp does not overflow, 0 * u and g * u at the tails
+    mid = np.abs(g) < 50
+    gm, um = g[mid], u[mid]
+    np.testing.assert_allclose(silu[mid], gm / (1 + np.exp(-gm)) * um, rtol=1e-12, atol=1e-300)
+    assert silu[-6] == 0.0 * u[-6] and silu[-7] == g[-7] * u[-7]
+    inf, nan = np.inf, np.nan
+    gs = np.array([inf, -inf, nan, 1.0, 1.0, 1.0, inf])
+    us = np.array([1.0, 1.0, 1.0, inf, -inf, nan, inf])
+    for fn in (O.swiglu_clipped_f64, O.swiglu_f64):
+        with warnings.catch_warnings():
+            warnings.simplefilter("error")
+            assert np.all(np.isnan(fn(gs, us)))
+    assert all(math.isnan(O.swiglu_clipped(float(a), float(b))) for a, b in zip(gs, us))
 
 
 @pytest.mark.parametrize("batch,experts,tile", [(17, 32, 64), (257, 32, 64), (512, 128, 16), (1, 32, 64)])
