@@ -115,7 +115,8 @@ class ReadFloor(Workload):
 
 
 class MatvecStack(Workload):
-    """Qwen3-8B-shaped decode stack: ffn_up/gate Q4_K, ffn_down Q6_K, lm_head Q6_K."""
+    """Qwen3-8B-shaped decode stack: ffn_up/gate Q4_K (one grouped launch, the
+    reference's concurrent pair), ffn_down Q6_K, lm_head Q6_K."""
     name = "qwen3_8b_q4km_decode_stack"
 
     def setup(self, oco, stream):
@@ -129,11 +130,15 @@ class MatvecStack(Workload):
         self.bytes = sum(m[4] for m in self.mats)
         self.x = oco.DeviceBuffer.from_array(synth.activations(35, 12288))
         self.h = oco.DeviceBuffer(151936 * 4)
+        self.h2 = oco.DeviceBuffer(12288 * 4)
 
     def launch(self, i):
-        for fmt, n, k, w, nb in self.mats:
-            self.oco.matvec(fmt, w, self.x, self.h, self.oco.Matrix(k, n, 1, 0, 1, 1, 0),
-                            stream=self.stream)
+        o = self.oco
+        (fu, nu, ku, wu, _), (_, _, _, wg, _) = self.mats[:2]
+        o.matvec_group(fu, [wu, wg], self.x, [self.h, self.h2], o.Matrix(ku, nu, 1, 0, 1, 1, 0), o.DType.F32,
+                       stream=self.stream)
+        for fmt, n, k, w, nb in self.mats[2:]:
+            o.matvec(fmt, w, self.x, self.h, o.Matrix(k, n, 1, 0, 1, 1, 0), stream=self.stream)
 
     def work_per_step(self):
         return float(self.bytes)
@@ -191,21 +196,33 @@ class Argmax(Workload):
 
 class NormUpGate(Workload):
     """Qwen3-8B FFN entry: RMS norm of the bf16 residual row, then ffn_up and
-    ffn_gate [12288 x 4096] Q4_K.  fused: the norm inside both matvecs'
-    activation staging (oco_matvec_norm); else oco_norm then two matvecs.
-    Work = the two weight matrices' bytes."""
+    ffn_gate [12288 x 4096] Q4_K.  mode "group": the norm and both matrices
+    in one grid (oco_matvec_group, the reference's concurrent up/gate pair);
+    "fused": the norm inside each matvec's activation staging
+    (oco_matvec_norm), two launches; "unfused": oco_norm then two matvecs.
+    The pair is replicated into enough copies (> 512 MiB) that successive
+    steps rotate through them past the Infinity Cache.  Work = the two
+    weight matrices' bytes."""
 
-    def __init__(self, fused):
-        self.fused = fused
-        self.name = "norm_up_gate_qwen3_8b" + ("_fused" if fused else "_unfused")
+    def __init__(self, mode):
+        self.mode = mode
+        self.name = "norm_up_gate_qwen3_8b_" + mode
 
     def setup(self, oco, stream):
         import numpy as np
         from oco_amd import synth
         self.oco, self.stream = oco, stream
         self.n, self.k = 12288, 4096
-        self.mats = [oco.DeviceBuffer.from_array(synth.weights(12, self.n, self.k, s)) for s in (31, 32)]
-        self.bytes = 2 * self.n * (self.k // 256) * 144
+        mats = [synth.weights(12, self.n, self.k, s) for s in (31, 32)]
+        self.mbytes = mats[0].nbytes
+        self.bytes = 2 * self.mbytes
+        self.copies = max(1, math.ceil(ROTATE_BYTES / self.bytes))
+        self.w = oco.DeviceBuffer(self.bytes * self.copies)
+        self.w.upload(mats[0], 0)
+        self.w.upload(mats[1], self.mbytes)
+        for c in range(1, self.copies):
+            oco.load_library().oco_buffer_copy(self.w.ptr + c * self.bytes, self.w.ptr, self.bytes, stream.handle)
+        stream.sync()
         self.x = oco.DeviceBuffer.from_array(synth.bf16_bits(synth.activations(37, self.k)))
         self.nw = oco.DeviceBuffer.from_array((1 + 0.1 * np.random.default_rng(2).normal(size=self.k)).astype(np.float32))
         self.normed = oco.DeviceBuffer(self.k * 2)
@@ -214,12 +231,17 @@ class NormUpGate(Workload):
 
     def launch(self, i):
         o = self.oco
-        if self.fused:
-            for w, y in zip(self.mats, self.y):
+        base = self.w.ptr + (i % self.copies) * self.bytes
+        mats = [base, base + self.mbytes]
+        if self.mode == "group":
+            o.matvec_group(12, mats, self.x, self.y, self.p, o.DType.BF16, o.DType.F32, self.nw, 1e-6, True,
+                           stream=self.stream)
+        elif self.mode == "fused":
+            for w, y in zip(mats, self.y):
                 o.matvec_norm(12, w, self.x, self.nw, 1e-6, y, self.p, True, stream=self.stream)
         else:
             o.norm(self.x, self.nw, self.normed, 1, self.k, 1e-6, True, stream=self.stream)
-            for w, y in zip(self.mats, self.y):
+            for w, y in zip(mats, self.y):
                 o.matvec(12, w, self.normed, y, self.p, o.DType.BF16, stream=self.stream)
 
     def work_per_step(self):
@@ -403,8 +425,9 @@ WORKLOADS = {
     "moe_prefill_qwen3_30b_a3b": MoePrefill,
     "lm_head_argmax_qwen3_8b": LmHeadArgmax,
     "argmax_f32_151936": Argmax,
-    "norm_up_gate_qwen3_8b_fused": lambda: NormUpGate(True),
-    "norm_up_gate_qwen3_8b_unfused": lambda: NormUpGate(False),
+    "norm_up_gate_qwen3_8b_group": lambda: NormUpGate("group"),
+    "norm_up_gate_qwen3_8b_fused": lambda: NormUpGate("fused"),
+    "norm_up_gate_qwen3_8b_unfused": lambda: NormUpGate("unfused"),
 }
 PEAK_TFLOPS = {"bf16": 2500.0, "fp4": 10100.0}
 HEADLINE = "mxfp4_decode_matvec_5760x2880"
@@ -555,7 +578,8 @@ def main():
                      "q6_k_lm_head_151936x4096", "qwen3_8b_q4km_decode_stack", "moe_decode_gpt_oss_b1",
                      "moe_decode_gpt_oss_b4", "moe_decode_gpt_oss_b16", "prefill_mxfp4_5760x2880_m512",
                      "moe_prefill_qwen3_30b_a3b", "lm_head_argmax_qwen3_8b", "argmax_f32_151936",
-                     "norm_up_gate_qwen3_8b_fused", "norm_up_gate_qwen3_8b_unfused", "read_floor_8812800"]:
+                     "norm_up_gate_qwen3_8b_group", "norm_up_gate_qwen3_8b_fused",
+                     "norm_up_gate_qwen3_8b_unfused", "read_floor_8812800"]:
             if name == wl.name:
                 continue
             w2 = WORKLOADS[name]()

@@ -382,6 +382,24 @@ int oco_matvec_norm(uint32_t format, const void *w, const void *x, const float *
                     int full_layer, void *y, oco_dtype y_dtype, const float *bias,
                     const uint32_t *ids, const oco_matrix *p, oco_stream stream);
 
+/* Several matrices of one format and shape -- `count` (1..4) weights w[i]
+ * into outputs y[i] with biases bias[i] (bias may be NULL when
+ * p->has_bias == 0) -- over the same input rows x, in one grid: the
+ * projections that share an input (ffn_up and ffn_gate) stream back to
+ * back with no launch between them, and the input row and its optional
+ * RMS norm (norm_w != NULL: x is the bf16 row before normalisation, as in
+ * oco_matvec_norm) are staged once per workgroup for all of them.  Each
+ * y[i] equals oco_matvec (or oco_matvec_norm) of w[i] bit for bit.  Dense
+ * matrices only (p->experts <= 1).  Replaces the concurrent pair of the
+ * reference's feed-forward entry: apply_norm for `up`, then
+ * apply_norm_concurrent for `gate`, which skips the barrier between the two
+ * dispatches (src/weights/compute/feed_forward.rs:97-104,
+ * compute/matrix.rs:127-146, src/gpu/dispatch.rs:235-259). */
+#define OCO_MATVEC_GROUP_MAX 4u
+int oco_matvec_group(uint32_t format, uint32_t count, const void *const *w, const void *x, oco_dtype x_dtype,
+                     const float *norm_w, float epsilon, int full_layer, void *const *y, oco_dtype y_dtype,
+                     const float *const *bias, const oco_matrix *p, oco_stream stream);
+
 /* Greedy token selection over n f32 logits: out[0] = index of the largest
  * value (ties: lowest index; -0 == +0), or 0xffffffff if any logit is Inf or
  * NaN or n == 0.  Replaces Compute::argmax / argmax_f32

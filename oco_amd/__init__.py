@@ -173,6 +173,7 @@ SIGNATURES = {
     "oco_norm": (_i32, [_vp, _vp, _vp, _u32, _u32, ctypes.c_float, _i32, _vp]),
     "oco_add_norm": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, ctypes.c_float, _i32, _vp]),
     "oco_matvec_norm": (_i32, [_u32, _vp, _vp, _vp, ctypes.c_float, _i32, _vp, _i32, _vp, _vp, _MP, _vp]),
+    "oco_matvec_group": (_i32, [_u32, _u32, _vp, _vp, _i32, _vp, ctypes.c_float, _i32, _vp, _i32, _vp, _MP, _vp]),
     "oco_argmax_f32": (_i32, [_vp, _u32, _vp, _vp]),
     "oco_argmax_workspace": (_u64, [_u32]),
     "oco_argmax_f32_ws": (_i32, [_vp, _u32, _vp, _vp, _u64, _vp]),
@@ -493,6 +494,19 @@ def matvec_norm(fmt: int, w, x, norm_w, epsilon: float, y, p: Matrix, full_layer
     _check(load_library().oco_matvec_norm(int(fmt), _addr(w), _addr(x), _addr(norm_w), epsilon,
                                           int(full_layer), _addr(y), int(y_dtype), _addr(bias), _addr(ids),
                                           ctypes.byref(as_matrix(p)), _stream(stream)))
+
+
+def matvec_group(fmt: int, ws, x, ys, p: Matrix, x_dtype=DType.BF16, y_dtype=DType.F32, norm_w=None,
+                 epsilon: float = 1e-6, full_layer: bool = True, biases=None, stream=None):
+    """Several matrices over the same input rows in one grid (the concurrent
+    up/gate pair of feed_forward.rs:97-104); norm_w: fused RMS norm of bf16 x."""
+    n = len(ws)
+    wa = (ctypes.c_void_p * n)(*[_addr(w) for w in ws])
+    ya = (ctypes.c_void_p * n)(*[_addr(y) for y in ys])
+    ba = (ctypes.c_void_p * n)(*[_addr(b) for b in biases]) if biases is not None else None
+    _check(load_library().oco_matvec_group(int(fmt), n, wa, _addr(x), int(x_dtype), _addr(norm_w), epsilon,
+                                           int(full_layer), ya, int(y_dtype), ba, ctypes.byref(as_matrix(p)),
+                                           _stream(stream)))
 
 
 def argmax_workspace(n: int) -> int:

@@ -17,7 +17,7 @@ LIB = os.path.join(HERE, "liboco_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-SOURCES = ["runtime.hip", "dequant.hip", "matvec.hip", "routing.hip", "experts.hip", "matmul.hip", "mxmatmul.hip", "moe_prefill.hip", "mx_experts.hip", "elementwise.hip", "gguf.cpp"]
+SOURCES = ["matvec.hip", "matvec_group.hip", "runtime.hip", "dequant.hip", "routing.hip", "experts.hip", "matmul.hip", "mxmatmul.hip", "moe_prefill.hip", "mx_experts.hip", "elementwise.hip", "gguf.cpp"]
 
 FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17",

@@ -13,7 +13,7 @@ import pytest
 
 import argmax_cases as A
 import oracle as O
-from _util import Guarded, say
+from _util import Guarded, say, upload_at_offset
 
 pytestmark = pytest.mark.gpu
 
@@ -141,11 +141,16 @@ def test_matvec_norm_equals_norm_then_matvec(lib, fmt, n, k):
     assert np.linalg.norm(got - want) <= 1e-3 * np.linalg.norm(want)  # the input itself differs by one bf16 rounding
 
 
-@pytest.mark.parametrize("plan", ["1,2,2", "1,4,2", "2,1,3"])
-def test_matvec_norm_stream_plans(lib, plan, monkeypatch):
-    """Fused staging under K splits (the LDS area the norm reduction shares)."""
+@pytest.mark.parametrize("plan", [(1, 2, 2), (1, 4, 2), (1, 1, 3)])
+def test_matvec_norm_stream_plans(lib, plan):
+    """Fused staging under K splits (the LDS area the norm reduction shares),
+    forced through the stream-plan knob."""
+    with lib.overridden(lib.Knob.STREAM_PLAN, plan):
+        _matvec_norm_stream_plan_case(lib)
+
+
+def _matvec_norm_stream_plan_case(lib):
     from oco_amd import synth
-    monkeypatch.setenv("OCO_STREAM_PLAN", plan)
     fmt, n, k = 14, 100, 8192
     data = synth.weights(fmt, n, k, seed=3)
     x, w = _rows(9, 1, k)
@@ -190,3 +195,56 @@ def test_buffer_xor32(lib, words):
     buf.xor32(out)
     lib.synchronize()
     assert np.bitwise_xor.reduce(out.download(np.uint32)) == np.bitwise_xor.reduce(data)
+
+
+GROUP_CASES = [(12, 2, 300, 4096, 0), (12, 2, 12288, 4096, 0), (12, 3, 257, 2048, 7), (14, 2, 130, 12288, 0),
+               (8, 4, 100, 4096, 0), (39, 2, 201, 2880, 3), (2, 2, 70, 512, 0), (13, 2, 96, 1024, 0),
+               (1, 2, 33, 512, 0)]
+
+
+@pytest.mark.parametrize("fmt,count,n,k,offset", GROUP_CASES)
+def test_matvec_group_equals_separate_calls(lib, fmt, count, n, k, offset):
+    """oco_matvec_group (the up/gate pair in one grid) equals one
+    oco_matvec_norm / oco_matvec call per matrix bit for bit: with and
+    without the fused norm (both rounding modes), bias, bf16 and f32
+    outputs, two input rows, 2-4 matrices, weights 16-byte aligned (the
+    direct Q4_K loads) or at a byte offset (the LDS tile), and formats
+    without a streaming kernel (one call per matrix)."""
+    from oco_amd import synth
+    import packers as P
+    say("matvec_group", fmt, count, n, k, offset)
+    mats = []
+    for i in range(count):
+        if fmt in (8, 12, 14, 39):
+            data = synth.weights(fmt, n, k, seed=fmt + n + 31 * i)
+        else:
+            data = np.frombuffer(P.dense_weights(fmt, n, k)[0], np.uint8)[::-1].copy() if i else \
+                np.frombuffer(P.dense_weights(fmt, n, k)[0], np.uint8)
+        mats.append(upload_at_offset(lib, data, offset))
+    wptrs = [ptr for _, ptr in mats]
+    rows = 2
+    x, w = _rows(k + 3 * n, rows, k, scale=2.0)
+    xb, nb = lib.DeviceBuffer.from_array(x), lib.DeviceBuffer.from_array(w)
+    xf = lib.DeviceBuffer.from_array(O.bf16_to_f32(x).astype(np.float32))
+    biases = [lib.DeviceBuffer.from_array(np.random.default_rng(i).normal(size=n).astype(np.float32))
+              for i in range(count)]
+    for norm, full, y_dt, has_bias, x_dt in [(True, True, lib.DType.F32, 0, lib.DType.BF16),
+                                              (True, False, lib.DType.BF16, 1, lib.DType.BF16),
+                                              (False, True, lib.DType.F32, 1, lib.DType.F32),
+                                              (False, True, lib.DType.BF16, 0, lib.DType.BF16)]:
+        p = lib.Matrix(k, n, rows, 0, 1, 1, has_bias)
+        esz = 2 if y_dt == lib.DType.BF16 else 4
+        xin = xb if x_dt == lib.DType.BF16 else xf
+        sep = [Guarded(lib, rows * n * esz) for _ in range(count)]
+        grp = [Guarded(lib, rows * n * esz) for _ in range(count)]
+        for i in range(count):
+            b = biases[i] if has_bias else None
+            if norm:
+                lib.matvec_norm(fmt, wptrs[i], xb, nb, 1e-5, sep[i].ptr, p, full, y_dt, b)
+            else:
+                lib.matvec(fmt, wptrs[i], xin, sep[i].ptr, p, x_dt, y_dt, b)
+        lib.matvec_group(fmt, wptrs, xin, [g.ptr for g in grp], p, x_dt, y_dt, nb if norm else None, 1e-5, full,
+                         biases if has_bias else None)
+        lib.synchronize()
+        for i in range(count):
+            assert np.array_equal(sep[i].read(np.uint8), grp[i].read(np.uint8)), (i, norm, full, y_dt)
