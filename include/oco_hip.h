@@ -385,15 +385,15 @@ int oco_matvec_norm(uint32_t format, const void *w, const void *x, const float *
 /* Several matrices of one format and shape -- `count` (1..4) weights w[i]
  * into outputs y[i] with biases bias[i] (bias may be NULL when
  * p->has_bias == 0) -- over the same input rows x, in one grid: the
- * projections that share an input (ffn_up and ffn_gate) stream back to
+ * projections that share an input (ffn_gate and ffn_up) stream back to
  * back with no launch between them, and the input row and its optional
  * RMS norm (norm_w != NULL: x is the bf16 row before normalisation, as in
  * oco_matvec_norm) are staged once per workgroup for all of them.  Each
  * y[i] equals oco_matvec (or oco_matvec_norm) of w[i] bit for bit.  Dense
  * matrices only (p->experts <= 1).  Replaces the concurrent pair of the
- * reference's feed-forward entry: apply_norm for `up`, then
- * apply_norm_concurrent for `gate`, which skips the barrier between the two
- * dispatches (src/weights/compute/feed_forward.rs:97-104,
+ * reference's feed-forward entry (Compute::feed_forward): apply_norm for
+ * `gate`, then apply_norm_concurrent for `up`, which skips the barrier
+ * between the two dispatches (src/weights/compute/feed_forward.rs:97-104,
  * compute/matrix.rs:127-146, src/gpu/dispatch.rs:235-259). */
 #define OCO_MATVEC_GROUP_MAX 4u
 int oco_matvec_group(uint32_t format, uint32_t count, const void *const *w, const void *x, oco_dtype x_dtype,

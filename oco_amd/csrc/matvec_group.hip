@@ -1,6 +1,6 @@
 // The grouped streaming matvec: several matrices of one format and shape
 // over the same activation rows in one grid (oco_matvec_group), so that
-// the projections that share an input -- ffn_up and ffn_gate after one
+// the projections that share an input -- ffn_gate and ffn_up after one
 // norm -- stream back to back without a launch between them, with the
 // activation vector (and its fused norm) staged once per workgroup for all
 // of them.  The reference issues the second of such a pair with
