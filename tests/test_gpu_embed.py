@@ -22,14 +22,12 @@ def same_bf16_nan_aware(got, want):
 
 
 @pytest.mark.parametrize("fmt", ALL_FORMATS)
-@pytest.mark.parametrize("k", [512, 2880 + 32 * 3, 4096])
+@pytest.mark.parametrize("k", [512, 2816, 4096])
 def test_embed_random_bytes_bit_exact(lib, fmt, k):
     """Random bytes reach every code and subnormal/Inf/NaN scale; rows of
     the vocabulary in any order and repeated, two feature rows, and one id
     past them (a NaN row); weights at byte offset 7 and 0."""
     e, b = O.block_layout(fmt)
-    if k % e:
-        pytest.skip("width is not whole blocks")
     say("embed random bytes", fmt, k)
     vocab = 37
     rb = k // e * b
