@@ -272,7 +272,7 @@ static int matvec_impl(uint32_t format, const void *w, const void *x, oco_dtype 
         const uint32_t P = (format == OCO_Q4_K || format == OCO_Q5_K || format == OCO_Q6_K) ? 8 : 1;
         const uint32_t nblocks = p->k / be;
         const uint32_t nmat = grp ? grp->count : 1u;
-        StreamPlan sp = stream_plan(format, p->k, p->n * nmat, p->m, norm != nullptr);
+        StreamPlan sp = stream_plan(format, p->k, p->n * nmat, p->m, norm != nullptr && !grp);
         if (sp.ks != 1 && sp.ks != 2 && sp.ks != 4) sp.ks = 1;
         uint32_t slice_blocks = (nblocks + sp.ks - 1) / sp.ks;
         int npl = (int)((slice_blocks * P + 31) / 32);

@@ -164,7 +164,12 @@ __global__ __launch_bounds__(256) void stream_kernel(const uint8_t *w_, const vo
     u32x4 ra[DIRECT ? 1 : ROWS * LPR], rb[DIRECT ? 1 : ROWS * LPR];
     // DIRECT: a ring of three sets of pieces; a set is refilled right after
     // its group is decoded, so two groups stay in flight with no copies.
-    typename T::Raw da[DIRECT ? NPL : 1], db[DIRECT ? NPL : 1], dc[DIRECT ? NPL : 1];
+    // DIRECT: groups in flight per wavefront.  The grouped form runs longer
+    // per workgroup and takes a fourth, at three workgroups per CU even with
+    // the fused norm (norm + Qwen3-8B up + gate: 21.6 -> 20.8-21.3 us);
+    // single matrices lose with it (Q4_K 12288 x 4096: 10.5 -> 11.0 us).
+    constexpr int RD = MULTI ? 4 : 3;
+    typename T::Raw da[DIRECT ? NPL : 1], db[DIRECT ? NPL : 1], dc[DIRECT ? NPL : 1], dd[DIRECT && RD > 3 ? NPL : 1];
     // DIRECT: one buffer resource over the matrix.  The range ends at a
     // whole dword: a block's dword-aligned span may end up to three bytes
     // past the tensor, and a dword that straddles the range end would read
@@ -272,6 +277,7 @@ __global__ __launch_bounds__(256) void stream_kernel(const uint8_t *w_, const vo
         if (g0 < total) issue_direct(g0, da);
         if (g0 + G < total) issue_direct(g0 + G, db);
         if (g0 + 2 * G < total) issue_direct(g0 + 2 * G, dc);
+        if (RD > 3 && g0 + 3 * G < total) issue_direct(g0 + 3 * G, dd);
     } else {
         if (g0 < total) issue(g0, ra);
         if (g0 + G < total) issue(g0 + G, rb);
@@ -371,7 +377,7 @@ __global__ __launch_bounds__(256) void stream_kernel(const uint8_t *w_, const vo
                 const uint32_t pl = c + 32 * s;
                 if (pl < pieces) acc += tile_dot<FMT>(dr[s], xv[s], sv[s], pl % T::P);
             }
-            if (g + 3 * G < total) issue_direct(g + 3 * G, dr);
+            if (g + RD * G < total) issue_direct(g + RD * G, dr);
         } else {
 #pragma unroll
             for (int i = 0; i < ROWS * LPR; i++) reinterpret_cast<u32x4 *>(tile)[i * 64 + lane] = regs[i];
@@ -417,10 +423,11 @@ __global__ __launch_bounds__(256) void stream_kernel(const uint8_t *w_, const vo
         }
     };
     if constexpr (DIRECT) {
-        for (uint32_t g = g0; g < total; g += 3 * G) {
+        for (uint32_t g = g0; g < total; g += RD * G) {
             group(g, ra, da);
             if (g + G < total) group(g + G, rb, db);
             if (g + 2 * G < total) group(g + 2 * G, ra, dc);
+            if (RD > 3 && g + 3 * G < total) group(g + 3 * G, ra, dd);
         }
     } else {
         for (uint32_t g = g0; g < total; g += 2 * G) {
