@@ -39,19 +39,26 @@ namespace oco {
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-// One record per (32-row tile, K step of 64): [term 2][lane 64][16 B] then
-// [term 2][lane 64][8 B] of E2M3 codes (lane l's 24-byte fragment is its
-// 16-byte part and its 8-byte part), then [lane 64] u32 of E8M0 scales
-// (byte t = term t).  Lane l = row l % 32, block l / 32 of the step.
-constexpr uint32_t MX_LO = 2 * 64 * 16, MX_DATA = 2 * 64 * 24, MX_REC = MX_DATA + 64 * 4;
+// Split activations, lane l = (row l % 32, block l / 32) of a 32-row tile
+// and K step of 64:
+//  * codes: one record per (tile, step), [chunk 3][lane 64][16 B]: lane l's
+//    48 bytes are term 0's 24 bytes of E2M3 codes, then term 1's, so three
+//    aligned 16-byte loads give both MFMA operands in six consecutive
+//    dwords each;
+//  * scales: one record per (tile, stage of 8 steps), [lane 64][16 B]:
+//    byte 2 L + t is step L's term-t E8M0 scale (dword L / 2, selected by
+//    the MFMA's op_sel).
+// Steps are counted to whole stages; the split writes the padding steps as
+// zero codes under scale byte 0 (2^-127), which add nothing.
+constexpr uint32_t MX_STAGE = 8, MX_REC = 3 * 64 * 16, MX_SREC = 64 * 16;
 
 typedef mx_f32x32 f32x32;
 typedef mx_i32x6 i32x6;
 
 struct MxSplitArgs {
     const uint16_t *x;
-    uint8_t *frag;
-    uint32_t m, k, ksteps, records;
+    uint8_t *frag, *scl;
+    uint32_t m, k, kpad, records;
 };
 
 // One wavefront (workgroup) per record, so the records spread over every CU;
@@ -66,7 +73,7 @@ struct MxSplitArgs {
 __global__ __launch_bounds__(64) void mx_split_kernel(KPRE_PARAMS, MxSplitArgs a) {
     KPRE_APPLY(a);
     const uint32_t rec = blockIdx.x;
-    const uint32_t lane = threadIdx.x, tile = rec / a.ksteps, s = rec % a.ksteps;
+    const uint32_t lane = threadIdx.x, tile = rec / a.kpad, s = rec % a.kpad;
     const uint32_t row = tile * 32 + (lane & 31), k0 = s * 64 + 32 * (lane >> 5);
     uint32_t w[16];
     if (row < a.m && k0 < a.k) {
@@ -88,6 +95,7 @@ __global__ __launch_bounds__(64) void mx_split_kernel(KPRE_PARAMS, MxSplitArgs a
     }
     auto out = gp(a.frag + (uint64_t)rec * MX_REC);
     uint32_t scales = 0;
+    i32x6 c0;
 #pragma unroll
     for (int t = 0; t < 2; t++) {
         // |x| bit patterns order like the values, with Inf above every finite
@@ -110,9 +118,16 @@ __global__ __launch_bounds__(64) void mx_split_kernel(KPRE_PARAMS, MxSplitArgs a
             hi[i] = v[16 + i] * inv;
         }
         const i32x6 c = fp6_pack(lo, hi);
-        *reinterpret_cast<__attribute__((address_space(1))) u32x4 *>(out + (t * 64 + lane) * 16) =
-            u32x4{(uint32_t)c[0], (uint32_t)c[1], (uint32_t)c[2], (uint32_t)c[3]};
-        *reinterpret_cast<__attribute__((address_space(1))) u32x2 *>(out + MX_LO + (t * 64 + lane) * 8) = u32x2{(uint32_t)c[4], (uint32_t)c[5]};
+        auto chunk = [&](int q, u32x4 v) {
+            *reinterpret_cast<__attribute__((address_space(1))) u32x4 *>(out + (q * 64 + lane) * 16) = v;
+        };
+        if (t == 0) {
+            chunk(0, u32x4{(uint32_t)c[0], (uint32_t)c[1], (uint32_t)c[2], (uint32_t)c[3]});
+            c0 = c;
+        } else {
+            chunk(1, u32x4{(uint32_t)c0[4], (uint32_t)c0[5], (uint32_t)c[0], (uint32_t)c[1]});
+            chunk(2, u32x4{(uint32_t)c[2], (uint32_t)c[3], (uint32_t)c[4], (uint32_t)c[5]});
+        }
         if (t == 0) {
             const f32x32 d = fp6_unpack(c);
 #pragma unroll
@@ -122,7 +137,9 @@ __global__ __launch_bounds__(64) void mx_split_kernel(KPRE_PARAMS, MxSplitArgs a
             }
         }
     }
-    *reinterpret_cast<__attribute__((address_space(1))) uint32_t *>(out + MX_DATA + lane * 4) = scales;
+    *reinterpret_cast<__attribute__((address_space(1))) uint16_t *>(
+        gp(a.scl + ((uint64_t)tile * (a.kpad / MX_STAGE) + s / MX_STAGE) * MX_SREC + lane * 16 + 2 * (s % MX_STAGE))) =
+        (uint16_t)scales;
 }
 
 // The first 56 bytes arrive in SGPRs (KPre).
@@ -130,6 +147,8 @@ struct MxArgs {
     const uint8_t *w;
     const uint8_t *frag;
     uint32_t m, n, k, ksteps, tiles;
+    uint32_t kpad;
+    const uint8_t *scl;
     uint32_t row_bytes;
     uint32_t wspan;  // weight bytes from the 16-byte aligned base, rounded up to 16 (< 4 GiB)
     uint32_t y_bf16;
@@ -152,117 +171,101 @@ __device__ __forceinline__ void static_for(F &&f) {
 typedef void (*MxFn)(u32x4, u32x4, u32x4, u32x2, MxArgs);
 
 // ---------------------------------------------------------------------------
-// Prefill tile: workgroup = four wavefronts, WM along the activation rows
-// and 4 / WM along the weight rows (output columns); each wavefront owns one
-// 32-row activation tile and CTW 32-column weight tiles, so a K step is
-// 2 CTW independent MFMAs (the two activation terms of every column tile).
+// Prefill tile: 32 RT activation rows x 32 CT weight rows (output columns)
+// per workgroup of eight wavefronts in two roles, one of each per SIMD:
 //
-//  * A: each wavefront's split records go straight into a register ring RA
-//    K steps deep, through a buffer resource whose step offset is scalar.
-//  * B: GGUF rows staged eight K steps (16 blocks, 272 bytes) at a time.
-//    272 is a multiple of 16, so a row's stage span starts at the same
-//    misalignment every time: it is fetched as the 18 aligned 16-byte
-//    chunks that cover it, 18 consecutive lanes per row -- nearly the
-//    contiguous pattern L2 serves best (measured from L2: contiguous 1 KB
-//    wavefront loads ~55 bytes/clock per CU; four lanes per 68-byte row
-//    segment ~19).  The chunks land in a raw LDS buffer as they are; one
-//    pass per stage, shared by the workgroup, realigns every 17-byte block
-//    into an aligned [block][row] payload array and a [row][block] array
-//    of scale bytes.  A step then reads one aligned 16-byte fragment per
-//    column tile, and the stage's eight scales per row come in one 8-byte
-//    read (op_sel picks the step's byte).  Realigning per wavefront at
-//    fragment-read time instead put five dependent LDS reads and four
-//    v_alignbyte per fragment on every wavefront's critical path
-//    (measured: that loop alone, without loads or MFMAs, took 15 us).
+//  * Wavefronts 0 .. RT - 1 (one per 32-row activation tile) only issue
+//    MFMAs.  A K step is 2 CT independent MFMAs (the two activation terms of
+//    every column tile).  Their split records go straight into a register
+//    ring RA K steps deep, through a buffer resource whose step offset is
+//    scalar; their B fragments come from LDS, one aligned 16-byte read per
+//    column tile, read one step ahead.
+//  * Wavefronts RT .. 7 only stage the weights.  GGUF rows are staged eight
+//    K steps (16 blocks, 272 bytes) at a time.  272 is a multiple of 16, so
+//    a row's stage span starts at the same misalignment every time: it is
+//    fetched as the 18 aligned 16-byte chunks that cover it, 18 consecutive
+//    lanes per row (nearly the contiguous pattern L2 serves best), and
+//    written to a raw LDS buffer as it comes.  One pass per stage realigns
+//    every 17-byte block into an aligned [block][row] payload array and a
+//    [row][block] array of scale bytes (unaligned 16-byte LDS reads are
+//    correct on gfx950 but run at an eighth of the aligned rate; five dword
+//    reads and four v_alignbyte per block cost the staging wavefronts, not
+//    the MFMA issue).
 //
-//    Per stage o (one barrier): realign raw stage o + 1; write stage
-//    o + 2's chunks (in registers since stage o - 1) to the other raw
-//    buffer; request stage o + 3's chunks; run the eight steps of stage o.
-template <int WM, int CTW>
+// Per stage o (one barrier): the staging wavefronts realign raw stage
+// o + 1, write stage o + 2's chunks (in their registers since stage o - 1)
+// to the other raw buffer and request stage o + 3's; meanwhile the MFMA
+// wavefronts run the eight steps of stage o from the aligned buffer written
+// during stage o - 1.
+template <int CT>
 struct MxPlan {
-    static constexpr int WN = 4 / WM, BM = 32 * WM, BN = 32 * CTW * WN;
+    static constexpr int RT = 4, BM = 32 * RT, BN = 32 * CT;
     static constexpr int OCT = 8;     // K steps per B stage
     static constexpr int CH = 18;     // 16-byte chunks per row and stage
     static constexpr int RSTR = 296;  // raw LDS bytes per row (18 chunks + pad)
-    static constexpr int NTH = 512;                          // threads: two wavefronts per (row tile, columns)
-    static constexpr int BU = (BN * CH + NTH - 1) / NTH;      // chunk slots per thread
-    static constexpr int RU = (BN * 2 * OCT + NTH - 1) / NTH; // realigned blocks per thread
-    static constexpr int PROW = BN + 1;                     // payload slots per block row
+    static constexpr int NTH = 512, NL = NTH - 64 * RT;     // threads; staging threads
+    static constexpr int BU = (BN * CH + NL - 1) / NL;       // chunk slots per staging thread
+    static constexpr int RU = (BN * 2 * OCT + NL - 1) / NL;  // realigned blocks per staging thread
+    static constexpr int PROW = BN + 1;                      // payload slots per block row
     static constexpr int RAW = BN * RSTR, PAY = 2 * OCT * PROW * 16, SCL = BN * 2 * OCT;
     static constexpr int ALN = PAY + SCL;
     static constexpr int LDS = 2 * RAW + 2 * ALN;
-    static constexpr int RA = 2;  // A ring: this wavefront's next two own steps (four K steps ahead)
-    static_assert((OCT / 2) % RA == 0, "ring slots repeat every stage");
-    static constexpr int RED = 4 * CTW * 16 * 64 * 4, OROW = BN + 4, OUT = BM * OROW * 4;
-    static_assert(RED + OUT <= LDS, "the K-half sums and the output tile fit the stage buffers");
+    static constexpr int RA = OCT;  // A ring: one stage of K steps ahead
+    static_assert(OCT == (int)MX_STAGE, "A scale records cover one B stage");
+    static constexpr int OROW = BN + 4, OUT = BM * OROW * 4;
+    static_assert(OUT <= LDS, "the output tile fits the stage buffers");
 };
 
-template <int WM, int CTW>
+template <int CT>
 __global__ __launch_bounds__(512) void mx_matmul_kernel(KPRE_PARAMS, MxArgs a) {
     KPRE_APPLY(a);
-    using P = MxPlan<WM, CTW>;
-    constexpr int BN = P::BN, BU = P::BU, RU = P::RU, RA = P::RA, CT = CTW, OCT = P::OCT;
+    using P = MxPlan<CT>;
+    constexpr int BN = P::BN, BU = P::BU, RU = P::RU, RA = P::RA, OCT = P::OCT, RT = P::RT;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     uint8_t *const raw = lds, *const aln = lds + 2 * P::RAW;
-    // The wavefront index is uniform: readfirstlane keeps the A resource in SGPRs.
+    // The wavefront index is uniform: readfirstlane keeps the role and the
+    // A resource in SGPRs.
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, c = lane & 31,
               part = lane >> 5;
-    // Wavefronts w and w + 4 share a row tile and its column tiles: kw = 0
-    // takes the even steps of every stage, kw = 1 the odd ones.
-    const int kw = wave >> 2, w4 = wave & 3, wm = w4 % WM, wn = w4 / WM;
+    const bool mfma_wave = wave < RT;
     // Logical (column tile, row group), column-major per XCD: the row groups
     // of one weight column tile share its GGUF bytes in one L2.
     const uint32_t lin = xcd_order(blockIdx.x + gridDim.x * blockIdx.y, gridDim.x * gridDim.y);
     const uint32_t bx = lin / gridDim.y, by = lin % gridDim.y;
-    const uint32_t tile = by * WM + wm, col0 = bx * BN;
+    const uint32_t col0 = bx * BN;
     const uint32_t nblk = a.k / 32, nsteps = a.ksteps;
+    const uint32_t nst = (nsteps + OCT - 1) / OCT;
 
-    // A: this wavefront's records; steps past the end read as zero.
-    const __amdgpu_buffer_rsrc_t ra_rs =
-        uniform_rsrc(a.frag + (uint64_t)min(tile, a.tiles - 1) * a.ksteps * MX_REC, a.ksteps * MX_REC);
+    // ---- staging wavefronts: B chunk slots and realignment slots ----
     // B: the tensor from its 16-byte aligned base; bytes past the end read as zero.
     const uint32_t wsh = (uint32_t)((uintptr_t)a.w & 15u);
     const __amdgpu_buffer_rsrc_t rb_rs = uniform_rsrc(a.w - wsh, a.wspan);
-    const uint32_t rbytes = (uint32_t)a.row_bytes;
-    // Chunk slot q = tid + 512 u: chunk q % 18 of tile row q / 18 (rows past
+    const uint32_t rbytes = (uint32_t)a.row_bytes, st = (uint32_t)(tid - 64 * RT);
+    // Chunk slot q = st + NL u: chunk q % 18 of tile row q / 18 (rows past
     // n repeat row n - 1 and are never stored).
     uint32_t boff[BU], bdst[BU];
-#pragma unroll
-    for (int u = 0; u < BU; u++) {
-        const uint32_t q = tid + P::NTH * u, row = min(q / P::CH, (uint32_t)BN - 1), ch = q % P::CH;
-        const bool live = q < (uint32_t)(BN * P::CH);
-        boff[u] = live ? ((wsh + min(col0 + row, a.n - 1) * rbytes) & ~15u) + 16 * ch : 0u;
-        bdst[u] = live ? row * P::RSTR + 16 * ch : ~0u;  // ~0: no slot (the last round's spare threads)
-    }
-    // Realign slot r = tid + 512 u: block r / BN of tile row r % BN; its
-    // scale byte sits at rsrc in the raw buffer, its payload right after.
+    // Realign slot r = st + NL u: block r / BN of tile row r % BN; its scale
+    // byte sits at rsrc in the raw buffer, its payload right after.
     uint32_t rsrc[RU], rpay[RU], rscl[RU];
-#pragma unroll
-    for (int u = 0; u < RU; u++) {
-        const uint32_t r = tid + P::NTH * u, row = r % BN, blk = r / BN;
-        const bool live = r < (uint32_t)(BN * 2 * OCT);
-        rsrc[u] = row * P::RSTR + ((wsh + min(col0 + row, a.n - 1) * rbytes) & 15u) + 17 * blk;
-        rpay[u] = live ? (blk * P::PROW + row) * 16 : ~0u;
-        rscl[u] = P::PAY + row * 2 * OCT + (blk & 1) * OCT + (blk >> 1);
-    }
-    const uint32_t wcol = wn * CT * 32;  // this wavefront's first column within the tile
-
-    i32x8 av[RA][2];
-    uint32_t as[RA];
     u32x4 bv[BU];
-    auto load_a = [&](auto slot, uint32_t s) {
-        constexpr int U = decltype(slot)::value;
-        const uint32_t so = s * MX_REC;
+    if (!mfma_wave) {
 #pragma unroll
-        for (int t = 0; t < 2; t++) {
-            const u32x4 lo = __builtin_amdgcn_raw_buffer_load_b128(ra_rs, (t * 64 + lane) * 16, so, 0);
-            const u32x2 hi = __builtin_amdgcn_raw_buffer_load_b64(ra_rs, MX_LO + (t * 64 + lane) * 8, so, 0);
-            av[U][t] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, 0, 0};
+        for (int u = 0; u < BU; u++) {
+            const uint32_t q = st + P::NL * u, row = min(q / P::CH, (uint32_t)BN - 1), ch = q % P::CH;
+            const bool live = q < (uint32_t)(BN * P::CH);
+            boff[u] = live ? ((wsh + min(col0 + row, a.n - 1) * rbytes) & ~15u) + 16 * ch : 0u;
+            bdst[u] = live ? row * P::RSTR + 16 * ch : ~0u;  // ~0: no slot (the last round's spare threads)
         }
-        as[U] = __builtin_amdgcn_raw_buffer_load_b32(ra_rs, MX_DATA + lane * 4, so, 0);
-    };
+#pragma unroll
+        for (int u = 0; u < RU; u++) {
+            const uint32_t r = st + P::NL * u, row = r % BN, blk = r / BN;
+            const bool live = r < (uint32_t)(BN * 2 * OCT);
+            rsrc[u] = row * P::RSTR + ((wsh + min(col0 + row, a.n - 1) * rbytes) & 15u) + 17 * blk;
+            rpay[u] = live ? (blk * P::PROW + row) * 16 : ~0u;
+            rscl[u] = P::PAY + row * 2 * OCT + (blk & 1) * OCT + (blk >> 1);
+        }
+    }
     // B chunks of stage o (steps 8 o .. 8 o + 7).
-    const uint32_t nst = (nsteps + OCT - 1) / OCT;
     auto load_b = [&](uint32_t o) {
 #pragma unroll
         for (int u = 0; u < BU; u++) bv[u] = __builtin_amdgcn_raw_buffer_load_b128(rb_rs, boff[u], o * 272, 0);
@@ -271,7 +274,7 @@ __global__ __launch_bounds__(512) void mx_matmul_kernel(KPRE_PARAMS, MxArgs a) {
         constexpr int S = decltype(buf)::value;
 #pragma unroll
         for (int u = 0; u < BU; u++) {
-            if ((BN * P::CH) % P::NTH == 0 || u + 1 < BU || bdst[u] != ~0u) {
+            if ((BN * P::CH) % P::NL == 0 || u + 1 < BU || bdst[u] != ~0u) {
                 *reinterpret_cast<u32x2 *>(raw + S * P::RAW + bdst[u]) = u32x2{bv[u].x, bv[u].y};
                 *reinterpret_cast<u32x2 *>(raw + S * P::RAW + bdst[u] + 8) = u32x2{bv[u].z, bv[u].w};
             }
@@ -282,7 +285,7 @@ __global__ __launch_bounds__(512) void mx_matmul_kernel(KPRE_PARAMS, MxArgs a) {
         constexpr int S = decltype(buf)::value;
 #pragma unroll
         for (int u = 0; u < RU; u++) {
-            if ((BN * 2 * OCT) % P::NTH == 0 || u + 1 < RU || rpay[u] != ~0u) {
+            if ((BN * 2 * OCT) % P::NL == 0 || u + 1 < RU || rpay[u] != ~0u) {
                 const uint32_t o = S * P::RAW + rsrc[u], p = o + 1, sh = p & 3u;
                 const uint32_t *w = reinterpret_cast<const uint32_t *>(raw + (p & ~3u));
                 const uint32_t w0 = w[0], w1 = w[1], w2 = w[2], w3 = w[3], w4 = w[4];
@@ -294,117 +297,145 @@ __global__ __launch_bounds__(512) void mx_matmul_kernel(KPRE_PARAMS, MxArgs a) {
         }
     };
 
+    // ---- MFMA wavefronts ----
+    const uint32_t tile = by * RT + (mfma_wave ? wave : 0);
+    // A: this wavefront's records; steps past the end read as zero.
+    const uint32_t atile = min(tile, a.tiles - 1);
+    const __amdgpu_buffer_rsrc_t ra_rs = uniform_rsrc(a.frag + (uint64_t)atile * a.kpad * MX_REC, a.kpad * MX_REC);
+    const __amdgpu_buffer_rsrc_t rs_rs =
+        uniform_rsrc(a.scl + (uint64_t)atile * (a.kpad / OCT) * MX_SREC, (a.kpad / OCT) * MX_SREC);
+    u32x4 av[RA][3];
+    auto load_a = [&](auto slot, uint32_t s) {
+        constexpr int U = decltype(slot)::value;
+#pragma unroll
+        for (int q = 0; q < 3; q++) av[U][q] = __builtin_amdgcn_raw_buffer_load_b128(ra_rs, (q * 64 + lane) * 16, s * MX_REC, 0);
+    };
+    // The A scales of a stage, one word per pair of steps.
+    u32x4 asv[2];
+    auto load_as = [&](auto buf, uint32_t o) {
+        constexpr int S = decltype(buf)::value;
+        asv[S] = __builtin_amdgcn_raw_buffer_load_b128(rs_rs, lane * 16, o * MX_SREC, 0);
+    };
     // One accumulator per column tile; a step issues term 0 over all tiles,
     // then term 1, so consecutive MFMAs never share an accumulator.
     f32x16 acc[CT];
 #pragma unroll
     for (int j = 0; j < CT; j++) acc[j] = f32x16{};
-
     // The stage's scale bytes of this lane's rows: 8 steps, byte L of word L / 4.
     u32x2 sw[CT];
-    // Fragments of step L of aligned buffer S, read one own step (two steps)
-    // ahead of their MFMAs, into set (L / 2) & 1.
+    // Fragments of step L of aligned buffer S, read one step ahead of their
+    // MFMAs, into set L & 1.
     i32x8 bf[2][CT];
     auto frag = [&](auto buf, auto local) {
         constexpr int S = decltype(buf)::value, L = decltype(local)::value;
 #pragma unroll
         for (int t = 0; t < CT; t++) {
-            const u32x4 v = *reinterpret_cast<const u32x4 *>(aln + S * P::ALN +
-                                                             ((2 * L + part) * P::PROW + wcol + t * 32 + c) * 16);
-            bf[(L / 2) & 1][t] = i32x8{(int)v.x, (int)v.y, (int)v.z, (int)v.w, 0, 0, 0, 0};
+            const u32x4 v =
+                *reinterpret_cast<const u32x4 *>(aln + S * P::ALN + ((2 * L + part) * P::PROW + t * 32 + c) * 16);
+            bf[L & 1][t] = i32x8{(int)v.x, (int)v.y, (int)v.z, (int)v.w, 0, 0, 0, 0};
         }
     };
-    // Step s = 8 o + L of stage o (aligned buffer S), A ring slot (L / 2) % RA.
+    // Step s = 8 o + L of stage o (aligned buffer S), A ring slot L.  The
+    // step runs whether or not s < nsteps: branches around the loads or the
+    // MFMAs would make the compiler wait for every outstanding load at each
+    // step.  Past the last step the A records read as zero (codes 0, scale
+    // byte 0) and the weight scales are forced to 1, so the stage span's
+    // bytes of the next row (which may hold the NaN scale byte) add zero.
     auto step = [&](auto buf, auto local, uint32_t s) {
         constexpr int S = decltype(buf)::value, L = decltype(local)::value;
-        if constexpr (L + 2 < OCT) frag(buf, Int<L + 2>{});
-        if (s < nsteps) {
-            // A block past K (odd block count, last step): its weight scale
-            // byte may be E8M0 255 (NaN); the activations there are zero, so
-            // scale 1 keeps it out.
-            const bool dead = part && (nblk & 1) && s == nsteps - 1;
-            uint32_t scl[CT];
+        if constexpr (L + 1 < OCT) frag(buf, Int<L + 1>{});
+        // A block past K (odd block count, last step): its weight scale byte
+        // may be E8M0 255 (NaN); the activations there are zero, so scale 1
+        // keeps it out.
+        const bool dead = (s >= nsteps) | ((part != 0) & ((nblk & 1) != 0) & (s + 1 == nsteps));
+        uint32_t scl[CT];
 #pragma unroll
-            for (int t = 0; t < CT; t++) scl[t] = dead ? 0x7f7f7f7fu : (L < 4 ? sw[t].x : sw[t].y);
-            constexpr int U = (L / 2) % RA, B = L & 3, F = (L / 2) & 1;
-#pragma unroll
-            for (int t = 0; t < CT; t++)
-                acc[t] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av[U][0], bf[F][t], acc[t], 2, 4, 0,
-                                                                          (int)as[U], B, (int)scl[t]);
-#pragma unroll
-            for (int t = 0; t < CT; t++)
-                acc[t] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av[U][1], bf[F][t], acc[t], 2, 4, 1,
-                                                                          (int)as[U], B, (int)scl[t]);
-        }
-        (void)S;
-    };
-    // Stage o: realign raw stage o + 1; write stage o + 2's chunks to the
-    // other raw buffer; request stage o + 3's; then this wavefront's four
-    // steps of stage o (parity kw), each followed by the A request of the
-    // same step one stage ahead.
-    auto body = [&](auto par, uint32_t o) {
-        constexpr int S = decltype(par)::value;
-        realign(Int<1 - S>{});
-        if (o + 2 < nst) store_b(Int<S>{});
-        // (no requests past the last stage: they would be HBM reads that
-        // the kernel's tail waits behind)
-        if (o + 3 < nst) load_b(o + 3);
+        for (int t = 0; t < CT; t++) scl[t] = dead ? 0x7f7f7f7fu : (L < 4 ? sw[t].x : sw[t].y);
+        constexpr int B = L & 3, F = L & 1, AW = L / 2, AB = 2 * (L & 1);
+        const uint32_t asw = asv[S][AW];
+        const u32x4 c0 = av[L][0], c1 = av[L][1], c2 = av[L][2];
+        const i32x8 a0 = {(int)c0.x, (int)c0.y, (int)c0.z, (int)c0.w, (int)c1.x, (int)c1.y, 0, 0};
+        const i32x8 a1 = {(int)c1.z, (int)c1.w, (int)c2.x, (int)c2.y, (int)c2.z, (int)c2.w, 0, 0};
 #pragma unroll
         for (int t = 0; t < CT; t++)
-            sw[t] = *reinterpret_cast<const u32x2 *>(aln + S * P::ALN + P::PAY + (wcol + t * 32 + c) * 2 * OCT + part * OCT);
-        if (kw == 0) {
-            frag(Int<S>{}, Int<0>{});
-            static_for<OCT / 2>([&](auto i) {
-                step(Int<S>{}, Int<2 * i.value>{}, o * OCT + 2 * i.value);
-                load_a(Int<i.value % RA>{}, o * OCT + 2 * (i.value + RA));
-            });
-        } else {
-            frag(Int<S>{}, Int<1>{});
-            static_for<OCT / 2>([&](auto i) {
-                step(Int<S>{}, Int<2 * i.value + 1>{}, o * OCT + 2 * i.value + 1);
-                load_a(Int<i.value % RA>{}, o * OCT + 2 * (i.value + RA) + 1);
-            });
-        }
-        __syncthreads();
+            acc[t] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a0, bf[F][t], acc[t], 2, 4, AB, (int)asw, B,
+                                                                      (int)scl[t]);
+#pragma unroll
+        for (int t = 0; t < CT; t++)
+            acc[t] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a1, bf[F][t], acc[t], 2, 4, AB + 1, (int)asw, B,
+                                                                      (int)scl[t]);
     };
-
-    // Prologue: stage 0 realigned, stage 1 raw in LDS, stage 2 in registers.
-    load_b(0);
-    static_for<RA>([&](auto u) { load_a(u, 2 * u.value + kw); });
-    store_b(Int<0>{});
-    if (nst > 1) load_b(1);
-    __syncthreads();
-    realign(Int<0>{});
-    if (nst > 1) store_b(Int<1>{});
-    if (nst > 2) load_b(2);
-    __syncthreads();
-    for (uint32_t o = 0; o < nst; o += 2) {
-        body(Int<0>{}, o);
-        if (o + 1 < nst) body(Int<1>{}, o + 1);
+    // The two roles run separate loops with the same barriers, so that
+    // neither role's registers are live in the other's.
+    if (mfma_wave) {
+        // The A ring fills in two halves: at the start every workgroup's
+        // requests meet in HBM and L2 at once, and the first B stage (needed
+        // before any MFMA) should not queue behind A steps that are needed
+        // later.
+        load_as(Int<0>{}, 0);
+        static_for<RA / 2>([&](auto u) { load_a(u, u.value); });
+        __syncthreads();
+        static_for<RA / 2>([&](auto u) { load_a(Int<RA / 2 + u.value>{}, RA / 2 + u.value); });
+        __syncthreads();
+        auto body = [&](auto par, uint32_t o) {
+            constexpr int S = decltype(par)::value;
+#pragma unroll
+            for (int t = 0; t < CT; t++)
+                sw[t] = *reinterpret_cast<const u32x2 *>(aln + S * P::ALN + P::PAY + (t * 32 + c) * 2 * OCT + part * OCT);
+            frag(Int<S>{}, Int<0>{});
+            load_as(Int<1 - S>{}, o + 1);  // past the records: zeros, no memory access
+            static_for<OCT>([&](auto i) {
+                step(Int<S>{}, i, o * OCT + i.value);
+                load_a(i, o * OCT + i.value + RA);  // past the records: zeros, no memory access
+                // Keep each step's fragment reads and loads in place: hoisted
+                // reads of later steps only occupy registers.
+                __builtin_amdgcn_sched_barrier(0);
+            });
+            __syncthreads();
+        };
+        // Stages run in pairs (static buffer indices); an odd count gets one
+        // stage of dead steps.
+        for (uint32_t o = 0; o < nst; o += 2) {
+            body(Int<0>{}, o);
+            body(Int<1>{}, o + 1);
+        }
+    } else {
+        // Prologue: stage 0 realigned, stage 1 raw in LDS, stage 2 in registers.
+        load_b(0);
+        store_b(Int<0>{});
+        if (nst > 1) load_b(1);
+        __syncthreads();
+        realign(Int<0>{});
+        if (nst > 1) store_b(Int<1>{});
+        if (nst > 2) load_b(2);
+        __syncthreads();
+        auto body = [&](auto par, uint32_t o) {
+            constexpr int S = decltype(par)::value;
+            if (o + 1 < nst) realign(Int<1 - S>{});
+            if (o + 2 < nst) store_b(Int<S>{});
+            // (no requests past the last stage: they would be HBM reads that
+            // the kernel's tail waits behind)
+            if (o + 3 < nst) load_b(o + 3);
+            __syncthreads();
+        };
+        for (uint32_t o = 0; o < nst; o += 2) {
+            body(Int<0>{}, o);
+            body(Int<1>{}, o + 1);
+        }
     }
 
-    // The odd-step wavefronts hand their sums to the even-step ones, which
-    // put the tile in LDS (f32, [row][column]; the stage buffers are free
-    // after the loop's last barrier); then all threads store it as rows of
-    // 4-column chunks -- contiguous 8- or 16-byte stores instead of one
-    // 2-byte store per accumulator.
-    float *red = reinterpret_cast<float *>(lds);
-    float *ot = reinterpret_cast<float *>(lds + P::RED);
+    // The MFMA wavefronts put the tile in LDS (f32, [row][column]; the stage
+    // buffers are free after the loop's last barrier); then all threads
+    // store it as rows of 8- or 4-column chunks -- contiguous 16- or 8-byte
+    // stores instead of one 2-byte store per accumulator.
+    float *ot = reinterpret_cast<float *>(lds);
     constexpr int OROW = P::OROW;  // floats per LDS row (pad: rows 4 banks apart)
-    if (kw == 1) {
-#pragma unroll
-        for (int j = 0; j < CT; j++)
-#pragma unroll
-            for (int v = 0; v < 16; v++) red[((w4 * CT + j) * 16 + v) * 64 + lane] = acc[j][v];
-    }
-    __syncthreads();
-    if (kw == 0) {
+    if (mfma_wave) {
 #pragma unroll
         for (int j = 0; j < CT; j++)
 #pragma unroll
             for (int v = 0; v < 16; v++)
-                ot[(wm * 32 + 8 * (v / 4) + 4 * part + (v % 4)) * OROW + wcol + j * 32 + c] =
-                    acc[j][v] + red[((w4 * CT + j) * 16 + v) * 64 + lane];
+                ot[(wave * 32 + 8 * (v / 4) + 4 * part + (v % 4)) * OROW + j * 32 + c] = acc[j][v];
     }
     __syncthreads();
     const uint32_t rows = min((uint32_t)P::BM, a.m - min(a.m, by * P::BM));
@@ -464,19 +495,15 @@ __global__ __launch_bounds__(512) void mx_matmul_kernel(KPRE_PARAMS, MxArgs a) {
     }
 }
 
-// Tile plan of one call: wavefronts along the activation rows (WM) and
-// column tiles per wavefront (CTW); 128 x 96 is the one that fits LDS with
-// both buffer pairs (192 columns would need 219 KB).
+// Tile plan of one call: 128 x 96 (three column tiles per MFMA wavefront)
+// is the one that fits LDS with both buffer pairs (192 columns would need
+// 219 KB).
 struct MxTilePlan {
-    int wm, ctw;
     uint32_t col_tiles, groups;
 };
 static MxTilePlan mx_plan(uint32_t m, uint32_t n) {
-    const int wm = 4, ctw = 3;  // 128 x 96: 240 workgroups at 512 x 5760
-    MxTilePlan p;
-    p.wm = wm;
-    p.ctw = ctw;
-    const uint32_t bn = 32 * ctw * (4 / wm), bm = 32 * wm;
+    MxTilePlan p;  // 128 x 96: 240 workgroups at 512 x 5760
+    const uint32_t bn = MxPlan<3>::BN, bm = MxPlan<3>::BM;
     p.col_tiles = (n + bn - 1) / bn;
     p.groups = (m + bm - 1) / bm;
     return p;
@@ -484,36 +511,42 @@ static MxTilePlan mx_plan(uint32_t m, uint32_t n) {
 
 uint64_t mx_workspace_bytes(uint32_t m, uint32_t n, uint32_t k) {
     (void)n;
-    return (uint64_t)((m + 31) / 32) * ((k + 63) / 64) * MX_REC;
+    const uint64_t tiles = (m + 31) / 32, stages = ((k + 63) / 64 + MX_STAGE - 1) / MX_STAGE;
+    return tiles * stages * (MX_STAGE * MX_REC + MX_SREC);
 }
 
-template <int WM, int CTW>
+template <int CT>
 static MxFn mx_kernel_fn(size_t &lds) {
-    lds = (size_t)MxPlan<WM, CTW>::LDS;
-    return mx_matmul_kernel<WM, CTW>;
+    lds = (size_t)MxPlan<CT>::LDS;
+    return mx_matmul_kernel<CT>;
 }
 
 int mx_matmul_launch(const void *w, const void *x, void *y, bool y_bf16, const float *bias, uint32_t m, uint32_t n,
                      uint32_t k, void *workspace, hipStream_t stream) {
     const uint32_t ksteps = (k + 63) / 64, tiles = (m + 31) / 32;
+    const uint32_t kpad = (ksteps + MX_STAGE - 1) / MX_STAGE * MX_STAGE;
     const MxTilePlan plan = mx_plan(m, n);
+    uint8_t *const frag = (uint8_t *)workspace, *const scl = frag + (uint64_t)tiles * kpad * MX_REC;
     MxSplitArgs sa;
     sa.x = (const uint16_t *)x;
-    sa.frag = (uint8_t *)workspace;
+    sa.frag = frag;
+    sa.scl = scl;
     sa.m = m;
     sa.k = k;
-    sa.ksteps = ksteps;
-    sa.records = tiles * ksteps;
+    sa.kpad = kpad;
+    sa.records = tiles * kpad;
     hipLaunchKernelGGL(mx_split_kernel, dim3(sa.records), dim3(64), 0, stream, KPRE_ARGS(sa), sa);
     OCO_TRY(launch_check("oco_matmul (mx split)"));
     size_t lds = 0;
-    MxFn fn = mx_kernel_fn<4, 3>(lds);
+    MxFn fn = mx_kernel_fn<3>(lds);
     if (lds > 64 * 1024)
         OCO_TRY(hip_check(hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
                           "hipFuncSetAttribute"));
     MxArgs a;
     a.w = (const uint8_t *)w;
-    a.frag = (const uint8_t *)workspace;
+    a.frag = frag;
+    a.scl = scl;
+    a.kpad = kpad;
     a.y = y;
     a.bias = bias;
     a.m = m;
@@ -530,7 +563,7 @@ int mx_matmul_launch(const void *w, const void *x, void *y, bool y_bf16, const f
         return fail(OCO_ERR_UNSUPPORTED, "oco_matmul: MXFP4 weight of %llu bytes (4 GiB limit)",
                     (unsigned long long)wspan);
     a.wspan = (uint32_t)wspan;
-    hipLaunchKernelGGL(fn, dim3(plan.col_tiles, plan.groups), dim3(MxPlan<4, 3>::NTH), lds, stream, KPRE_ARGS(a), a);
+    hipLaunchKernelGGL(fn, dim3(plan.col_tiles, plan.groups), dim3(MxPlan<3>::NTH), lds, stream, KPRE_ARGS(a), a);
     return launch_check("oco_matmul (mx)");
 }
 
