@@ -207,6 +207,18 @@ int oco_matvec(uint32_t format, const void *w, const void *x, oco_dtype x_dtype,
                oco_dtype y_dtype, const float *bias, const uint32_t *ids, const oco_matrix *p,
                oco_stream stream);
 
+/* oco_matvec with relu^2 applied to every input element on load:
+ * x -> max(x, 0)^2 in f32 (a NaN element reads as 0), before the dot
+ * products.  Replaces the vector kernels specialised with `input_relu_sqr`
+ * (shaders/matrix/weights.metal:22-24, vector.metal:120-123, 185-190,
+ * q8-dot.metal:12-15, 59-64) as Builder::vector_kernel(kind, output,
+ * relu_sqr = true, ..) builds them (src/weights/pipelines.rs:227-254) for
+ * Nemotron's relu^2 feed-forward down projection (nemotron/load.rs:408).
+ * Same arguments and rules as oco_matvec. */
+int oco_matvec_relu_sqr(uint32_t format, const void *w, const void *x, oco_dtype x_dtype, void *y,
+                        oco_dtype y_dtype, const float *bias, const uint32_t *ids, const oco_matrix *p,
+                        oco_stream stream);
+
 /* ---- prefill matmul ----------------------------------------------------- */
 
 /* Y[m, n] = X[m, k] W^T (+ bias) on MFMA with fp32 accumulation.

@@ -157,6 +157,7 @@ SIGNATURES = {
     "oco_dequant": (_i32, [_u32, _vp, _u64, _vp, _vp]),
     "oco_embed": (_i32, [_u32, _vp, _u32, _u32, _vp, _u32, _vp, _u32, _vp, _vp]),
     "oco_matvec": (_i32, [_u32, _vp, _vp, _i32, _vp, _i32, _vp, _vp, _MP, _vp]),
+    "oco_matvec_relu_sqr": (_i32, [_u32, _vp, _vp, _i32, _vp, _i32, _vp, _vp, _MP, _vp]),
     "oco_matmul": (_i32, [_u32, _vp, _vp, _i32, _vp, _i32, _vp, _MP, _vp]),
     "oco_matmul_workspace": (_u64, [_u32, _i32, _MP]),
     "oco_matmul_ws": (_i32, [_u32, _vp, _vp, _i32, _vp, _i32, _vp, _MP, _vp, _u64, _vp]),
@@ -428,10 +429,12 @@ class Embedding:
 
 
 def matvec(fmt: int, w, x, y, p: Matrix, x_dtype=DType.F32, y_dtype=DType.F32, bias=None,
-           ids=None, stream=None):
-    _check(load_library().oco_matvec(int(fmt), _addr(w), _addr(x), int(x_dtype), _addr(y),
-                                     int(y_dtype), _addr(bias), _addr(ids), ctypes.byref(as_matrix(p)),
-                                     _stream(stream)))
+           ids=None, stream=None, relu_sqr: bool = False):
+    """oco_matvec, or oco_matvec_relu_sqr (x -> max(x, 0)^2 on load) when relu_sqr."""
+    lib = load_library()
+    fn = lib.oco_matvec_relu_sqr if relu_sqr else lib.oco_matvec
+    _check(fn(int(fmt), _addr(w), _addr(x), int(x_dtype), _addr(y), int(y_dtype), _addr(bias), _addr(ids),
+              ctypes.byref(as_matrix(p)), _stream(stream)))
 
 
 def matmul(fmt: int, w, x, y, p: Matrix, x_dtype=DType.BF16, y_dtype=DType.F32, bias=None,

@@ -216,12 +216,20 @@ struct bf16_t {
 
 template <typename XT>
 struct XLoad;
+// The relu² input transform of the vector kernels (weights.metal:22-24,
+// vector.metal:120-123): the positive part of x, squared in f32.  max
+// returns its non-NaN operand, so NaN inputs become 0, as Metal's max does.
+__device__ __forceinline__ float relu_sqr(float v) {
+    const float r = fmaxf(v, 0.f);
+    return r * r;
+}
+
 template <>
 struct XLoad<float> {
     // n contiguous values starting at p (n multiple of 4, p 16-byte aligned
-    // whenever k is a multiple of 4).
+    // whenever k is a multiple of 4), squared positive parts when rs.
     template <int N>
-    __device__ __forceinline__ static void run(const float *p, float *out) {
+    __device__ __forceinline__ static void run(const float *p, float *out, bool rs = false) {
 #pragma unroll
         for (int i = 0; i < N; i += 4) {
             float4 v = *reinterpret_cast<const float4 *>(p + i);
@@ -230,13 +238,17 @@ struct XLoad<float> {
             out[i + 2] = v.z;
             out[i + 3] = v.w;
         }
+        if (rs) {
+#pragma unroll
+            for (int i = 0; i < N; i++) out[i] = relu_sqr(out[i]);
+        }
     }
     __device__ __forceinline__ static float one(const float *p, uint64_t i) { return p[i]; }
 };
 template <>
 struct XLoad<bf16_t> {
     template <int N>
-    __device__ __forceinline__ static void run(const bf16_t *p, float *out) {
+    __device__ __forceinline__ static void run(const bf16_t *p, float *out, bool rs = false) {
 #pragma unroll
         for (int i = 0; i < N; i += 8) {
             uint4 v = *reinterpret_cast<const uint4 *>(p + i);
@@ -246,6 +258,10 @@ struct XLoad<bf16_t> {
                 out[i + 2 * j] = __uint_as_float(w[j] << 16);
                 out[i + 2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
             }
+        }
+        if (rs) {
+#pragma unroll
+            for (int i = 0; i < N; i++) out[i] = relu_sqr(out[i]);
         }
     }
     __device__ __forceinline__ static float one(const bf16_t *p, uint64_t i) {

@@ -103,8 +103,8 @@ struct Piece<OCO_Q8_0> {
         float v[8];
     };
     template <typename XT>
-    __device__ __forceinline__ static void load_x(const XT *xr, uint32_t block, int piece, X &x) {
-        XLoad<XT>::template run<8>(xr + block * 32 + piece * 8, x.v);
+    __device__ __forceinline__ static void load_x(const XT *xr, uint32_t block, int piece, X &x, bool rs = false) {
+        XLoad<XT>::template run<8>(xr + block * 32 + piece * 8, x.v, rs);
     }
     __device__ __forceinline__ static float dot(const WSrc &w, uint32_t b, int piece, const X &x) {
         uint2 q = w.u64(b + 2 + piece * 8);
@@ -133,9 +133,9 @@ struct Piece<OCO_MXFP4> {
         float lo[8], hi[8];
     };
     template <typename XT>
-    __device__ __forceinline__ static void load_x(const XT *xr, uint32_t block, int piece, X &x) {
-        XLoad<XT>::template run<8>(xr + block * 32 + piece * 8, x.lo);
-        XLoad<XT>::template run<8>(xr + block * 32 + 16 + piece * 8, x.hi);
+    __device__ __forceinline__ static void load_x(const XT *xr, uint32_t block, int piece, X &x, bool rs = false) {
+        XLoad<XT>::template run<8>(xr + block * 32 + piece * 8, x.lo, rs);
+        XLoad<XT>::template run<8>(xr + block * 32 + 16 + piece * 8, x.hi, rs);
     }
     template <int I>
     __device__ __forceinline__ static void pair(uint32_t w, const X &x, int base, float &s0, float &s1) {
@@ -173,10 +173,10 @@ struct KQuant4 {
         float sum_lo, sum_hi;
     };
     template <typename XT>
-    __device__ __forceinline__ static void load_x(const XT *xr, uint32_t block, int piece, X &x) {
+    __device__ __forceinline__ static void load_x(const XT *xr, uint32_t block, int piece, X &x, bool rs = false) {
         int g = piece >> 1, l0 = (piece & 1) * 16;
-        XLoad<XT>::template run<16>(xr + block * 256 + g * 64 + l0, x.lo);
-        XLoad<XT>::template run<16>(xr + block * 256 + g * 64 + 32 + l0, x.hi);
+        XLoad<XT>::template run<16>(xr + block * 256 + g * 64 + l0, x.lo, rs);
+        XLoad<XT>::template run<16>(xr + block * 256 + g * 64 + 32 + l0, x.hi, rs);
         float a = 0.f, c = 0.f;
 #pragma unroll
         for (int i = 0; i < 16; i++) {
@@ -270,11 +270,11 @@ struct Piece<OCO_Q6_K> {
         float sum[4];
     };
     template <typename XT>
-    __device__ __forceinline__ static void load_x(const XT *xr, uint32_t block, int piece, X &x) {
+    __device__ __forceinline__ static void load_x(const XT *xr, uint32_t block, int piece, X &x, bool rs = false) {
         int h = piece >> 2, l0 = (piece & 3) * 8;
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-            XLoad<XT>::template run<8>(xr + block * 256 + h * 128 + q * 32 + l0, x.v[q]);
+            XLoad<XT>::template run<8>(xr + block * 256 + h * 128 + q * 32 + l0, x.v[q], rs);
             x.sum[q] = ((x.v[q][0] + x.v[q][1]) + (x.v[q][2] + x.v[q][3])) +
                        ((x.v[q][4] + x.v[q][5]) + (x.v[q][6] + x.v[q][7]));
         }
@@ -318,9 +318,9 @@ struct Q4Legacy {
         float sum;
     };
     template <typename XT>
-    __device__ __forceinline__ static void load_x(const XT *xr, uint32_t block, int piece, X &x) {
-        XLoad<XT>::template run<8>(xr + block * 32 + piece * 8, x.lo);
-        XLoad<XT>::template run<8>(xr + block * 32 + 16 + piece * 8, x.hi);
+    __device__ __forceinline__ static void load_x(const XT *xr, uint32_t block, int piece, X &x, bool rs = false) {
+        XLoad<XT>::template run<8>(xr + block * 32 + piece * 8, x.lo, rs);
+        XLoad<XT>::template run<8>(xr + block * 32 + 16 + piece * 8, x.hi, rs);
         float s = 0.f;
 #pragma unroll
         for (int i = 0; i < 8; i++) s += x.lo[i] + x.hi[i];
@@ -358,8 +358,8 @@ struct Plain {
         float v[E];
     };
     template <typename XT>
-    __device__ __forceinline__ static void load_x(const XT *xr, uint32_t block, int, X &x) {
-        XLoad<XT>::template run<E>(xr + block * E, x.v);
+    __device__ __forceinline__ static void load_x(const XT *xr, uint32_t block, int, X &x, bool rs = false) {
+        XLoad<XT>::template run<E>(xr + block * E, x.v, rs);
     }
     __device__ __forceinline__ static float dot(const WSrc &w, uint32_t b, int, const X &x) {
         uint4 q = w.u128(b);

@@ -31,6 +31,7 @@ struct MatvecArgs {
     oco_matrix p;
     uint64_t row_bytes;
     int y_bf16;
+    int relu_sqr;  // relu² of x on load
 };
 
 template <int FMT, typename XT, int R, int KS>
@@ -65,7 +66,7 @@ __global__ __launch_bounds__(256) void matvec_kernel(MatvecArgs a) {
 #pragma unroll 2
     for (uint32_t b = (uint32_t)split * BPS + lane / F::P; b < blocks; b += BPS * KS) {
         typename F::X xv;
-        F::load_x(xr, b, piece, xv);
+        F::load_x(xr, b, piece, xv, a.relu_sqr != 0);
 #pragma unroll
         for (int r = 0; r < R; r++) acc[r] += F::dot(src, r * rb + b * F::BYTES, piece, xv);
     }
@@ -236,8 +237,10 @@ StreamFn stream_pick_group(bool x_bf16, uint32_t fmt, int xs, int npl, bool dire
 // without a streaming kernel normalise into a stream-ordered temporary first.
 static int matvec_impl(uint32_t format, const void *w, const void *x, oco_dtype x_dtype, void *y,
                        oco_dtype y_dtype, const float *bias, const uint32_t *ids, const oco_matrix *p,
-                       const NormSpec *norm, oco_stream stream, const GroupSpec *grp = nullptr) {
+                       const NormSpec *norm, oco_stream stream, const GroupSpec *grp = nullptr,
+                       bool relu_sqr = false) {
     if (!p || !w || !x || !y) return fail(OCO_ERR_INVALID, "oco_matvec: null argument");
+    if (relu_sqr && (norm || grp)) return fail(OCO_ERR_INVALID, "oco_matvec: relu_sqr takes neither a norm nor a group");
     uint32_t e, bb;
     OCO_TRY(oco_block_layout(format, &e, &bb));
     uint32_t align = e;
@@ -350,7 +353,7 @@ static int matvec_impl(uint32_t format, const void *w, const void *x, oco_dtype 
                                   "hipFuncSetAttribute"));
             const uint32_t grid = std::min<uint32_t>(a.ngroups * nmat, (uint32_t)(cus * sp.wg_per_cu));
             if (a.p.routes > 0x7fffffffu) return fail(OCO_ERR_INVALID, "oco_matvec: routes=%u", a.p.routes);
-            const uint32_t mode = sp.ks == 4 ? 2u : sp.ks == 2 ? 1u : 0u;
+            const uint32_t mode = (sp.ks == 4 ? 2u : sp.ks == 2 ? 1u : 0u) | (relu_sqr ? 4u : 0u);
             hipLaunchKernelGGL(fn, dim3(grid, p->m), dim3(256), lds, (hipStream_t)stream, a.w, a.x,
                                (uint32_t)a.row_bytes, a.p.n, a.p.k, mode, a.slice_blocks, a.ngroups, a.p.experts,
                                a.p.routes | (a.p.route_major ? 0x80000000u : 0u), a);
@@ -388,6 +391,7 @@ static int matvec_impl(uint32_t format, const void *w, const void *x, oco_dtype 
     a.row_bytes = oco_row_bytes(format, p->k);
     // Routed, non-route-major outputs are always f32 (vector.metal:142-146).
     a.y_bf16 = (y_dtype == OCO_DT_BF16) && !(p->experts > 1 && !p->route_major);
+    a.relu_sqr = relu_sqr;
     uint32_t rows_per_group = (4 / plan.ks) * plan.r;
     dim3 grid((p->n + rows_per_group - 1) / rows_per_group, p->m);
     hipLaunchKernelGGL(fn, grid, dim3(256), 0, (hipStream_t)stream, a);
@@ -399,6 +403,12 @@ extern "C" int oco_matvec(uint32_t format, const void *w, const void *x, oco_dty
                           oco_dtype y_dtype, const float *bias, const uint32_t *ids,
                           const oco_matrix *p, oco_stream stream) {
     return matvec_impl(format, w, x, x_dtype, y, y_dtype, bias, ids, p, nullptr, stream);
+}
+
+extern "C" int oco_matvec_relu_sqr(uint32_t format, const void *w, const void *x, oco_dtype x_dtype, void *y,
+                                   oco_dtype y_dtype, const float *bias, const uint32_t *ids, const oco_matrix *p,
+                                   oco_stream stream) {
+    return matvec_impl(format, w, x, x_dtype, y, y_dtype, bias, ids, p, nullptr, stream, nullptr, true);
 }
 
 extern "C" int oco_matvec_norm(uint32_t format, const void *w, const void *x, const float *norm_w, float epsilon,

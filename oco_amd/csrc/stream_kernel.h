@@ -93,8 +93,9 @@ __global__ __launch_bounds__(256) void stream_kernel(const uint8_t *w_, const vo
     a.row_bytes = row_bytes_;
     a.p.n = n_;
     a.p.k = k_;
-    // mode_: bits 0-1 log2 of the K split
+    // mode_: bits 0-1 log2 of the K split, bit 2 relu² of x on load
     const uint32_t ks_log2 = mode_ & 3u;
+    const bool rs = (mode_ >> 2) & 1u;
     a.ks = 1u << ks_log2;
     a.slice_blocks = slice_;
     a.ngroups = ngroups_;
@@ -269,6 +270,10 @@ __global__ __launch_bounds__(256) void stream_kernel(const uint8_t *w_, const vo
                     xv[s][4 * t + 2] = __uint_as_float(q.y << 16); xv[s][4 * t + 3] = __uint_as_float(q.y & 0xffff0000u);
                 }
             }
+            if (rs) {
+#pragma unroll
+                for (int e = 0; e < 32; e++) xv[s][e] = relu_sqr(xv[s][e]);
+            }
         }
     }
 
@@ -326,6 +331,9 @@ __global__ __launch_bounds__(256) void stream_kernel(const uint8_t *w_, const vo
 #pragma unroll
                         for (int e = 0; e < 4; e++)
                             v[u][e] = bf16_bits_to_f32(norm_value_bits(v[u][e], inv, wn[e], XS == XS_NORM_FULL));
+                    } else if (rs) {
+#pragma unroll
+                        for (int e = 0; e < 4; e++) v[u][e] = relu_sqr(v[u][e]);
                     }
                     uint32_t pp, tt;
                     T::map(f, pp, tt);

@@ -110,6 +110,17 @@ def _x_dtype(x: np.ndarray) -> int:
     raise TypeError(x.dtype)
 
 
+def relu_sqr_input(x: np.ndarray) -> np.ndarray:
+    """The relu² input transform of the vector kernels, as f32: max(v, 0)
+    squared in f32 (weights.metal:22-24, vector.metal:120-123,
+    q8-dot.metal:12-15); x is f32 or bf16 bits.  A NaN element becomes 0
+    (fmax keeps the non-NaN operand)."""
+    v = bf16_to_f32(x) if x.dtype == np.uint16 else np.asarray(x, np.float32)
+    r = np.fmax(v, np.float32(0))
+    with np.errstate(over="ignore"):
+        return (r * r).astype(np.float32)
+
+
 def matvec_f64(fmt, w, x, p: Matrix, bias=None, ids=None, xdt=None):
     """fp64 y (routes*n) and magnitude sum|w x| + |b| per output."""
     w = np.ascontiguousarray(w, np.uint8)

@@ -64,7 +64,10 @@ def test_argument_validation_without_gpu():
     assert lib.oco_matmul(12, fake, fake, 1, fake, 0, None, ctypes.byref(p), None) == 1
     p = oco_amd.Matrix(2880, 5760, 512, 0, 1, 1, 0)
     need = lib.oco_matmul_workspace(39, 1, ctypes.byref(p))
-    assert need == (512 // 32) * (2880 // 64) * 3328  # per (32 rows, 64 k): two E2M3 terms of 24 B per lane + scales
+    # per 32 rows and stage of eight 64-wide K steps: two E2M3 terms of 24 B
+    # per lane and step, plus one 16-byte scale word per lane (K steps
+    # counted to whole stages: 45 -> 48)
+    assert need == (512 // 32) * ((2880 // 64 + 7) // 8) * (8 * 64 * 48 + 64 * 16)
     assert lib.oco_matmul_workspace(12, 1, ctypes.byref(p)) == 0
     assert lib.oco_matmul_ws(39, fake, fake, 1, fake, 0, None, ctypes.byref(p), fake, need - 1, None) == 1
     assert b"workspace" in lib.oco_last_error()

@@ -239,3 +239,74 @@ def _stream_plan_cases(lib, plan):
     bias = np.random.default_rng(14).normal(size=E * n).astype(np.float32)
     x = synth.activations(15, 2 * k).reshape(2, k)
     check_matvec(lib, P.Q6_K, data, x, O.Matrix(k, n, 4, 0, 2, E, 2), bias=bias, ids=ids)
+
+
+def _relu_sqr_cases(lib, tag):
+    from oco_amd import synth
+    cases = [(fmt, 129, 1024) for fmt in [P.F32, P.F16, P.BF16]] + \
+            [(O.MXFP4, 131, 2880), (P.Q8_0, 77, 4096), (P.Q4_K, 257, 2048), (P.Q6_K, 100, 4096),
+             (P.Q4_0, 90, 4096), (P.Q4_1, 65, 2048), (P.Q5_K, 130, 4096)]
+    for fmt, n, k in cases:
+        say("matvec relu_sqr", tag, fmt, n, k)
+        if fmt in (P.F32, P.F16, P.BF16):
+            wf = np.random.default_rng(21).normal(0, 0.02, n * k).astype(np.float32)
+            data = (wf if fmt == P.F32 else wf.astype(np.float16) if fmt == P.F16 else synth.bf16_bits(wf)).view(np.uint8)
+        else:
+            data = synth.weights(fmt, n, k, seed=21)
+        x = synth.activations(22, k)
+        x[::7] = np.nan  # NaN inputs read as 0
+        p = O.Matrix(k, n, 1, 0, 1, 1, 0)
+        xr = O.relu_sqr_input(x)
+        # The transform on load equals the plain matvec of the transformed
+        # input, bit for bit (same kernel, same f32 values, same order).
+        wbuf, wptr = upload_at_offset(lib, data, 0)
+        outs = []
+        for xin, rs in ((x, True), (xr, False)):
+            xb = lib.DeviceBuffer.from_array(xin)
+            y = Guarded(lib, n * 4)
+            lib.matvec(fmt, wptr, xb, y.ptr, p, lib.DType.F32, lib.DType.F32, relu_sqr=rs)
+            lib.synchronize()
+            outs.append(y.read(np.float32))
+        np.testing.assert_array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+        want, mag = O.matvec_f64(fmt, np.asarray(data, np.uint8), xr, p)
+        assert rel_l2(outs[0], want) <= 1e-5
+        assert np.all(np.abs(outs[0] - want) <= O.roundoff_bound(want, mag, k, False))
+        # bf16 activations, bf16 output: against the fp64 oracle of the
+        # transformed (f32) input.
+        xb16 = synth.bf16_bits(synth.activations(23, k))
+        xb = lib.DeviceBuffer.from_array(xb16)
+        y = Guarded(lib, n * 2)
+        lib.matvec(fmt, wptr, xb, y.ptr, p, lib.DType.BF16, lib.DType.BF16, relu_sqr=True)
+        lib.synchronize()
+        got = O.bf16_to_f32(y.read(np.uint16))
+        want, mag = O.matvec_f64(fmt, np.asarray(data, np.uint8), O.relu_sqr_input(xb16), p)
+        assert rel_l2(got, want) <= 4e-3
+        assert np.all(np.abs(got - want) <= O.roundoff_bound(want, mag, k, True))
+    # routed rows (the relu² experts' down projection): route-major Q4_0 bank
+    E, n, k = 4, 64, 1024
+    data = synth.weights(P.Q4_0, E * n, k, seed=24)
+    ids = np.array([2, 0, 3], np.uint32)
+    x = synth.activations(25, 3 * k)
+    p = O.Matrix(k, n, 3, 1, 1, E, 0)
+    got, _ = run_matvec(lib, P.Q4_0, data, O.relu_sqr_input(x), p, ids=ids)
+    wbuf, wptr = upload_at_offset(lib, data, 0)
+    xb, ib = lib.DeviceBuffer.from_array(x), lib.DeviceBuffer.from_array(ids)
+    y = Guarded(lib, 3 * n * 4)
+    lib.matvec(P.Q4_0, wptr, xb, y.ptr, p, lib.DType.F32, lib.DType.F32, ids=ib, relu_sqr=True)
+    lib.synchronize()
+    np.testing.assert_array_equal(y.read(np.float32).view(np.uint32), got.view(np.uint32))
+
+
+@pytest.mark.parametrize("path", ["default", "xreg", "plain"])
+def test_matvec_relu_sqr(lib, path):
+    """oco_matvec_relu_sqr (the input_relu_sqr specialisation): staged,
+    register-read and plain-kernel activations, every format, f32 and bf16
+    activations, routed rows."""
+    if path == "default":
+        _relu_sqr_cases(lib, path)
+    elif path == "xreg":
+        with lib.overridden(lib.Knob.STREAM_DIRECT, [0, 1]):
+            _relu_sqr_cases(lib, path)
+    else:
+        with lib.overridden(lib.Knob.MATVEC_PLAIN, [1]):
+            _relu_sqr_cases(lib, path)

@@ -231,6 +231,19 @@ def test_matvec_oracle_against_numpy_fp64(fmt):
         assert np.all(np.abs(y32 - y64) <= bound)
 
 
+def test_relu_sqr_input_closed_form():
+    """max(x, 0)^2 in f32; NaN reads as 0 and -0 as 0; squares overflow to
+    Inf as f32 products do; bf16 bits are widened first."""
+    x = np.array([-2.0, -0.0, 0.0, 1.5, 3.0, np.nan, np.inf, -np.inf, 1e20, 2.0 ** -80], np.float32)
+    want = np.array([0, 0, 0, 2.25, 9, 0, np.inf, 0, np.inf, 0], np.float32)
+    got = O.relu_sqr_input(x)
+    assert got.dtype == np.float32
+    np.testing.assert_array_equal(got, want)
+    assert not np.any(np.signbit(got))
+    bits = np.array([0xBF80, 0x4000, 0x7FC0, 0x3F81], np.uint16)  # -1, 2, NaN, 1.0078125
+    np.testing.assert_array_equal(O.relu_sqr_input(bits), np.float32([0, 4, 0, np.float32(1.0078125) ** 2]))
+
+
 def test_matvec_linearity_and_bias_rules():
     k, n = 256, 5
     data, _ = P.dense_weights(P.Q4_K, n, k)
