@@ -340,8 +340,8 @@ int oco_experts_forward(const oco_experts *w, const float *router_w, const float
  * cannot allocate device memory -- code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc.  Its workspace is a
  * static device array of OCO_EXPERTS_SCRATCH_BYTES per GPU (held until the
- * process ends; gpt-oss-20b needs 2.2 MB of it at 16 tokens and fits up to
- * 62); calls whose oco_experts_workspace(w, tokens) exceeds it fail with
+ * process ends; gpt-oss-20b needs 2.3 MB of it at 16 tokens and fits up to
+ * 57); calls whose oco_experts_workspace(w, tokens) exceeds it fail with
  * OCO_ERR_INVALID.
  * Every call on one GPU shares that GPU's array: calls that overlap on one
  * GPU (two streams, two threads) race and must be ordered by the caller.

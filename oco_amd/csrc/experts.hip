@@ -488,7 +488,7 @@ static int experts_apply(const oco_experts *w, const void *x, oco_dtype x_dtype,
     const bool tiled = w->hidden % 32 == 0 && w->ffn % 32 == 0;
     if (tiled && w->format == OCO_MXFP4 && tokens >= mx_tokens) {
         // MXFP4 banks: block-scaled FP6 x FP4 MFMA on the GGUF bytes (no
-        // weight decode); activations split per row into three E2M3 terms.
+        // weight decode); activations split per row into four E2M3 terms.
         // Decode batches take 16-row tiles (half the staged activations).
         const uint32_t tile_rows = tokens <= 16 ? 16 : 32;
         // The input rows' split runs beside the router or the plan; the

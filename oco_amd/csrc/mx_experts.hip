@@ -6,7 +6,7 @@
 // stored and its E8M0 byte the B scale (the operand layout is described in
 // mxmatmul.hip).
 //
-// Activations come split per row into three E2M3 terms (mxsplit.h): the A
+// Activations come split per row into four E2M3 terms (mxsplit.h): the A
 // operand is FP6, which issues at the FP4 rate.
 #include "matmul.h"
 #include "mxsplit.h"
@@ -246,8 +246,10 @@ __global__ __launch_bounds__(64 * NW) void mx_experts_kernel(KPRE_PARAMS, Matmul
                             acc16[ct] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(avt, bv, acc16[ct], 2, 4, 0, (int)sa, 0, sb);
                         else if (t == 1)
                             acc16[ct] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(avt, bv, acc16[ct], 2, 4, 1, (int)sa, 0, sb);
-                        else
+                        else if (t == 2)
                             acc16[ct] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(avt, bv, acc16[ct], 2, 4, 2, (int)sa, 0, sb);
+                        else
+                            acc16[ct] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(avt, bv, acc16[ct], 2, 4, 3, (int)sa, 0, sb);
                     }
                 }
             }
@@ -290,8 +292,10 @@ __global__ __launch_bounds__(64 * NW) void mx_experts_kernel(KPRE_PARAMS, Matmul
                         acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(avt, bv, acc[j], 2, 4, 0, (int)sa, 0, sb);
                     else if (t == 1)
                         acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(avt, bv, acc[j], 2, 4, 1, (int)sa, 0, sb);
-                    else
+                    else if (t == 2)
                         acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(avt, bv, acc[j], 2, 4, 2, (int)sa, 0, sb);
+                    else
+                        acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(avt, bv, acc[j], 2, 4, 3, (int)sa, 0, sb);
                 }
             }
         }

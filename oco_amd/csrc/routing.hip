@@ -44,7 +44,7 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const XT *x, const f
 // 1024-column chunk (16-byte weight loads, all of a thread's loads issued
 // before its first FMA), partial sums over DPP and then LDS.  Needs hidden %
 // 4 == 0 and 16-byte (f32) or 8-byte (bf16) aligned rows.  Workgroups past
-// the logits' (`rec` set) split the rows into records of three E2M3 terms
+// the logits' (`rec` set) split the rows into records of four E2M3 terms
 // (mxsplit.h), one split item (row, K step, block) per thread.
 constexpr int ROUTER_TOKENS = 4;
 template <typename XT>

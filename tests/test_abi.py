@@ -74,14 +74,14 @@ def test_argument_validation_without_gpu():
     assert lib.oco_route_plan(fake, 64, 32, 8, 0, 0, fake, None) == 1  # tile_rows < 16
     assert lib.oco_moe_sum(fake, 0, fake, fake, 64, 2, 9, None) == 1  # at most 8 routes per token
     assert b"at most 8" in lib.oco_last_error()
-    # MXFP4 expert records: 160 bytes per (row, K step of 64) -- three E2M3
+    # MXFP4 expert records: 208 bytes per (row, K step of 64) -- four E2M3
     # terms of 24 bytes per block (two blocks) and the scale words, padded
     mx = oco_amd.ExpertsDesc(39, 2880, 2880, 32, 4, 0, 1, fake, fake, fake, None, None, None)
-    assert lib.oco_experts_workspace(ctypes.byref(mx), 16) > 16 * 45 * 160 + 64 * 45 * 160
+    assert lib.oco_experts_workspace(ctypes.byref(mx), 16) > 16 * 45 * 208 + 64 * 45 * 208
     # the allocation-free entry point takes what fits its 8 MiB array and
     # rejects more before any GPU work
-    assert lib.oco_experts_workspace(ctypes.byref(mx), 62) <= 8 << 20 < lib.oco_experts_workspace(ctypes.byref(mx), 63)
-    rc = lib.oco_experts_forward_static(ctypes.byref(mx), fake, None, fake, 0, 63, fake, fake, fake, None, None)
+    assert lib.oco_experts_workspace(ctypes.byref(mx), 57) <= 8 << 20 < lib.oco_experts_workspace(ctypes.byref(mx), 58)
+    rc = lib.oco_experts_forward_static(ctypes.byref(mx), fake, None, fake, 0, 58, fake, fake, fake, None, None)
     assert rc == 1 and b"scratch" in lib.oco_last_error()
 
 
