@@ -258,14 +258,23 @@ struct Tile<OCO_Q6_K> {
             s[q] = a;
         }
     }
+    // The piece's fields sit at offsets from the block that are multiples of
+    // 4 (ql, qh, d) or not (the scales): one aligned base and one shift
+    // serve the first group, with the lane's field offsets folded into two
+    // adds and the reads' immediate offsets.
     __device__ __forceinline__ static Raw load(const uint8_t *blk, int c) {
         const int h = c >> 2, l0 = (c & 3) * 8;
+        const uint32_t a = (uint32_t)(uintptr_t)blk & 3u;
+        const uint8_t *b = blk - a;
+        const uint32_t *q = reinterpret_cast<const uint32_t *>(b + h * 64 + l0);
+        const uint32_t *qh = reinterpret_cast<const uint32_t *>(b + 128 + h * 32 + l0);
+        const uint32_t *dp = reinterpret_cast<const uint32_t *>(b + 208);
         Raw r;
-        r.ql0 = lds_u64(blk + h * 64 + l0);
-        r.ql1 = lds_u64(blk + h * 64 + 32 + l0);
-        r.qh = lds_u64(blk + 128 + h * 32 + l0);
+        r.ql0 = make_uint2(__builtin_amdgcn_alignbyte(q[1], q[0], a), __builtin_amdgcn_alignbyte(q[2], q[1], a));
+        r.ql1 = make_uint2(__builtin_amdgcn_alignbyte(q[9], q[8], a), __builtin_amdgcn_alignbyte(q[10], q[9], a));
+        r.qh = make_uint2(__builtin_amdgcn_alignbyte(qh[1], qh[0], a), __builtin_amdgcn_alignbyte(qh[2], qh[1], a));
+        r.d = __builtin_amdgcn_alignbyte(dp[1], dp[0], a) & 0xffffu;
         r.sc = lds_u64(blk + 192 + h * 8 + (l0 >> 4));
-        r.d = lds_u16(blk + 208);
         return r;
     }
     __device__ __forceinline__ static float dot(const Raw &r, const float *x, const float *s, int) {
