@@ -422,6 +422,9 @@ WORKLOADS = {
     "moe_decode_gpt_oss_b4": lambda: MoeDecode(4),
     "moe_decode_gpt_oss_b16": lambda: MoeDecode(16),
     "prefill_mxfp4_5760x2880_m512": lambda: Prefill("prefill_mxfp4_5760x2880_m512", 39, 5760, 2880, 512),
+    "prefill_q4_k_12288x4096_m512": lambda: Prefill("prefill_q4_k_12288x4096_m512", 12, 12288, 4096, 512),
+    "prefill_q6_k_4096x12288_m512": lambda: Prefill("prefill_q6_k_4096x12288_m512", 14, 4096, 12288, 512),
+    "prefill_q8_0_4096x4096_m512": lambda: Prefill("prefill_q8_0_4096x4096_m512", 8, 4096, 4096, 512),
     "moe_prefill_qwen3_30b_a3b": MoePrefill,
     "lm_head_argmax_qwen3_8b": LmHeadArgmax,
     "argmax_f32_151936": Argmax,
@@ -577,6 +580,7 @@ def main():
         for name in ["q8_0_matvec_4096x4096", "q4_k_matvec_12288x4096", "q6_k_matvec_4096x12288",
                      "q6_k_lm_head_151936x4096", "qwen3_8b_q4km_decode_stack", "moe_decode_gpt_oss_b1",
                      "moe_decode_gpt_oss_b4", "moe_decode_gpt_oss_b16", "prefill_mxfp4_5760x2880_m512",
+                     "prefill_q4_k_12288x4096_m512", "prefill_q6_k_4096x12288_m512", "prefill_q8_0_4096x4096_m512",
                      "moe_prefill_qwen3_30b_a3b", "lm_head_argmax_qwen3_8b", "argmax_f32_151936",
                      "norm_up_gate_qwen3_8b_group", "norm_up_gate_qwen3_8b_fused",
                      "norm_up_gate_qwen3_8b_unfused", "read_floor_8812800"]:

@@ -104,7 +104,9 @@ typedef enum oco_knob {
     OCO_KNOB_MX_EXPERTS_KS = 10,  /* MXFP4 expert down tiles of 16 rows: K split (1|2) */
     OCO_KNOB_STREAM_DIRECT = 11,  /* value 0: Q4_K/Q5_K streaming matvec through the LDS tile even when aligned;
                                      second value (optional): activations 0 staged in LDS, 1 in registers */
-    OCO_KNOB_COUNT = 12
+    OCO_KNOB_MATMUL_VENDOR = 12,  /* f16-operand prefill: value 0 the fused f16 MFMA tiles, 1 the dequantize pass
+                                     and the vendor GEMM (default: the vendor GEMM from 32 activation rows) */
+    OCO_KNOB_COUNT = 13
 } oco_knob;
 int oco_plan_override(uint32_t knob, const int32_t *values, uint32_t count);
 

@@ -53,6 +53,7 @@ class Knob(enum.IntEnum):
     MOE_WG = 9
     MX_EXPERTS_KS = 10
     STREAM_DIRECT = 11
+    MATMUL_VENDOR = 12
 
 
 class DType(enum.IntEnum):

@@ -12,7 +12,12 @@
 //
 // Tile: a 256-thread workgroup computes 128 activation rows x 64 weight rows
 // with K steps of 128 (see matmul_kernel).
+#include <hipblaslt/hipblaslt.h>
 #include <stdlib.h>
+
+#include <map>
+#include <mutex>
+#include <tuple>
 
 #include "formats.h"
 #include "matmul.h"
@@ -65,25 +70,25 @@ struct PrefillPiece {
     static constexpr uint32_t BE = BlockShape<FMT>::BE, BB = BlockShape<FMT>::BB;
     struct Raw {
         uint32_t w[FMT == OCO_Q4_K || FMT == OCO_Q6_K ? 8 : FMT == OCO_MXFP4 ? 5 : 1];
-        const uint8_t *row;
+        gbytes row;
     };
-    __device__ __forceinline__ static Raw load(const uint8_t *row, uint32_t k0, int c) {
+    __device__ __forceinline__ static Raw load(gbytes row, uint32_t k0, int c) {
         Raw r;
         r.row = row;
         if constexpr (FMT == OCO_MXFP4 && BF) {
-            const uint8_t *b = row + (uint64_t)(k0 / 32 + c) * BB;
+            const gbytes b = row + (uint64_t)(k0 / 32 + c) * BB;
             const uint4 q = ld_u128(b + 1);
             r.w[0] = q.x; r.w[1] = q.y; r.w[2] = q.z; r.w[3] = q.w;
             r.w[4] = ld_u8(b);
         } else if constexpr (FMT == OCO_Q4_K) {
             const uint32_t cc = (k0 % 256) / 128 * 4 + c;
-            const uint8_t *b = row + (uint64_t)(k0 / 256) * BB;
+            const gbytes b = row + (uint64_t)(k0 / 256) * BB;
             const uint4 hdr = ld_u128(b), qs = ld_u128(b + 16 + 16 * cc);
             r.w[0] = hdr.x; r.w[1] = hdr.y; r.w[2] = hdr.z; r.w[3] = hdr.w;
             r.w[4] = qs.x; r.w[5] = qs.y; r.w[6] = qs.z; r.w[7] = qs.w;
         } else if constexpr (FMT == OCO_Q6_K) {
             const uint32_t hb = (k0 % 256) / 128, l0 = 8 * c;
-            const uint8_t *b = row + (uint64_t)(k0 / 256) * BB;
+            const gbytes b = row + (uint64_t)(k0 / 256) * BB;
             const uint2 ql0 = ld_u64(b + hb * 64 + l0), ql1 = ld_u64(b + hb * 64 + 32 + l0),
                         qh = ld_u64(b + 128 + hb * 32 + l0);
             r.w[0] = ql0.x; r.w[1] = ql0.y; r.w[2] = ql1.x; r.w[3] = ql1.y; r.w[4] = qh.x; r.w[5] = qh.y;
@@ -179,9 +184,9 @@ struct PrefillPiece {
 #pragma unroll
             for (int i = 0; i < 16; i++) {
                 const uint32_t col = kbase + 2 * i;
-                uint16_t v0 = operand_bits<BF>(decode_scalar(FMT, r.row + (uint64_t)(col / BE) * BB, col % BE));
+                uint16_t v0 = operand_bits<BF>(decode_scalar(FMT, (const uint8_t *)r.row + (uint64_t)(col / BE) * BB, col % BE));
                 uint16_t v1 =
-                    operand_bits<BF>(decode_scalar(FMT, r.row + (uint64_t)((col + 1) / BE) * BB, (col + 1) % BE));
+                    operand_bits<BF>(decode_scalar(FMT, (const uint8_t *)r.row + (uint64_t)((col + 1) / BE) * BB, (col + 1) % BE));
                 out[i] = pack2(v0, v1);
             }
 #pragma unroll
@@ -197,10 +202,10 @@ struct PrefillPiece {
 // other buffer, and the loads for step s+2 are in flight; one barrier per
 // step.  Weight piece p = tid + 256 u goes to row p % BN, piece p / BN, so a
 // wavefront's 64 lanes write 64 different rows (conflict-free LDS stores).
-template <int FMT, bool BF, int BM, int BN>
+template <int FMT, bool BF, int BM, int BN, int G>
 struct Stage {
     static constexpr int XPT = BM * 16 / 256, WPT = BN * 4 / 256;
-    uint4 x[XPT];
+    uint4 x[G == MM_DOWN ? 2 * XPT : XPT];  // down mode: eight f32 activations per chunk
     typename PrefillPiece<FMT, BF>::Raw w[WPT];
 };
 
@@ -216,7 +221,7 @@ template <int FMT, bool BF, int BM, int BN, int G = MM_DENSE>
 __global__ __launch_bounds__(256) void matmul_kernel(KPRE_PARAMS, MatmulArgs a) {
     KPRE_APPLY(a);
     using PP = PrefillPiece<FMT, BF>;
-    using ST = Stage<FMT, BF, BM, BN>;
+    using ST = Stage<FMT, BF, BM, BN, G>;
     constexpr int BK = 128, LD = BK + 8;  // LDS row stride: 136 halves (272 bytes, conflict-free fragments)
     constexpr int MI = BM / 32, NJ = BN / 32, XPT = ST::XPT, WPT = ST::WPT;
     constexpr int XS = BM * LD, WS = BN * LD;
@@ -260,8 +265,8 @@ __global__ __launch_bounds__(256) void matmul_kernel(KPRE_PARAMS, MatmulArgs a) 
 #pragma unroll
         for (int j = 0; j < NJ; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    const uint16_t *xg = reinterpret_cast<const uint16_t *>(a.x);
-    const uint8_t *wr[WPT];
+    const GLOBAL uint16_t *xg = gp(reinterpret_cast<const uint16_t *>(a.x));
+    gbytes wr[WPT];
     int wrow[WPT], wpc[WPT];
 #pragma unroll
     for (int u = 0; u < WPT; u++) {
@@ -272,16 +277,16 @@ __global__ __launch_bounds__(256) void matmul_kernel(KPRE_PARAMS, MatmulArgs a) 
             // LDS row q: column half h = q / (BN/2); its first BN/4 rows gate, the next BN/4 up
             const int q = wrow[u], h = q / (BN / 2), rr = q % (BN / 2);
             const uint32_t col = n0 + h * (BN / 4) + rr % (BN / 4);
-            const uint8_t *base = (rr < BN / 4 ? a.w : a.w2) + expert * a.expert_bytes;
+            const gbytes base = gp(rr < BN / 4 ? a.w : a.w2) + expert * a.expert_bytes;
             wr[u] = base + (uint64_t)min(col, a.n - 1) * a.row_bytes;
         } else {
-            wr[u] = a.w + expert * a.expert_bytes + (uint64_t)min(n0 + wrow[u], a.n - 1) * a.row_bytes;
+            wr[u] = gp(a.w) + expert * a.expert_bytes + (uint64_t)min(n0 + wrow[u], a.n - 1) * a.row_bytes;
         }
     }
     // Activation row of each X chunk this thread stages (fixed over K).  In
     // down mode the rows are f32 activations, scaled by a power of two
     // (row_gain) into f16 range; the epilogue divides it back out exactly.
-    const uint16_t *xrow[XPT];
+    const GLOBAL uint16_t *xrow[XPT];
     bool xlive[XPT];
     float xgain[G == MM_DOWN ? XPT : 1];
 #pragma unroll
@@ -293,37 +298,35 @@ __global__ __launch_bounds__(256) void matmul_kernel(KPRE_PARAMS, MatmulArgs a) 
         xlive[i] = (uint32_t)r < rows && (G != MM_DENSE || m0 + r < a.m);
         const uint32_t row = xlive[i] ? src : 0;
         if constexpr (G == MM_DOWN) {
-            xrow[i] = reinterpret_cast<const uint16_t *>(reinterpret_cast<const float *>(a.x) + (uint64_t)row * a.k);
+            xrow[i] = reinterpret_cast<const GLOBAL uint16_t *>(gp(reinterpret_cast<const float *>(a.x)) + (uint64_t)row * a.k);
             xgain[i] = row_gain(a.rowmax[row]);
         } else {
             xrow[i] = xg + (uint64_t)row * a.k;
         }
     }
 
+    // Loads are unconditional (addresses clamped into the operands; what lies
+    // past k is zeroed when the step is stored), so the compiler can count
+    // them: with a branch around them it waits for every load in flight
+    // before each step.
     auto load = [&](ST &st, uint32_t k0) {
 #pragma unroll
         for (int i = 0; i < XPT; i++) {
-            const int chunk = tid + 256 * i, cc = (chunk & 15) * 8;
+            const int chunk = tid + 256 * i;
+            const uint32_t kc = min(k0 + (chunk & 15) * 8, a.k - 8);
             if constexpr (G == MM_DOWN) {
-                uint4 v = make_uint4(0, 0, 0, 0);
-                if (xlive[i] && k0 + cc < a.k) {
-                    const float4 *src = reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(xrow[i]) + k0 + cc);
-                    const float4 p = src[0], q = src[1];
-                    const float g = xgain[i];
-                    v = make_uint4(pack2(operand_bits<false>(p.x * g), operand_bits<false>(p.y * g)),
-                                   pack2(operand_bits<false>(p.z * g), operand_bits<false>(p.w * g)),
-                                   pack2(operand_bits<false>(q.x * g), operand_bits<false>(q.y * g)),
-                                   pack2(operand_bits<false>(q.z * g), operand_bits<false>(q.w * g)));
-                }
-                st.x[i] = v;
+                const gbytes src = reinterpret_cast<gbytes>(reinterpret_cast<const GLOBAL float *>(xrow[i]) + kc);
+                st.x[2 * i] = ld_u128(src);
+                st.x[2 * i + 1] = ld_u128(src + 16);
             } else {
-                st.x[i] = xlive[i] && k0 + cc < a.k ? *reinterpret_cast<const uint4 *>(xrow[i] + k0 + cc)
-                                                    : make_uint4(0, 0, 0, 0);
+                st.x[i] = ld_u128(reinterpret_cast<gbytes>(xrow[i] + kc));
             }
         }
 #pragma unroll
-        for (int u = 0; u < WPT; u++)  // 32-block formats: the last step may cover a partial 128
-            if (k0 + 32 * wpc[u] < a.k) st.w[u] = PP::load(wr[u], k0, wpc[u]);
+        for (int u = 0; u < WPT; u++) {  // 32-block formats: the last step may cover a partial 128
+            const bool ok = k0 + 32 * wpc[u] < a.k;
+            st.w[u] = PP::load(wr[u], ok ? k0 : 0, ok ? wpc[u] : 0);
+        }
     };
     auto store = [&](const ST &st, uint32_t k0, int buf) {
         uint16_t *xs = lds + buf * XS;
@@ -331,8 +334,22 @@ __global__ __launch_bounds__(256) void matmul_kernel(KPRE_PARAMS, MatmulArgs a) 
 #pragma unroll
         for (int i = 0; i < XPT; i++) {
             const int chunk = tid + 256 * i, r = chunk >> 4, cc = (chunk & 15) * 8;
-            uint4 v = st.x[i];
-            if (!BF && !a.x_f16) {  // bf16 activations -> f16 operands
+            const bool ok = xlive[i] && k0 + cc < a.k;
+            uint4 v;
+            if constexpr (G == MM_DOWN) {
+                float f[8];
+                __builtin_memcpy(f, &st.x[2 * i], 16);
+                __builtin_memcpy(f + 4, &st.x[2 * i + 1], 16);
+                const float g = xgain[i];
+                v = make_uint4(pack2(operand_bits<false>(f[0] * g), operand_bits<false>(f[1] * g)),
+                               pack2(operand_bits<false>(f[2] * g), operand_bits<false>(f[3] * g)),
+                               pack2(operand_bits<false>(f[4] * g), operand_bits<false>(f[5] * g)),
+                               pack2(operand_bits<false>(f[6] * g), operand_bits<false>(f[7] * g)));
+            } else {
+                v = st.x[i];
+            }
+            if (!ok) v = make_uint4(0, 0, 0, 0);
+            if (G != MM_DOWN && !BF && !a.x_f16) {  // bf16 activations -> f16 operands
                 uint32_t w4[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
                 for (int j = 0; j < 4; j++)
@@ -389,29 +406,27 @@ __global__ __launch_bounds__(256) void matmul_kernel(KPRE_PARAMS, MatmulArgs a) 
         }
     };
 
-    // Prologue: step 0 in LDS buffer 0, step 1 in registers (s1), step 2 loading (s0).
+    // Prologue: step 0 in LDS buffer 0, step 1 in registers (s1), step 2
+    // loading (s0).  Steps run in pairs, every one unconditionally: a step
+    // past k stores zeros (its MFMAs add nothing), and loads past the last
+    // step re-read it (never stored).
     ST s0, s1;
+    const uint32_t steps = (a.k + BK - 1) / BK, last = (steps - 1) * BK;
     load(s0, 0);
-    if (BK < a.k) load(s1, BK);
+    load(s1, min(BK, last));
     store(s0, 0, 0);
-    if (2 * BK < a.k) load(s0, 2 * BK);
+    load(s0, min(2 * BK, last));
     __syncthreads();
-    const uint32_t steps = (a.k + BK - 1) / BK;
     for (uint32_t s = 0; s < steps; s += 2) {
         // even step s: compute buffer 0, stage step s+1 (s1) into buffer 1, prefetch s+3 into s1
         mfma_step(0);
-        if (s + 1 < steps) {
-            store(s1, (s + 1) * BK, 1);
-            if (s + 3 < steps) load(s1, (s + 3) * BK);
-        }
+        store(s1, (s + 1) * BK, 1);
+        load(s1, min((s + 3) * BK, last));
         __syncthreads();
-        if (s + 1 >= steps) break;
         // odd step s+1: compute buffer 1, stage step s+2 (s0) into buffer 0, prefetch s+4 into s0
         mfma_step(1);
-        if (s + 2 < steps) {
-            store(s0, (s + 2) * BK, 0);
-            if (s + 4 < steps) load(s0, (s + 4) * BK);
-        }
+        store(s0, (s + 2) * BK, 0);
+        load(s0, min((s + 4) * BK, last));
         __syncthreads();
     }
     // C fragment: lane l holds column l % 16, rows 4 (l / 16) .. + 4.
@@ -542,6 +557,212 @@ int grouped_matmul_launch(int mode, uint32_t fmt, const MatmulArgs &a, uint32_t 
     return launch_check("experts grouped matmul");
 }
 
+// ---- Dense prefill as a dequantize pass and a vendor GEMM --------------------
+// At prefill sizes the fused tiles above decode every weight once per row
+// tile and convert every activation once per column tile, on one wavefront
+// per SIMD; the decode alone is about a third of their time.  Here each
+// weight is decoded once, into the same f16 operand bits the fused tiles put
+// in LDS (PrefillPiece::decode, the reference's half(w)), the bf16
+// activations convert once to f16 (as the fused tiles convert them), and the
+// product is a plain f16 GEMM with fp32 accumulation on hipBLASLt.  Its
+// fp32 result then takes the fused tiles' epilogue: + bf16-rounded bias,
+// then f32 or bf16 (weights.metal:24-33).
+
+// Grid: weight blocks first (one thread per 32-coefficient piece of a
+// 128-wide K step, consecutive threads along a row), then activation blocks
+// (eight values per thread).
+template <int FMT>
+__global__ __launch_bounds__(256) void operand_kernel(const uint8_t *w, uint64_t row_bytes, uint32_t n, uint32_t k,
+                                                      uint16_t *wo, const uint16_t *x, uint16_t *xo, uint64_t xchunks,
+                                                      uint32_t wblocks) {
+    if (blockIdx.x >= wblocks) {
+        const uint64_t i = (uint64_t)(blockIdx.x - wblocks) * 256 + threadIdx.x;
+        if (i >= xchunks) return;
+        const uint4 v = *reinterpret_cast<const uint4 *>(x + 8 * i);
+        uint32_t h[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            h[j] = pack2(operand_bits<false>(bf16_bits_to_f32(h[j] & 0xffffu)),
+                         operand_bits<false>(bf16_bits_to_f32(h[j] >> 16)));
+        *reinterpret_cast<uint4 *>(xo + 8 * i) = make_uint4(h[0], h[1], h[2], h[3]);
+        return;
+    }
+    using PP = PrefillPiece<FMT, false>;
+    const uint32_t steps = (k + 127) / 128;
+    const uint64_t p = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (p >= (uint64_t)n * steps * 4) return;
+    const uint32_t row = (uint32_t)(p / (steps * 4)), rem = (uint32_t)(p % (steps * 4));
+    const uint32_t k0 = rem / 4 * 128, c = rem % 4;
+    if (k0 + 32 * c >= k) return;  // 32-block formats: the last step may be partial
+    const typename PP::Raw r = PP::load(gp(w) + (uint64_t)row * row_bytes, k0, c);
+    uint32_t out[16], col0[4];
+    PP::decode(r, k0, c, out, col0);
+    uint16_t *dst = wo + (uint64_t)row * k + k0;
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+        *reinterpret_cast<uint4 *>(dst + col0[q]) = make_uint4(out[4 * q], out[4 * q + 1], out[4 * q + 2], out[4 * q + 3]);
+}
+
+// y[m, n] = acc + bf16(bias), as f32 or bf16: four columns per thread.
+__global__ __launch_bounds__(256) void gemm_epilogue_kernel(const float *acc, const float *bias, void *y, bool y_bf16,
+                                                            uint32_t n, uint64_t quads) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= quads) return;
+    const uint32_t col = (uint32_t)(4 * i % n);
+    const float4 v = *reinterpret_cast<const float4 *>(acc + 4 * i);
+    float r[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; j++) r[j] += bias ? round_bf16(bias[col + j]) : 0.f;
+    if (y_bf16)
+        *reinterpret_cast<uint2 *>(reinterpret_cast<uint16_t *>(y) + 4 * i) =
+            make_uint2(pack2(f32_to_bf16_bits(r[0]), f32_to_bf16_bits(r[1])),
+                       pack2(f32_to_bf16_bits(r[2]), f32_to_bf16_bits(r[3])));
+    else
+        *reinterpret_cast<float4 *>(reinterpret_cast<float *>(y) + 4 * i) = make_float4(r[0], r[1], r[2], r[3]);
+}
+
+// One GEMM shape's hipBLASLt objects, built once per (device, m, n, k): D
+// [n rows of m, column-major] = W^T X with W the f16 operands as k x n
+// column-major (the weight rows as stored) and X as k x m.
+struct BlasPlan {
+    hipblasLtHandle_t handle = nullptr;
+    hipblasLtMatmulDesc_t desc = nullptr;
+    hipblasLtMatrixLayout_t a = nullptr, b = nullptr, d = nullptr;
+    hipblasLtMatmulAlgo_t algo;
+    uint64_t ws = 0;
+    bool ok = false;
+};
+constexpr uint64_t BLAS_WS_MAX = 32ull << 20;
+static std::mutex g_blas_lock;
+static std::map<int, hipblasLtHandle_t> g_blas_handles;
+static std::map<std::tuple<int, uint32_t, uint32_t, uint32_t>, BlasPlan> g_blas_plans;
+
+// The plan for this shape on the current device; ok == false when hipBLASLt
+// offers no algorithm (the fused tiles then run).
+static const BlasPlan &blas_plan(uint32_t m, uint32_t n, uint32_t k) {
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    std::lock_guard<std::mutex> hold(g_blas_lock);
+    const auto key = std::make_tuple(dev, m, n, k);
+    auto it = g_blas_plans.find(key);
+    if (it != g_blas_plans.end()) return it->second;
+    BlasPlan &pl = g_blas_plans[key];
+    // hipblasLtCreate ends the process when no device is present: ask first.
+    int devices = 0;
+    if (hipGetDeviceCount(&devices) != hipSuccess || devices <= 0) return pl;
+    hipblasLtHandle_t &h = g_blas_handles[dev];
+    if (!h && hipblasLtCreate(&h) != HIPBLAS_STATUS_SUCCESS) {
+        h = nullptr;
+        return pl;
+    }
+    pl.handle = h;
+    const int32_t op_t = HIPBLAS_OP_T, op_n = HIPBLAS_OP_N;
+    if (hipblasLtMatmulDescCreate(&pl.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS ||
+        hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &op_t, sizeof(op_t)) != HIPBLAS_STATUS_SUCCESS ||
+        hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &op_n, sizeof(op_n)) != HIPBLAS_STATUS_SUCCESS ||
+        hipblasLtMatrixLayoutCreate(&pl.a, HIP_R_16F, k, n, k) != HIPBLAS_STATUS_SUCCESS ||
+        hipblasLtMatrixLayoutCreate(&pl.b, HIP_R_16F, k, m, k) != HIPBLAS_STATUS_SUCCESS ||
+        hipblasLtMatrixLayoutCreate(&pl.d, HIP_R_32F, n, m, n) != HIPBLAS_STATUS_SUCCESS)
+        return pl;
+    hipblasLtMatmulPreference_t pref = nullptr;
+    if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS) return pl;
+    const uint64_t wsmax = BLAS_WS_MAX;
+    hipblasLtMatmulHeuristicResult_t res;
+    int count = 0;
+    if (hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsmax, sizeof(wsmax)) ==
+            HIPBLAS_STATUS_SUCCESS &&
+        hipblasLtMatmulAlgoGetHeuristic(h, pl.desc, pl.a, pl.b, pl.d, pl.d, pref, 1, &res, &count) ==
+            HIPBLAS_STATUS_SUCCESS &&
+        count > 0 && res.state == HIPBLAS_STATUS_SUCCESS && res.workspaceSize <= BLAS_WS_MAX) {
+        pl.algo = res.algo;
+        pl.ws = res.workspaceSize;
+        pl.ok = true;
+    }
+    hipblasLtMatmulPreferenceDestroy(pref);
+    return pl;
+}
+
+static bool vendor_format(uint32_t format) {
+    switch (format) {
+    case OCO_Q4_0: case OCO_Q4_1: case OCO_Q8_0: case OCO_Q4_K: case OCO_Q5_K: case OCO_Q6_K: case OCO_F16: case OCO_F32:
+        return true;
+    }
+    return false;
+}
+
+// The vendor path from 32 activation rows, where prefill starts (measured
+// on the box at 32..256 rows: as fast or faster for Q4_K 12288 x 4096, 2-3x
+// for Q8_0 4096 x 4096 and Q6_K 4096 x 12288), unless the
+// OCO_KNOB_MATMUL_VENDOR override chooses.
+static bool use_vendor(uint32_t format, uint32_t m) {
+    if (!vendor_format(format)) return false;
+    int32_t ov[4];
+    if (plan_override(OCO_KNOB_MATMUL_VENDOR, ov)) return ov[0] != 0;
+    return m >= 32;
+}
+
+struct VendorLayout {
+    uint64_t w, x, d, blas, total;  // byte offsets in the workspace, and its size
+};
+static VendorLayout vendor_layout(uint32_t format, oco_dtype x_dtype, uint32_t m, uint32_t n, uint32_t k, uint64_t blas_ws) {
+    auto al = [](uint64_t b) { return (b + 255) & ~255ull; };
+    VendorLayout v;
+    v.w = 0;
+    v.x = v.w + (format == OCO_F16 ? 0 : al((uint64_t)n * k * 2));
+    v.d = v.x + (x_dtype == OCO_DT_F16 ? 0 : al((uint64_t)m * k * 2));
+    v.blas = v.d + al((uint64_t)m * n * 4);
+    v.total = v.blas + blas_ws;
+    return v;
+}
+
+template <int FMT>
+static void operand_launch(const void *w, uint64_t row_bytes, uint32_t n, uint32_t k, uint16_t *wo, const void *x,
+                           uint16_t *xo, uint64_t xchunks, hipStream_t stream) {
+    const uint64_t pieces = (uint64_t)n * ((k + 127) / 128) * 4;
+    const uint32_t wblocks = FMT == OCO_F16 ? 0 : (uint32_t)((pieces + 255) / 256);
+    const uint32_t xblocks = (uint32_t)((xchunks + 255) / 256);
+    hipLaunchKernelGGL(operand_kernel<FMT>, dim3(wblocks + xblocks), dim3(256), 0, stream, (const uint8_t *)w, row_bytes,
+                       n, k, wo, (const uint16_t *)x, xo, xchunks, wblocks);
+}
+
+static int vendor_matmul(uint32_t format, const void *w, const void *x, oco_dtype x_dtype, void *y, oco_dtype y_dtype,
+                         const float *bias, const oco_matrix *p, const BlasPlan &pl, void *workspace,
+                         uint64_t workspace_bytes, hipStream_t stream) {
+    const uint32_t m = p->m, n = p->n, k = p->k;
+    const VendorLayout v = vendor_layout(format, x_dtype, m, n, k, pl.ws);
+    if (!workspace || workspace_bytes < v.total)
+        return fail(OCO_ERR_INVALID, "oco_matmul_ws: workspace of %llu bytes, need %llu",
+                    (unsigned long long)workspace_bytes, (unsigned long long)v.total);
+    uint8_t *ws = (uint8_t *)workspace;
+    uint16_t *wo = format == OCO_F16 ? nullptr : (uint16_t *)(ws + v.w);
+    uint16_t *xo = x_dtype == OCO_DT_F16 ? nullptr : (uint16_t *)(ws + v.x);
+    const uint64_t xchunks = xo ? (uint64_t)m * k / 8 : 0;
+    if (wo || xo) {
+        const uint64_t rb = oco_row_bytes(format, k);
+        switch (format) {
+#define CASE(F) case F: operand_launch<F>(w, rb, n, k, wo, x, xo, xchunks, stream); break;
+            CASE(OCO_Q4_0) CASE(OCO_Q4_1) CASE(OCO_Q8_0) CASE(OCO_Q4_K) CASE(OCO_Q5_K) CASE(OCO_Q6_K) CASE(OCO_F16)
+            CASE(OCO_F32)
+#undef CASE
+        }
+        OCO_TRY(launch_check("oco_matmul: operand pass"));
+    }
+    const bool direct = y_dtype == OCO_DT_F32 && !(p->has_bias && bias);
+    float *acc = direct ? (float *)y : (float *)(ws + v.d);
+    const float alpha = 1.0f, beta = 0.0f;
+    const hipblasStatus_t st = hipblasLtMatmul(pl.handle, pl.desc, &alpha, wo ? (const void *)wo : w, pl.a,
+                                               xo ? (const void *)xo : x, pl.b, &beta, acc, pl.d, acc, pl.d, &pl.algo,
+                                               pl.ws ? ws + v.blas : nullptr, pl.ws, stream);
+    if (st != HIPBLAS_STATUS_SUCCESS) return fail(OCO_ERR_HIP, "oco_matmul: hipblasLtMatmul status %d", (int)st);
+    if (!direct) {
+        const uint64_t quads = (uint64_t)m * n / 4;
+        hipLaunchKernelGGL(gemm_epilogue_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, stream, acc,
+                           p->has_bias ? bias : nullptr, y, y_dtype == OCO_DT_BF16, n, quads);
+        OCO_TRY(launch_check("oco_matmul: epilogue"));
+    }
+    return OCO_OK;
+}
+
 uint64_t mx_workspace_bytes(uint32_t m, uint32_t n, uint32_t k);
 int mx_matmul_launch(const void *w, const void *x, void *y, bool y_bf16, const float *bias, uint32_t m, uint32_t n,
                      uint32_t k, void *workspace, hipStream_t stream);
@@ -601,10 +822,18 @@ static int matmul_decode_launch(uint32_t format, const void *w, const void *x, o
 
 using namespace oco;
 
+// The vendor path needs n % 4 == 0 (the epilogue's four columns per thread).
+static const BlasPlan *vendor_plan(uint32_t format, const oco_matrix *p) {
+    if (!use_vendor(format, p->m) || p->n % 4 || p->m == 0 || p->n == 0) return nullptr;
+    const BlasPlan &pl = blas_plan(p->m, p->n, p->k);
+    return pl.ok ? &pl : nullptr;
+}
+
 extern "C" uint64_t oco_matmul_workspace(uint32_t format, oco_dtype x_dtype, const oco_matrix *p) {
-    (void)x_dtype;
-    if (!p || !use_mx(format)) return 0;
-    return mx_workspace_bytes(p->m, p->n, p->k);
+    if (!p) return 0;
+    if (use_mx(format)) return mx_workspace_bytes(p->m, p->n, p->k);
+    if (const BlasPlan *pl = vendor_plan(format, p)) return vendor_layout(format, x_dtype, p->m, p->n, p->k, pl->ws).total;
+    return 0;
 }
 
 extern "C" int oco_matmul_ws(uint32_t format, const void *w, const void *x, oco_dtype x_dtype, void *y,
@@ -620,6 +849,9 @@ extern "C" int oco_matmul_ws(uint32_t format, const void *w, const void *x, oco_
         return mx_matmul_launch(w, x, y, y_dtype == OCO_DT_BF16, p->has_bias ? bias : nullptr, p->m, p->n, p->k,
                                 workspace, (hipStream_t)stream);
     }
+    if (const BlasPlan *pl = vendor_plan(format, p))
+        return vendor_matmul(format, w, x, x_dtype, y, y_dtype, bias, p, *pl, workspace, workspace_bytes,
+                             (hipStream_t)stream);
     return matmul_decode_launch(format, w, x, x_dtype, y, y_dtype, bias, p, (hipStream_t)stream);
 }
 

@@ -68,6 +68,7 @@ def test_argument_validation_without_gpu():
     # per lane and step, plus one 16-byte scale word per lane (K steps
     # counted to whole stages: 45 -> 48)
     assert need == (512 // 32) * ((2880 // 64 + 7) // 8) * (8 * 64 * 48 + 64 * 16)
+    # Q4_K prefill takes the vendor GEMM, whose plan needs a device: none here
     assert lib.oco_matmul_workspace(12, 1, ctypes.byref(p)) == 0
     assert lib.oco_matmul_ws(39, fake, fake, 1, fake, 0, None, ctypes.byref(p), fake, need - 1, None) == 1
     assert b"workspace" in lib.oco_last_error()

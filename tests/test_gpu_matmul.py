@@ -200,3 +200,115 @@ def test_matmul_mxfp4_tails(lib, m, n, k):
     for _ in range(2):
         again = run(lib, 39, w, x, m, n, k)
         assert np.array_equal(again.view(np.uint32), first.view(np.uint32))
+
+
+# Formats with f16 operands: at 64 activation rows and more (n % 4 == 0)
+# they take the dequantize pass and the vendor GEMM unless the knob says
+# otherwise.  Both paths run the same operand bits, so both meet the
+# half-operand roundoff bound per element.
+VENDOR_FORMATS = [P.Q8_0, P.Q4_K, P.Q6_K, P.Q5_K, P.Q4_0, P.Q4_1, 1, 0]
+
+
+def _dense_weights(fmt, n, k, seed):
+    if fmt in (0, 1):  # F32 / F16 weights as stored
+        v = np.random.default_rng(seed).normal(0, 0.05, n * k)
+        return np.frombuffer(v.astype(np.float16 if fmt == 1 else np.float32).tobytes(), np.uint8)
+    from oco_amd import synth
+    return synth.weights(fmt, n, k, seed=seed)
+
+
+def _run_dense(oco, fmt, w, x, m, n, k, x_f16=False, y_bf16=False, bias=None):
+    wb = oco.DeviceBuffer.from_array(w)
+    xb = oco.DeviceBuffer.from_array(x)
+    y = Guarded(oco, m * n * (2 if y_bf16 else 4))
+    bb = oco.DeviceBuffer.from_array(bias) if bias is not None else None
+    p = oco.Matrix(k, n, m, 0, 1, 1, 1 if bias is not None else 0)
+    oco.matmul(fmt, wb, xb, y.ptr, p, oco.DType.F16 if x_f16 else oco.DType.BF16,
+               oco.DType.BF16 if y_bf16 else oco.DType.F32, bb)
+    oco.synchronize()
+    got = y.read(np.uint16 if y_bf16 else np.float32)
+    return (O.bf16_to_f32(got) if y_bf16 else got).reshape(m, n)
+
+
+@pytest.mark.parametrize("fmt", VENDOR_FORMATS)
+@pytest.mark.parametrize("m,n", [(64, 256), (200, 132)])
+@pytest.mark.parametrize("vendor", [0, 1])
+def test_matmul_vendor_and_fused(lib, fmt, m, n, vendor):
+    """Both f16-operand paths against the fp64 oracle; 32-block formats at
+    k = 1184 (a partial last 128-wide step), K-quants at k = 1280."""
+    from oco_amd import synth
+    k = 1280 if fmt in (P.Q4_K, P.Q6_K, P.Q5_K) else 1184
+    say("matmul vendor/fused", fmt, m, n, k, vendor)
+    w = _dense_weights(fmt, n, k, 21)
+    x = synth.bf16_bits(synth.activations(22, m * k)).reshape(m, k)
+    with lib.overridden(lib.Knob.MATMUL_VENDOR, [vendor]):
+        got = _run_dense(lib, fmt, w, x, m, n, k)
+    exact, _ = O.matmul_reference(fmt, w, x, n, k, half_operands=False)
+    half, mag = O.matmul_reference(fmt, w, x, n, k, half_operands=True)
+    assert rel_l2(got, exact) <= 2e-3
+    assert np.all(np.abs(got - half) <= O.roundoff_bound(half, mag, k, False))
+
+
+@pytest.mark.parametrize("vendor", [0, 1])
+def test_matmul_f16_input_bias_bf16_output(lib, vendor):
+    """f16 activations (no conversion pass), bias and bf16 output through
+    the epilogue; reruns bit-identical."""
+    from oco_amd import synth
+    m, n, k = 96, 260, 768
+    w = synth.weights(P.Q4_K, n, k, seed=31)
+    x = (synth.activations(32, m * k).reshape(m, k)).astype(np.float16)
+    bias = np.random.default_rng(33).normal(size=n).astype(np.float32)
+    with lib.overridden(lib.Knob.MATMUL_VENDOR, [vendor]):
+        got = _run_dense(lib, P.Q4_K, w, x, m, n, k, x_f16=True, y_bf16=True, bias=bias)
+        again = _run_dense(lib, P.Q4_K, w, x, m, n, k, x_f16=True, y_bf16=True, bias=bias)
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+    half, mag = O.matmul_reference(P.Q4_K, w, x, n, k, half_operands=True)
+    want = half + O.bf16_round(bias)
+    assert np.all(np.abs(got - want) <= O.roundoff_bound(want, mag + np.abs(O.bf16_round(bias)), k, True))
+
+
+def test_matmul_vendor_workspace(lib):
+    """The vendor path's workspace: the f16 weights, the f16 activations and
+    the fp32 product; too small a workspace is refused."""
+    from oco_amd import synth
+    m, n, k = 128, 512, 1024
+    p = lib.Matrix(k, n, m, 0, 1, 1, 0)
+    need = lib.matmul_workspace(P.Q4_K, p)
+    assert need >= n * k * 2 + m * k * 2 + m * n * 4
+    assert lib.matmul_workspace(P.Q4_K, p, lib.DType.F16) == need - m * k * 2
+    w = lib.DeviceBuffer.from_array(synth.weights(P.Q4_K, n, k, seed=5))
+    x = lib.DeviceBuffer.from_array(synth.bf16_bits(synth.activations(6, m * k)))
+    y = lib.DeviceBuffer(m * n * 4)
+    ws = lib.DeviceBuffer(need)
+    with pytest.raises(RuntimeError):
+        lib.matmul(P.Q4_K, w, x, y, p, workspace=ws, workspace_bytes=need - 256)
+    lib.matmul(P.Q4_K, w, x, y, p, workspace=ws, workspace_bytes=need)
+    lib.synchronize()
+
+
+def test_matmul_vendor_in_graph(lib):
+    """A shape first seen inside stream capture (its GEMM plan is made
+    there), replayed three times with eager work between: every replay
+    equals the eager result bit for bit."""
+    from oco_amd import synth
+    m, n, k = 72, 388, 640
+    fmt = P.Q8_0
+    w = lib.DeviceBuffer.from_array(synth.weights(fmt, n, k, seed=41))
+    x = lib.DeviceBuffer.from_array(synth.bf16_bits(synth.activations(42, m * k)))
+    p = lib.Matrix(k, n, m, 0, 1, 1, 0)
+    y = lib.DeviceBuffer(m * n * 2)
+    s = lib.Stream()
+    g = lib.Graph(s, lambda: lib.matmul(fmt, w, x, y, p, y_dtype=lib.DType.BF16, stream=s))
+    s.sync()
+    eager = lib.DeviceBuffer(m * n * 2)
+    lib.matmul(fmt, w, x, eager, p, y_dtype=lib.DType.BF16)
+    lib.synchronize()
+    want = eager.download(np.uint16, m * n)
+    for _ in range(3):
+        y.fill32(0)
+        lib.synchronize()
+        g.launch()
+        s.sync()
+        assert np.array_equal(y.download(np.uint16, m * n), want)
+        lib.matmul(fmt, w, x, eager, p, y_dtype=lib.DType.BF16)  # eager work between replays
+        lib.synchronize()
