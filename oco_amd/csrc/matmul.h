@@ -46,6 +46,28 @@ __device__ __forceinline__ float row_gain(uint32_t bits) {
     return __builtin_ldexpf(1.0f, max(-100, min(100, 14 - e)));
 }
 
+// Four weights from the nibbles of one dword (one per byte, high nibbles
+// clear), rounded to f16 as a * q - m (the reference's scale * value -
+// minimum, then half(); a * q is exact in f32):
+//   - a byte c < 16 read as E4M3 is c * 2^-9 (exponent 0: c/8 * 2^-6;
+//     exponent 1: (8 + c - 8)/8 * 2^-6), so v_cvt_scalef32_pk_f32_fp8 with
+//     scale 2^9 gives two exact f32 codes per instruction;
+//   - v_fma_f32 gives fl32(a q - m); v_cvt_pk_f16_f32 rounds a pair to f16.
+// Measured on gfx950, this costs about two thirds of v_cvt_f32_ubyte +
+// v_fma_mix{lo,hi}_f16 per weight (the mixed-precision FMA issues at a
+// fraction of the full rate).
+typedef float q4f32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void q4_four(uint32_t n, float a, float m, uint32_t &p01, uint32_t &p23) {
+    const q4f32x2 c01 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(n, 512.0f, false);
+    const q4f32x2 c23 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(n, 512.0f, true);
+    const float f0 = __builtin_fmaf(a, c01[0], -m), f1 = __builtin_fmaf(a, c01[1], -m);
+    const float f2 = __builtin_fmaf(a, c23[0], -m), f3 = __builtin_fmaf(a, c23[1], -m);
+    // inline asm keeps the compiler from folding each FMA and its conversion
+    // back into a mixed-precision FMA
+    asm volatile("v_cvt_pk_f16_f32 %0, %1, %2" : "=v"(p01) : "v"(f0), "v"(f1));
+    asm volatile("v_cvt_pk_f16_f32 %0, %1, %2" : "=v"(p23) : "v"(f2), "v"(f3));
+}
+
 // Grouped modes of matmul_kernel.
 constexpr int MM_DENSE = 0;  // Y = X W^T
 constexpr int MM_GATE_UP = 1;  // per expert tile: act = f(X W_gate^T, X W_up^T), f32 at expert-sorted rows

@@ -136,19 +136,14 @@ struct PrefillPiece {
             kquant_scale_min(sb, 2 * g + 1, sc1, mn1);
             const float d = half_bits_to_f32(r.w[0] & 0xffffu), dmin = half_bits_to_f32(r.w[0] >> 16);
             const float a0 = d * (float)sc0, m0 = dmin * (float)mn0, a1 = d * (float)sc1, m1 = dmin * (float)mn1;
+            // half(a q - m): a q is exact in f32 (a = d sc has at most 17
+            // significant bits, q 4), so the fused multiply-add rounds the
+            // same value the reference's multiply and subtract do
+            static_assert(!BF, "K-quants take f16 operands");
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                uint16_t lo[4], hi[4];
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const uint32_t byte = byte_of(r.w[4 + j], i);
-                    lo[i] = operand_bits<BF>(__fsub_rn(__fmul_rn(a0, (float)(byte & 15u)), m0));
-                    hi[i] = operand_bits<BF>(__fsub_rn(__fmul_rn(a1, (float)(byte >> 4)), m1));
-                }
-                out[2 * j] = pack2(lo[0], lo[1]);
-                out[2 * j + 1] = pack2(lo[2], lo[3]);
-                out[8 + 2 * j] = pack2(hi[0], hi[1]);
-                out[8 + 2 * j + 1] = pack2(hi[2], hi[3]);
+                q4_four(r.w[4 + j] & 0x0f0f0f0fu, a0, m0, out[2 * j], out[2 * j + 1]);
+                q4_four((r.w[4 + j] >> 4) & 0x0f0f0f0fu, a1, m1, out[8 + 2 * j], out[8 + 2 * j + 1]);
             }
             const uint32_t base = 64 * g + 16 * odd - (k0 % 256) / 128 * 128;
             col0[0] = base;
