@@ -844,7 +844,11 @@ extern "C" int oco_matmul_ws(uint32_t format, const void *w, const void *x, oco_
         return mx_matmul_launch(w, x, y, y_dtype == OCO_DT_BF16, p->has_bias ? bias : nullptr, p->m, p->n, p->k,
                                 workspace, (hipStream_t)stream);
     }
-    if (const BlasPlan *pl = vendor_plan(format, p))
+    // Operands the GEMM reads as given (F16 weights, f16 activations) must be
+    // 16-byte aligned for it; otherwise the fused tiles run.
+    const bool aligned = (format != OCO_F16 || ((uintptr_t)w & 15) == 0) &&
+                         (x_dtype != OCO_DT_F16 || ((uintptr_t)x & 15) == 0);
+    if (const BlasPlan *pl = aligned ? vendor_plan(format, p) : nullptr)
         return vendor_matmul(format, w, x, x_dtype, y, y_dtype, bias, p, *pl, workspace, workspace_bytes,
                              (hipStream_t)stream);
     return matmul_decode_launch(format, w, x, x_dtype, y, y_dtype, bias, p, (hipStream_t)stream);

@@ -312,3 +312,22 @@ def test_matmul_vendor_in_graph(lib):
         assert np.array_equal(y.download(np.uint16, m * n), want)
         lib.matmul(fmt, w, x, eager, p, y_dtype=lib.DType.BF16)  # eager work between replays
         lib.synchronize()
+
+
+def test_matmul_f16_input_unaligned(lib):
+    """f16 activations at a 2-byte offset: the GEMM reads them as given, so
+    such a call takes the fused tiles, with the same bar."""
+    from oco_amd import synth
+    m, n, k = 64, 128, 512
+    w = lib.DeviceBuffer.from_array(synth.weights(P.Q8_0, n, k, seed=61))
+    x16 = synth.activations(62, m * k).astype(np.float16)
+    xb = lib.DeviceBuffer(m * k * 2 + 16)
+    xb.upload(x16, 2)
+    y = lib.DeviceBuffer(m * n * 4)
+    p = lib.Matrix(k, n, m, 0, 1, 1, 0)
+    lib.matmul(P.Q8_0, w, xb.ptr + 2, y, p, x_dtype=lib.DType.F16)
+    lib.synchronize()
+    got = y.download(np.float32, m * n).reshape(m, n)
+    wn = synth.weights(P.Q8_0, n, k, seed=61)
+    half, mag = O.matmul_reference(P.Q8_0, wn, x16.reshape(m, k), n, k, half_operands=True)
+    assert np.all(np.abs(got - half) <= O.roundoff_bound(half, mag, k, False))
