@@ -289,6 +289,14 @@ __global__ __launch_bounds__(64 * NW) void moe_q4k_kernel(KPRE_PARAMS, MatmulArg
 #pragma unroll
         for (int j = 0; j < 2; j++) acc[i][j] = q4f32x4{0.f, 0.f, 0.f, 0.f};
 
+    // 16-row fragments of the computing unit's tile that hold routes: the
+    // MFMAs of the others are skipped (their rows are never stored).
+    auto tile_live = [&](uint32_t u) __attribute__((always_inline)) {
+        const uint32_t rows = __builtin_amdgcn_readfirstlane(t_info[u / chunks - y0][1]);
+        return (min(rows, (uint32_t)ROWS) + 15) / 16;
+    };
+    uint32_t live = tile_live(lo);
+
     // One step: eight MFMA chunks of 32 k, each issuing its share of the
     // refill for step t + 2.
     auto compute = [&](int st, const Q4Set *wc, int nst, Q4Set *wn) __attribute__((always_inline)) {
@@ -330,6 +338,7 @@ __global__ __launch_bounds__(64 * NW) void moe_q4k_kernel(KPRE_PARAMS, MatmulArg
             const q4f16x8 b0 = q4_chunk<C>(r[0], s0), b1 = q4_chunk<C>(r[1], s1);
 #pragma unroll
             for (int i = 0; i < MI; i++) {
+                if (i > 0 && (uint32_t)i >= live) continue;  // uniform: a fragment past the tile's routes
                 acc[i][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], b0, acc[i][0], 0, 0, 0);
                 acc[i][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], b1, acc[i][1], 0, 0, 0);
             }
@@ -451,6 +460,7 @@ __global__ __launch_bounds__(64 * NW) void moe_q4k_kernel(KPRE_PARAMS, MatmulArg
             csb = 0;
             cu++;
             pend = true;
+            if (cu < hi) live = tile_live(cu);
         }
     };
     // The loop starts with step t's compute (its start is the previous
