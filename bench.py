@@ -407,6 +407,35 @@ class Prefill(Workload):
         return 2.0 * self.m * self.n * self.k
 
 
+class NormPrefill(Prefill):
+    """The norm -> MXFP4 prefill pair of a layer (prepare_norm_scales +
+    apply_norm, feed_forward.rs:99-101): the RMS norm of 512 bf16 residual
+    rows, then the 5760 x 2880 MXFP4 product of the normalised rows.
+    "fused": oco_norm_mx_split + oco_matmul_mx_split (two launches);
+    "unfused": oco_norm + oco_matmul_ws (norm, split, product: three)."""
+
+    def __init__(self, mode):
+        super().__init__(f"norm_prefill_mxfp4_5760x2880_m512_{mode}", 39, 5760, 2880, 512)
+        self.mode = mode
+
+    def setup(self, oco, stream):
+        super().setup(oco, stream)
+        import numpy as np
+        self.nw = oco.DeviceBuffer.from_array(np.random.default_rng(5).normal(1.0, 0.1, self.k).astype(np.float32))
+        self.xn = oco.DeviceBuffer(self.m * self.k * 2)
+
+    def launch(self, i):
+        o = self.oco
+        w = self.w.ptr + (i % self.copies) * self.bytes
+        if self.mode == "fused":
+            o.norm_mx_split(self.x, self.nw, None, self.m, self.k, 1e-5, True, self.ws, self.ws_bytes, stream=self.stream)
+            o.matmul_mx_split(w, self.ws, self.ws_bytes, self.y, self.p, y_dtype=o.DType.BF16, stream=self.stream)
+        else:
+            o.norm(self.x, self.nw, self.xn, self.m, self.k, 1e-5, True, stream=self.stream)
+            o.matmul(self.fmt, w, self.xn, self.y, self.p, y_dtype=o.DType.BF16, stream=self.stream,
+                     workspace=self.ws, workspace_bytes=self.ws_bytes)
+
+
 WORKLOADS = {
     "mxfp4_decode_matvec_5760x2880": lambda: Matvec("mxfp4_decode_matvec_5760x2880", 39, 5760, 2880),
     "q8_0_matvec_4096x4096": lambda: Matvec("q8_0_matvec_4096x4096", 8, 4096, 4096),
@@ -422,6 +451,8 @@ WORKLOADS = {
     "moe_decode_gpt_oss_b4": lambda: MoeDecode(4),
     "moe_decode_gpt_oss_b16": lambda: MoeDecode(16),
     "prefill_mxfp4_5760x2880_m512": lambda: Prefill("prefill_mxfp4_5760x2880_m512", 39, 5760, 2880, 512),
+    "norm_prefill_mxfp4_5760x2880_m512_fused": lambda: NormPrefill("fused"),
+    "norm_prefill_mxfp4_5760x2880_m512_unfused": lambda: NormPrefill("unfused"),
     "prefill_q4_k_12288x4096_m512": lambda: Prefill("prefill_q4_k_12288x4096_m512", 12, 12288, 4096, 512),
     "prefill_q6_k_4096x12288_m512": lambda: Prefill("prefill_q6_k_4096x12288_m512", 14, 4096, 12288, 512),
     "prefill_q8_0_4096x4096_m512": lambda: Prefill("prefill_q8_0_4096x4096_m512", 8, 4096, 4096, 512),
@@ -580,6 +611,7 @@ def main():
         for name in ["q8_0_matvec_4096x4096", "q4_k_matvec_12288x4096", "q6_k_matvec_4096x12288",
                      "q6_k_lm_head_151936x4096", "qwen3_8b_q4km_decode_stack", "moe_decode_gpt_oss_b1",
                      "moe_decode_gpt_oss_b4", "moe_decode_gpt_oss_b16", "prefill_mxfp4_5760x2880_m512",
+                     "norm_prefill_mxfp4_5760x2880_m512_fused", "norm_prefill_mxfp4_5760x2880_m512_unfused",
                      "prefill_q4_k_12288x4096_m512", "prefill_q6_k_4096x12288_m512", "prefill_q8_0_4096x4096_m512",
                      "moe_prefill_qwen3_30b_a3b", "lm_head_argmax_qwen3_8b", "argmax_f32_151936",
                      "norm_up_gate_qwen3_8b_group", "norm_up_gate_qwen3_8b_fused",

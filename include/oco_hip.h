@@ -227,13 +227,15 @@ int oco_matvec_relu_sqr(uint32_t format, const void *w, const void *x, oco_dtype
  * Replaces DenseMatrix::apply's tiled plans (compute/matrix.rs:130-379,
  * `matmul`/`matmul_q4*`/`matmul_tensor_*`, batch.metal:24-79, tensor.metal:9-102).
  * Operands: formats other than MXFP4 decode to f16 (the reference's
- * half(w), tile.metal:16-80) with activations converted to f16.  X is bf16
- * or f16 row-major; Y f32 or bf16.  MXFP4 runs the block-scaled FP6 x FP4
- * MFMA on the GGUF bytes as stored, with each 32-block of X split into two
- * E2M3 terms with their own E8M0 scales (at most 1/225 of the block maximum
- * per value; relative L2 of the product a few 1e-4, inside the 2e-3 bound
- * for bf16-activation MFMA prefill); that split needs a workspace, which
- * oco_matmul takes from the stream-ordered pool (hipMallocAsync). */
+ * half(w), tile.metal:16-80) with activations converted to f16; from 32
+ * rows (n % 4 == 0) that decode is one pass into a workspace and the
+ * product a vendor (hipBLASLt) f16 GEMM, below it fused MFMA tiles.  X is
+ * bf16 or f16 row-major; Y f32 or bf16.  MXFP4 runs the block-scaled FP6 x
+ * FP4 MFMA on the GGUF bytes as stored, with each 32-block of X split into
+ * two E2M3 terms with their own E8M0 scales (at most 1/225 of the block
+ * maximum per value; relative L2 of the product a few 1e-4, inside the 2e-3
+ * bound for bf16-activation MFMA prefill), also through a workspace.
+ * oco_matmul takes workspaces from the stream-ordered pool (hipMallocAsync). */
 int oco_matmul(uint32_t format, const void *w, const void *x, oco_dtype x_dtype, void *y,
                oco_dtype y_dtype, const float *bias, const oco_matrix *p, oco_stream stream);
 
@@ -246,6 +248,22 @@ uint64_t oco_matmul_workspace(uint32_t format, oco_dtype x_dtype, const oco_matr
 int oco_matmul_ws(uint32_t format, const void *w, const void *x, oco_dtype x_dtype, void *y,
                   oco_dtype y_dtype, const float *bias, const oco_matrix *p, void *workspace,
                   uint64_t workspace_bytes, oco_stream stream);
+
+/* The norm -> MXFP4 prefill pair in two launches instead of three: the RMS
+ * norm of oco_norm (same rounding) whose workgroups also split each output
+ * row into the E2M3 records the MXFP4 prefill reads, bit for bit the records
+ * oco_matmul would make from oco_norm's output.  `split`: at least
+ * oco_matmul_workspace(OCO_MXFP4, OCO_DT_BF16, {k = n, m = rows}) bytes; `y`
+ * (optional, may be null) receives the bf16 output rows too; n % 32 == 0.
+ * Replaces prepare_norm_scales + apply_norm (the batch norm folded into the
+ * matrix's input: feed_forward.rs:99-101, compute/matrix.rs:429-441). */
+int oco_norm_mx_split(const void *x, const float *norm_w, void *y, uint32_t rows, uint32_t n, float epsilon,
+                      int full_layer, void *split, uint64_t split_bytes, oco_stream stream);
+
+/* oco_matmul for MXFP4 weights from rows already split by oco_norm_mx_split
+ * (the same m and k): equal to oco_norm then oco_matmul, bit for bit. */
+int oco_matmul_mx_split(const void *w, const void *split, uint64_t split_bytes, void *y, oco_dtype y_dtype,
+                        const float *bias, const oco_matrix *p, oco_stream stream);
 
 /* ---- routing ------------------------------------------------------------ */
 

@@ -162,6 +162,8 @@ SIGNATURES = {
     "oco_matmul": (_i32, [_u32, _vp, _vp, _i32, _vp, _i32, _vp, _MP, _vp]),
     "oco_matmul_workspace": (_u64, [_u32, _i32, _MP]),
     "oco_matmul_ws": (_i32, [_u32, _vp, _vp, _i32, _vp, _i32, _vp, _MP, _vp, _u64, _vp]),
+    "oco_norm_mx_split": (_i32, [_vp, _vp, _vp, _u32, _u32, ctypes.c_float, _i32, _vp, _u64, _vp]),
+    "oco_matmul_mx_split": (_i32, [_vp, _vp, _u64, _vp, _i32, _vp, _MP, _vp]),
     "oco_route_select": (_i32, [_vp, _u32, _u32, _u32, _vp, _vp, _vp]),
     "oco_router": (_i32, [_vp, _i32, _vp, _vp, _u32, _u32, _u32, _u32, _vp, _vp, _vp, _vp]),
     "oco_route_plan_words": (_u64, [_u32, _u32]),
@@ -453,6 +455,20 @@ def matmul(fmt: int, w, x, y, p: Matrix, x_dtype=DType.BF16, y_dtype=DType.F32, 
 
 def matmul_workspace(fmt: int, p: Matrix, x_dtype=DType.BF16) -> int:
     return int(load_library().oco_matmul_workspace(int(fmt), int(x_dtype), ctypes.byref(as_matrix(p))))
+
+
+def norm_mx_split(x, w, y, rows: int, n: int, epsilon: float, full_layer: bool, split, split_bytes: int,
+                  stream=None):
+    """oco_norm_mx_split: RMS norm rows (y optional) and their MXFP4-prefill split records."""
+    _check(load_library().oco_norm_mx_split(_addr(x), _addr(w), _addr(y), rows, n, float(epsilon),
+                                            1 if full_layer else 0, _addr(split), int(split_bytes),
+                                            _stream(stream)))
+
+
+def matmul_mx_split(w, split, split_bytes: int, y, p: Matrix, y_dtype=DType.F32, bias=None, stream=None):
+    """oco_matmul_mx_split: the MXFP4 prefill from rows split by norm_mx_split."""
+    _check(load_library().oco_matmul_mx_split(_addr(w), _addr(split), int(split_bytes), _addr(y), int(y_dtype),
+                                              _addr(bias), ctypes.byref(as_matrix(p)), _stream(stream)))
 
 
 def route_select(logits, tokens: int, experts: int, k: int, ids, probs, stream=None):

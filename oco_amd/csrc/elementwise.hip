@@ -25,7 +25,24 @@ __global__ __launch_bounds__(256) void norm_kernel(uint16_t *x, const uint16_t *
         __syncthreads();  // each thread re-reads only its own elements, but keep the order explicit
     }
     const float inv = block_inv_rms(xr, n, epsilon, partial);
-    for (uint32_t i = threadIdx.x; i < n; i += 256) orow[i] = norm_value_bits(bf16_bits_to_f32(xr[i]), inv, w[i], full_layer);
+    // eight values per thread through 16-byte accesses when every row is aligned
+    uint32_t i0 = 0;
+    if ((((uintptr_t)xr | (uintptr_t)orow | (uintptr_t)w) & 15u) == 0) {
+        for (uint32_t c = threadIdx.x; 8 * c + 8 <= n; c += 256) {
+            const uint4 u = *reinterpret_cast<const uint4 *>(xr + 8 * c);
+            const float4 w0 = *reinterpret_cast<const float4 *>(w + 8 * c), w1 = *reinterpret_cast<const float4 *>(w + 8 * c + 4);
+            const uint32_t h[4] = {u.x, u.y, u.z, u.w};
+            const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+            uint32_t o[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                o[j] = (uint32_t)norm_value_bits(__uint_as_float(h[j] << 16), inv, wv[2 * j], full_layer) |
+                       ((uint32_t)norm_value_bits(__uint_as_float(h[j] & 0xffff0000u), inv, wv[2 * j + 1], full_layer) << 16);
+            *reinterpret_cast<uint4 *>(orow + 8 * c) = make_uint4(o[0], o[1], o[2], o[3]);
+        }
+        i0 = n / 8 * 8;
+    }
+    for (uint32_t i = i0 + threadIdx.x; i < n; i += 256) orow[i] = norm_value_bits(bf16_bits_to_f32(xr[i]), inv, w[i], full_layer);
 }
 
 // ---- argmax ----------------------------------------------------------------------

@@ -760,7 +760,9 @@ static int vendor_matmul(uint32_t format, const void *w, const void *x, oco_dtyp
 
 uint64_t mx_workspace_bytes(uint32_t m, uint32_t n, uint32_t k);
 int mx_matmul_launch(const void *w, const void *x, void *y, bool y_bf16, const float *bias, uint32_t m, uint32_t n,
-                     uint32_t k, void *workspace, hipStream_t stream);
+                     uint32_t k, void *workspace, hipStream_t stream, bool presplit = false);
+int mx_norm_split_launch(const void *x, const float *w, void *y, uint32_t m, uint32_t k, float epsilon,
+                         bool full_layer, void *workspace, hipStream_t stream);
 
 // MXFP4 goes to the block-scaled FP8 x FP4 MFMA unless the
 // OCO_KNOB_MX_PREFILL_OFF override says otherwise (comparisons against the
@@ -865,4 +867,36 @@ extern "C" int oco_matmul(uint32_t format, const void *w, const void *x, oco_dty
     const int rc = oco_matmul_ws(format, w, x, x_dtype, y, y_dtype, bias, p, ws, need, stream);
     const int rf = hip_check(hipFreeAsync(ws, (hipStream_t)stream), "oco_matmul: hipFreeAsync");
     return rc != OCO_OK ? rc : rf;
+}
+
+extern "C" int oco_norm_mx_split(const void *x, const float *norm_w, void *y, uint32_t rows, uint32_t n,
+                                 float epsilon, int full_layer, void *split, uint64_t split_bytes,
+                                 oco_stream stream) {
+    if (rows == 0) return OCO_OK;
+    if (!x || !norm_w || !split) return fail(OCO_ERR_INVALID, "oco_norm_mx_split: null pointer");
+    if (n == 0 || n % 32) return fail(OCO_ERR_INVALID, "oco_norm_mx_split: n=%u is not whole 32-blocks", n);
+    if (n > 65536) return fail(OCO_ERR_UNSUPPORTED, "oco_norm_mx_split: n=%u past 65536 (the row is staged in LDS)", n);
+    if (rows > 0x7fffffe0u) return fail(OCO_ERR_INVALID, "oco_norm_mx_split: %u rows", rows);
+    const uint64_t need = mx_workspace_bytes(rows, 0, n);
+    if (split_bytes < need)
+        return fail(OCO_ERR_INVALID, "oco_norm_mx_split: split buffer of %llu bytes, need %llu",
+                    (unsigned long long)split_bytes, (unsigned long long)need);
+    return mx_norm_split_launch(x, norm_w, y, rows, n, epsilon, full_layer != 0, split, (hipStream_t)stream);
+}
+
+extern "C" int oco_matmul_mx_split(const void *w, const void *split, uint64_t split_bytes, void *y, oco_dtype y_dtype,
+                                   const float *bias, const oco_matrix *p, oco_stream stream) {
+    if (!p || !w || !split || !y) return fail(OCO_ERR_INVALID, "oco_matmul_mx_split: null argument");
+    if (p->k == 0 || p->k % 32) return fail(OCO_ERR_INVALID, "oco_matmul_mx_split: k=%u must be a multiple of 32", p->k);
+    if (p->experts > 1) return fail(OCO_ERR_UNSUPPORTED, "oco_matmul_mx_split: routed rows go through oco_experts_apply");
+    if (p->has_bias && !bias) return fail(OCO_ERR_INVALID, "oco_matmul_mx_split: has_bias without bias");
+    if (y_dtype != OCO_DT_F32 && y_dtype != OCO_DT_BF16)
+        return fail(OCO_ERR_UNSUPPORTED, "oco_matmul_mx_split: output must be f32 or bf16");
+    if (p->m == 0 || p->n == 0) return OCO_OK;
+    const uint64_t need = mx_workspace_bytes(p->m, p->n, p->k);
+    if (split_bytes < need)
+        return fail(OCO_ERR_INVALID, "oco_matmul_mx_split: split buffer of %llu bytes, need %llu",
+                    (unsigned long long)split_bytes, (unsigned long long)need);
+    return mx_matmul_launch(w, nullptr, y, y_dtype == OCO_DT_BF16, p->has_bias ? bias : nullptr, p->m, p->n, p->k,
+                            const_cast<void *>(split), (hipStream_t)stream, true);
 }

@@ -32,6 +32,7 @@
 #include <algorithm>
 
 #include "mxsplit.h"
+#include "norm.h"
 #include "stream.h"
 
 namespace oco {
@@ -70,30 +71,11 @@ struct MxSplitArgs {
 // column 16 + i -- the nibble order of the GGUF MXFP4 payload the B operand
 // holds as stored.  The second term leaves at most 1/225 of the block
 // maximum per value: a few 1e-4 relative L2 on the product (N(0,1) rows).
-__global__ __launch_bounds__(64) void mx_split_kernel(KPRE_PARAMS, MxSplitArgs a) {
-    KPRE_APPLY(a);
-    const uint32_t rec = blockIdx.x;
-    const uint32_t lane = threadIdx.x, tile = rec / a.kpad, s = rec % a.kpad;
-    const uint32_t row = tile * 32 + (lane & 31), k0 = s * 64 + 32 * (lane >> 5);
-    uint32_t w[16];
-    if (row < a.m && k0 < a.k) {
-        const auto src = gp(reinterpret_cast<const u32x4 *>(a.x + (uint64_t)row * a.k + k0));
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const u32x4 u = src[q];
-            w[4 * q] = u.x; w[4 * q + 1] = u.y; w[4 * q + 2] = u.z; w[4 * q + 3] = u.w;
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < 16; i++) w[i] = 0;
-    }
-    float v[32];  // column order
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-        v[2 * i] = __uint_as_float(w[i] << 16);
-        v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
-    }
-    auto out = gp(a.frag + (uint64_t)rec * MX_REC);
+// One block's split: v holds its 32 values in column order (consumed);
+// lane `lane`'s three chunks of record `out` receive the codes, and the
+// return value the two E8M0 scale bytes (term 0 low).
+__device__ __forceinline__ uint32_t mx_split_block(float *v, __attribute__((address_space(1))) uint8_t *out,
+                                                   uint32_t lane) {
     uint32_t scales = 0;
     i32x6 c0;
 #pragma unroll
@@ -137,9 +119,134 @@ __global__ __launch_bounds__(64) void mx_split_kernel(KPRE_PARAMS, MxSplitArgs a
             }
         }
     }
-    *reinterpret_cast<__attribute__((address_space(1))) uint16_t *>(
-        gp(a.scl + ((uint64_t)tile * (a.kpad / MX_STAGE) + s / MX_STAGE) * MX_SREC + lane * 16 + 2 * (s % MX_STAGE))) =
-        (uint16_t)scales;
+    return scales;
+}
+
+// Record and scale-word addresses of (32-row tile, K step, lane).
+__device__ __forceinline__ __attribute__((address_space(1))) uint8_t *mx_rec(uint8_t *frag, uint32_t tile, uint32_t s,
+                                                                             uint32_t kpad) {
+    return gp(frag + ((uint64_t)tile * kpad + s) * MX_REC);
+}
+__device__ __forceinline__ __attribute__((address_space(1))) uint16_t *mx_scale_slot(uint8_t *scl, uint32_t tile,
+                                                                                      uint32_t s, uint32_t kpad,
+                                                                                      uint32_t lane) {
+    return reinterpret_cast<__attribute__((address_space(1))) uint16_t *>(
+        gp(scl + ((uint64_t)tile * (kpad / MX_STAGE) + s / MX_STAGE) * MX_SREC + lane * 16 + 2 * (s % MX_STAGE)));
+}
+
+__global__ __launch_bounds__(64) void mx_split_kernel(KPRE_PARAMS, MxSplitArgs a) {
+    KPRE_APPLY(a);
+    const uint32_t rec = blockIdx.x;
+    const uint32_t lane = threadIdx.x, tile = rec / a.kpad, s = rec % a.kpad;
+    const uint32_t row = tile * 32 + (lane & 31), k0 = s * 64 + 32 * (lane >> 5);
+    uint32_t w[16];
+    if (row < a.m && k0 < a.k) {
+        const auto src = gp(reinterpret_cast<const u32x4 *>(a.x + (uint64_t)row * a.k + k0));
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const u32x4 u = src[q];
+            w[4 * q] = u.x; w[4 * q + 1] = u.y; w[4 * q + 2] = u.z; w[4 * q + 3] = u.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; i++) w[i] = 0;
+    }
+    float v[32];  // column order
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        v[2 * i] = __uint_as_float(w[i] << 16);
+        v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+    *mx_scale_slot(a.scl, tile, s, a.kpad, lane) = (uint16_t)mx_split_block(v, mx_rec(a.frag, tile, s, a.kpad), lane);
+}
+
+// The RMS norm (elementwise.metal:6-28, oco_norm's rounding) with the split
+// of its output rows: one 256-thread workgroup per row of the 32-row tiles
+// (rows past m write zero records); each thread splits whole blocks of the
+// normalised bf16 row, so the records are bit for bit the split of
+// oco_norm's output.  `y`, when set, receives that bf16 row too.
+struct MxNormSplitArgs {
+    const uint16_t *x;
+    const float *w;
+    uint16_t *y;
+    uint8_t *frag, *scl;
+    uint32_t m, k, kpad, full_layer;
+    float epsilon;
+};
+
+__global__ __launch_bounds__(256) void mx_norm_split_kernel(MxNormSplitArgs a) {
+    __shared__ float partial[4];
+    extern __shared__ __attribute__((aligned(16))) uint16_t nrow[];  // the normalised row, bf16 [k]
+    const uint32_t row = blockIdx.x, tile = row / 32, r = row % 32;
+    const bool live = row < a.m;  // uniform
+    const uint16_t *xr = a.x + (uint64_t)row * a.k;
+    if (live) {
+        const float inv = block_inv_rms(xr, a.k, a.epsilon, partial);
+        // eight consecutive values per thread, coalesced, into LDS (and y)
+        uint16_t *yr = a.y ? a.y + (uint64_t)row * a.k : nullptr;
+        const bool vec = (((uintptr_t)xr | (uintptr_t)a.w | (uintptr_t)yr) & 15u) == 0;
+        for (uint32_t c = threadIdx.x; 8 * c < a.k; c += 256) {
+            float xv[8], wv[8];
+            if (vec) {
+                const uint4 u = *reinterpret_cast<const uint4 *>(xr + 8 * c);
+                const uint32_t h[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    xv[2 * j] = __uint_as_float(h[j] << 16);
+                    xv[2 * j + 1] = __uint_as_float(h[j] & 0xffff0000u);
+                }
+                const float4 w0 = *reinterpret_cast<const float4 *>(a.w + 8 * c);
+                const float4 w1 = *reinterpret_cast<const float4 *>(a.w + 8 * c + 4);
+                wv[0] = w0.x; wv[1] = w0.y; wv[2] = w0.z; wv[3] = w0.w;
+                wv[4] = w1.x; wv[5] = w1.y; wv[6] = w1.z; wv[7] = w1.w;
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    xv[j] = bf16_bits_to_f32(xr[8 * c + j]);
+                    wv[j] = a.w[8 * c + j];
+                }
+            }
+            uint32_t o[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                o[j] = (uint32_t)norm_value_bits(xv[2 * j], inv, wv[2 * j], a.full_layer) |
+                       ((uint32_t)norm_value_bits(xv[2 * j + 1], inv, wv[2 * j + 1], a.full_layer) << 16);
+            *reinterpret_cast<uint4 *>(nrow + 8 * c) = make_uint4(o[0], o[1], o[2], o[3]);
+            if (yr) {
+                if (vec) {
+                    *reinterpret_cast<uint4 *>(yr + 8 * c) = make_uint4(o[0], o[1], o[2], o[3]);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        yr[8 * c + 2 * j] = (uint16_t)o[j];
+                        yr[8 * c + 2 * j + 1] = (uint16_t)(o[j] >> 16);
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+    // one whole block per thread (padding steps and rows past m: zeros)
+    for (uint32_t b = threadIdx.x; b < 2 * a.kpad; b += 256) {
+        const uint32_t s = b / 2, lane = r + 32 * (b & 1), k0 = 32 * b;
+        float v[32];  // column order
+        if (live && k0 < a.k) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const uint4 u = *reinterpret_cast<const uint4 *>(nrow + k0 + 8 * q);
+                const uint32_t h[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    v[8 * q + 2 * j] = __uint_as_float(h[j] << 16);
+                    v[8 * q + 2 * j + 1] = __uint_as_float(h[j] & 0xffff0000u);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 32; i++) v[i] = 0.f;
+        }
+        *mx_scale_slot(a.scl, tile, s, a.kpad, lane) = (uint16_t)mx_split_block(v, mx_rec(a.frag, tile, s, a.kpad), lane);
+    }
 }
 
 // The first 56 bytes arrive in SGPRs (KPre).
@@ -521,22 +628,63 @@ static MxFn mx_kernel_fn(size_t &lds) {
     return mx_matmul_kernel<CT>;
 }
 
+// The workspace: the code records of every (tile, step), then the scale
+// words of every (tile, stage).
+struct MxSplitLayout {
+    uint32_t ksteps, tiles, kpad;
+    uint8_t *frag, *scl;
+};
+static MxSplitLayout mx_layout(uint32_t m, uint32_t k, void *workspace) {
+    MxSplitLayout l;
+    l.ksteps = (k + 63) / 64;
+    l.tiles = (m + 31) / 32;
+    l.kpad = (l.ksteps + MX_STAGE - 1) / MX_STAGE * MX_STAGE;
+    l.frag = (uint8_t *)workspace;
+    l.scl = l.frag + (uint64_t)l.tiles * l.kpad * MX_REC;
+    return l;
+}
+
+int mx_norm_split_launch(const void *x, const float *w, void *y, uint32_t m, uint32_t k, float epsilon,
+                         bool full_layer, void *workspace, hipStream_t stream) {
+    const MxSplitLayout l = mx_layout(m, k, workspace);
+    MxNormSplitArgs a;
+    a.x = (const uint16_t *)x;
+    a.w = w;
+    a.y = (uint16_t *)y;
+    a.frag = l.frag;
+    a.scl = l.scl;
+    a.m = m;
+    a.k = k;
+    a.kpad = l.kpad;
+    a.full_layer = full_layer ? 1u : 0u;
+    a.epsilon = epsilon;
+    const size_t lds = (size_t)k * 2;
+    if (lds > 64 * 1024)
+        OCO_TRY(hip_check(hipFuncSetAttribute((const void *)mx_norm_split_kernel,
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+                          "hipFuncSetAttribute"));
+    hipLaunchKernelGGL(mx_norm_split_kernel, dim3(l.tiles * 32), dim3(256), lds, stream, a);
+    return launch_check("oco_norm_mx_split");
+}
+
 int mx_matmul_launch(const void *w, const void *x, void *y, bool y_bf16, const float *bias, uint32_t m, uint32_t n,
-                     uint32_t k, void *workspace, hipStream_t stream) {
-    const uint32_t ksteps = (k + 63) / 64, tiles = (m + 31) / 32;
-    const uint32_t kpad = (ksteps + MX_STAGE - 1) / MX_STAGE * MX_STAGE;
+                     uint32_t k, void *workspace, hipStream_t stream, bool presplit) {
+    const MxSplitLayout l = mx_layout(m, k, workspace);
+    const uint32_t ksteps = l.ksteps, tiles = l.tiles, kpad = l.kpad;
+    uint8_t *const frag = l.frag, *const scl = l.scl;
     const MxTilePlan plan = mx_plan(m, n);
-    uint8_t *const frag = (uint8_t *)workspace, *const scl = frag + (uint64_t)tiles * kpad * MX_REC;
-    MxSplitArgs sa;
-    sa.x = (const uint16_t *)x;
-    sa.frag = frag;
-    sa.scl = scl;
-    sa.m = m;
-    sa.k = k;
-    sa.kpad = kpad;
-    sa.records = tiles * kpad;
-    hipLaunchKernelGGL(mx_split_kernel, dim3(sa.records), dim3(64), 0, stream, KPRE_ARGS(sa), sa);
-    OCO_TRY(launch_check("oco_matmul (mx split)"));
+    if (!presplit) {
+        MxSplitArgs sa;
+        sa.x = (const uint16_t *)x;
+        sa.frag = frag;
+        sa.scl = scl;
+        sa.m = m;
+        sa.k = k;
+        sa.kpad = kpad;
+        sa.records = tiles * kpad;
+        hipLaunchKernelGGL(mx_split_kernel, dim3(sa.records), dim3(64), 0, stream, KPRE_ARGS(sa), sa);
+        OCO_TRY(launch_check("oco_matmul (mx split)"));
+    }
     size_t lds = 0;
     MxFn fn = mx_kernel_fn<3>(lds);
     if (lds > 64 * 1024)

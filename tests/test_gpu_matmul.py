@@ -331,3 +331,39 @@ def test_matmul_f16_input_unaligned(lib):
     wn = synth.weights(P.Q8_0, n, k, seed=61)
     half, mag = O.matmul_reference(P.Q8_0, wn, x16.reshape(m, k), n, k, half_operands=True)
     assert np.all(np.abs(got - half) <= O.roundoff_bound(half, mag, k, False))
+
+
+@pytest.mark.parametrize("m,k,full,offset", [(1, 2880, 1, 0), (45, 160, 0, 0), (130, 2880, 1, 2), (512, 2880, 0, 0),
+                                             (33, 4128, 1, 0)])
+def test_norm_mx_split_equals_norm_then_matmul(lib, m, k, full, offset):
+    """The fused norm + split, then the MXFP4 prefill from the split: the
+    normalised rows and the product bit-identical to oco_norm then
+    oco_matmul (k % 64 == 32 and a partial last stage included; x at a
+    2-byte offset once; without the bf16 rows once)."""
+    from oco_amd import synth
+    n, eps = 200, 1e-5
+    say("norm mx split", m, k, full, offset)
+    rng = np.random.default_rng(m + k)
+    w = lib.DeviceBuffer.from_array(synth.weights(39, n, k, seed=71))
+    xs = synth.bf16_bits((synth.activations(72, m * k) * 3.0).astype(np.float32))
+    xb = lib.DeviceBuffer(m * k * 2 + 16)
+    xb.upload(xs, offset)
+    nw = lib.DeviceBuffer.from_array(rng.normal(1.0, 0.2, k).astype(np.float32))
+    p = lib.Matrix(k, n, m, 0, 1, 1, 0)
+    xn = lib.DeviceBuffer(m * k * 2)
+    y1 = lib.DeviceBuffer(m * n * 2)
+    lib.norm(xb.ptr + offset, nw, xn, m, k, eps, bool(full))
+    lib.matmul(39, w, xn, y1, p, y_dtype=lib.DType.BF16)
+    need = lib.matmul_workspace(39, p)
+    split = lib.DeviceBuffer(need)
+    split.fill32(0xdeadbeef)  # the fused kernel writes every byte the product reads
+    yn = lib.DeviceBuffer(m * k * 2)
+    y2 = lib.DeviceBuffer(m * n * 2)
+    lib.norm_mx_split(xb.ptr + offset, nw, yn if m != 1 else None, m, k, eps, bool(full), split, need)
+    lib.matmul_mx_split(w, split, need, y2, p, y_dtype=lib.DType.BF16)
+    lib.synchronize()
+    if m != 1:
+        assert np.array_equal(yn.download(np.uint16, m * k), xn.download(np.uint16, m * k))
+    assert np.array_equal(y2.download(np.uint16, m * n), y1.download(np.uint16, m * n))
+    with pytest.raises(RuntimeError):
+        lib.norm_mx_split(xb, nw, None, m, k, eps, bool(full), split, need - 1)
