@@ -260,8 +260,16 @@ int oco_matmul_ws(uint32_t format, const void *w, const void *x, oco_dtype x_dty
 int oco_norm_mx_split(const void *x, const float *norm_w, void *y, uint32_t rows, uint32_t n, float epsilon,
                       int full_layer, void *split, uint64_t split_bytes, oco_stream stream);
 
+/* oco_add_norm (x = bf16(x + y) in place, then the norm; `out` optional)
+ * writing the same split records: the residual add -> norm -> MXFP4 prefill
+ * of a layer step in two launches.  Replaces add_norm
+ * (elementwise.metal:32-58) feeding apply_norm (compute/matrix.rs:429-441). */
+int oco_add_norm_mx_split(void *x, const void *y, const float *norm_w, void *out, uint32_t rows, uint32_t n,
+                          float epsilon, int full_layer, void *split, uint64_t split_bytes, oco_stream stream);
+
 /* oco_matmul for MXFP4 weights from rows already split by oco_norm_mx_split
- * (the same m and k): equal to oco_norm then oco_matmul, bit for bit. */
+ * or oco_add_norm_mx_split (the same m and k): equal to the norm then
+ * oco_matmul, bit for bit. */
 int oco_matmul_mx_split(const void *w, const void *split, uint64_t split_bytes, void *y, oco_dtype y_dtype,
                         const float *bias, const oco_matrix *p, oco_stream stream);
 

@@ -163,6 +163,7 @@ SIGNATURES = {
     "oco_matmul_workspace": (_u64, [_u32, _i32, _MP]),
     "oco_matmul_ws": (_i32, [_u32, _vp, _vp, _i32, _vp, _i32, _vp, _MP, _vp, _u64, _vp]),
     "oco_norm_mx_split": (_i32, [_vp, _vp, _vp, _u32, _u32, ctypes.c_float, _i32, _vp, _u64, _vp]),
+    "oco_add_norm_mx_split": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, ctypes.c_float, _i32, _vp, _u64, _vp]),
     "oco_matmul_mx_split": (_i32, [_vp, _vp, _u64, _vp, _i32, _vp, _MP, _vp]),
     "oco_route_select": (_i32, [_vp, _u32, _u32, _u32, _vp, _vp, _vp]),
     "oco_router": (_i32, [_vp, _i32, _vp, _vp, _u32, _u32, _u32, _u32, _vp, _vp, _vp, _vp]),
@@ -463,6 +464,14 @@ def norm_mx_split(x, w, y, rows: int, n: int, epsilon: float, full_layer: bool, 
     _check(load_library().oco_norm_mx_split(_addr(x), _addr(w), _addr(y), rows, n, float(epsilon),
                                             1 if full_layer else 0, _addr(split), int(split_bytes),
                                             _stream(stream)))
+
+
+def add_norm_mx_split(x, y, w, out, rows: int, n: int, epsilon: float, full_layer: bool, split, split_bytes: int,
+                      stream=None):
+    """oco_add_norm_mx_split: x = bf16(x + y), then norm_mx_split of x (out optional)."""
+    _check(load_library().oco_add_norm_mx_split(_addr(x), _addr(y), _addr(w), _addr(out), rows, n, float(epsilon),
+                                                1 if full_layer else 0, _addr(split), int(split_bytes),
+                                                _stream(stream)))
 
 
 def matmul_mx_split(w, split, split_bytes: int, y, p: Matrix, y_dtype=DType.F32, bias=None, stream=None):

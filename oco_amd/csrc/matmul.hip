@@ -761,7 +761,7 @@ static int vendor_matmul(uint32_t format, const void *w, const void *x, oco_dtyp
 uint64_t mx_workspace_bytes(uint32_t m, uint32_t n, uint32_t k);
 int mx_matmul_launch(const void *w, const void *x, void *y, bool y_bf16, const float *bias, uint32_t m, uint32_t n,
                      uint32_t k, void *workspace, hipStream_t stream, bool presplit = false);
-int mx_norm_split_launch(const void *x, const float *w, void *y, uint32_t m, uint32_t k, float epsilon,
+int mx_norm_split_launch(void *x, const void *res, const float *w, void *y, uint32_t m, uint32_t k, float epsilon,
                          bool full_layer, void *workspace, hipStream_t stream);
 
 // MXFP4 goes to the block-scaled FP8 x FP4 MFMA unless the
@@ -869,19 +869,34 @@ extern "C" int oco_matmul(uint32_t format, const void *w, const void *x, oco_dty
     return rc != OCO_OK ? rc : rf;
 }
 
+static int norm_split_check(const char *who, uint32_t rows, uint32_t n, uint64_t split_bytes) {
+    if (n == 0 || n % 32) return fail(OCO_ERR_INVALID, "%s: n=%u is not whole 32-blocks", who, n);
+    if (n > 65536) return fail(OCO_ERR_UNSUPPORTED, "%s: n=%u past 65536 (the row is staged in LDS)", who, n);
+    if (rows > 0x7fffffe0u) return fail(OCO_ERR_INVALID, "%s: %u rows", who, rows);
+    const uint64_t need = mx_workspace_bytes(rows, 0, n);
+    if (split_bytes < need)
+        return fail(OCO_ERR_INVALID, "%s: split buffer of %llu bytes, need %llu", who,
+                    (unsigned long long)split_bytes, (unsigned long long)need);
+    return OCO_OK;
+}
+
 extern "C" int oco_norm_mx_split(const void *x, const float *norm_w, void *y, uint32_t rows, uint32_t n,
                                  float epsilon, int full_layer, void *split, uint64_t split_bytes,
                                  oco_stream stream) {
     if (rows == 0) return OCO_OK;
     if (!x || !norm_w || !split) return fail(OCO_ERR_INVALID, "oco_norm_mx_split: null pointer");
-    if (n == 0 || n % 32) return fail(OCO_ERR_INVALID, "oco_norm_mx_split: n=%u is not whole 32-blocks", n);
-    if (n > 65536) return fail(OCO_ERR_UNSUPPORTED, "oco_norm_mx_split: n=%u past 65536 (the row is staged in LDS)", n);
-    if (rows > 0x7fffffe0u) return fail(OCO_ERR_INVALID, "oco_norm_mx_split: %u rows", rows);
-    const uint64_t need = mx_workspace_bytes(rows, 0, n);
-    if (split_bytes < need)
-        return fail(OCO_ERR_INVALID, "oco_norm_mx_split: split buffer of %llu bytes, need %llu",
-                    (unsigned long long)split_bytes, (unsigned long long)need);
-    return mx_norm_split_launch(x, norm_w, y, rows, n, epsilon, full_layer != 0, split, (hipStream_t)stream);
+    OCO_TRY(norm_split_check("oco_norm_mx_split", rows, n, split_bytes));
+    return mx_norm_split_launch(const_cast<void *>(x), nullptr, norm_w, y, rows, n, epsilon, full_layer != 0, split,
+                                (hipStream_t)stream);
+}
+
+extern "C" int oco_add_norm_mx_split(void *x, const void *y, const float *norm_w, void *out, uint32_t rows,
+                                     uint32_t n, float epsilon, int full_layer, void *split, uint64_t split_bytes,
+                                     oco_stream stream) {
+    if (rows == 0) return OCO_OK;
+    if (!x || !y || !norm_w || !split) return fail(OCO_ERR_INVALID, "oco_add_norm_mx_split: null pointer");
+    OCO_TRY(norm_split_check("oco_add_norm_mx_split", rows, n, split_bytes));
+    return mx_norm_split_launch(x, y, norm_w, out, rows, n, epsilon, full_layer != 0, split, (hipStream_t)stream);
 }
 
 extern "C" int oco_matmul_mx_split(const void *w, const void *split, uint64_t split_bytes, void *y, oco_dtype y_dtype,

@@ -166,7 +166,8 @@ __global__ __launch_bounds__(64) void mx_split_kernel(KPRE_PARAMS, MxSplitArgs a
 // normalised bf16 row, so the records are bit for bit the split of
 // oco_norm's output.  `y`, when set, receives that bf16 row too.
 struct MxNormSplitArgs {
-    const uint16_t *x;
+    uint16_t *x;
+    const uint16_t *res;  // add form: the rows added into x first
     const float *w;
     uint16_t *y;
     uint8_t *frag, *scl;
@@ -174,13 +175,20 @@ struct MxNormSplitArgs {
     float epsilon;
 };
 
+template <bool ADD>
 __global__ __launch_bounds__(256) void mx_norm_split_kernel(MxNormSplitArgs a) {
     __shared__ float partial[4];
     extern __shared__ __attribute__((aligned(16))) uint16_t nrow[];  // the normalised row, bf16 [k]
     const uint32_t row = blockIdx.x, tile = row / 32, r = row % 32;
     const bool live = row < a.m;  // uniform
-    const uint16_t *xr = a.x + (uint64_t)row * a.k;
+    uint16_t *xr = a.x + (uint64_t)row * a.k;
     if (live) {
+        if constexpr (ADD) {  // the residual stream takes bf16(x + y) first, as oco_add_norm
+            const uint16_t *yr = a.res + (uint64_t)row * a.k;
+            for (uint32_t i = threadIdx.x; i < a.k; i += 256)
+                xr[i] = f32_to_bf16_bits(bf16_bits_to_f32(xr[i]) + bf16_bits_to_f32(yr[i]));
+            __syncthreads();
+        }
         const float inv = block_inv_rms(xr, a.k, a.epsilon, partial);
         // eight consecutive values per thread, coalesced, into LDS (and y)
         uint16_t *yr = a.y ? a.y + (uint64_t)row * a.k : nullptr;
@@ -644,11 +652,12 @@ static MxSplitLayout mx_layout(uint32_t m, uint32_t k, void *workspace) {
     return l;
 }
 
-int mx_norm_split_launch(const void *x, const float *w, void *y, uint32_t m, uint32_t k, float epsilon,
+int mx_norm_split_launch(void *x, const void *res, const float *w, void *y, uint32_t m, uint32_t k, float epsilon,
                          bool full_layer, void *workspace, hipStream_t stream) {
     const MxSplitLayout l = mx_layout(m, k, workspace);
     MxNormSplitArgs a;
-    a.x = (const uint16_t *)x;
+    a.x = (uint16_t *)x;
+    a.res = (const uint16_t *)res;
     a.w = w;
     a.y = (uint16_t *)y;
     a.frag = l.frag;
@@ -659,11 +668,11 @@ int mx_norm_split_launch(const void *x, const float *w, void *y, uint32_t m, uin
     a.full_layer = full_layer ? 1u : 0u;
     a.epsilon = epsilon;
     const size_t lds = (size_t)k * 2;
+    auto fn = res ? mx_norm_split_kernel<true> : mx_norm_split_kernel<false>;
     if (lds > 64 * 1024)
-        OCO_TRY(hip_check(hipFuncSetAttribute((const void *)mx_norm_split_kernel,
-                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+        OCO_TRY(hip_check(hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
                           "hipFuncSetAttribute"));
-    hipLaunchKernelGGL(mx_norm_split_kernel, dim3(l.tiles * 32), dim3(256), lds, stream, a);
+    hipLaunchKernelGGL(fn, dim3(l.tiles * 32), dim3(256), lds, stream, a);
     return launch_check("oco_norm_mx_split");
 }
 

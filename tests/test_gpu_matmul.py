@@ -367,3 +367,31 @@ def test_norm_mx_split_equals_norm_then_matmul(lib, m, k, full, offset):
     assert np.array_equal(y2.download(np.uint16, m * n), y1.download(np.uint16, m * n))
     with pytest.raises(RuntimeError):
         lib.norm_mx_split(xb, nw, None, m, k, eps, bool(full), split, need - 1)
+
+
+@pytest.mark.parametrize("m,k", [(45, 160), (130, 2880)])
+def test_add_norm_mx_split_equals_add_norm_then_matmul(lib, m, k):
+    """The residual add form: x updated in place, the normalised rows and the
+    product bit-identical to oco_add_norm then oco_matmul."""
+    from oco_amd import synth
+    n, eps = 136, 1e-6
+    rng = np.random.default_rng(k)
+    w = lib.DeviceBuffer.from_array(synth.weights(39, n, k, seed=81))
+    xs = synth.bf16_bits(synth.activations(82, m * k).astype(np.float32))
+    ys = synth.bf16_bits((synth.activations(83, m * k) * 0.5).astype(np.float32))
+    nw = lib.DeviceBuffer.from_array(rng.normal(1.0, 0.2, k).astype(np.float32))
+    p = lib.Matrix(k, n, m, 0, 1, 1, 0)
+    x1, x2 = lib.DeviceBuffer.from_array(xs), lib.DeviceBuffer.from_array(xs)
+    yb = lib.DeviceBuffer.from_array(ys)
+    o1, o2 = lib.DeviceBuffer(m * k * 2), lib.DeviceBuffer(m * k * 2)
+    p1, p2 = lib.DeviceBuffer(m * n * 4), lib.DeviceBuffer(m * n * 4)
+    lib.add_norm(x1, yb, nw, o1, m, k, eps, False)
+    lib.matmul(39, w, o1, p1, p)
+    need = lib.matmul_workspace(39, p)
+    split = lib.DeviceBuffer(need)
+    lib.add_norm_mx_split(x2, yb, nw, o2, m, k, eps, False, split, need)
+    lib.matmul_mx_split(w, split, need, p2, p)
+    lib.synchronize()
+    assert np.array_equal(x2.download(np.uint16, m * k), x1.download(np.uint16, m * k))
+    assert np.array_equal(o2.download(np.uint16, m * k), o1.download(np.uint16, m * k))
+    assert np.array_equal(p2.download(np.uint32, m * n), p1.download(np.uint32, m * n))
