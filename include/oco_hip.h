@@ -235,7 +235,13 @@ int oco_matvec_relu_sqr(uint32_t format, const void *w, const void *x, oco_dtype
  * two E2M3 terms with their own E8M0 scales (at most 1/225 of the block
  * maximum per value; relative L2 of the product a few 1e-4, inside the 2e-3
  * bound for bf16-activation MFMA prefill), also through a workspace.
- * oco_matmul takes workspaces from the stream-ordered pool (hipMallocAsync). */
+ * oco_matmul takes workspaces from the stream-ordered pool (hipMallocAsync).
+ * With bf16 X, up to Builder::dense's vector_rows rows (pipelines.rs:271-283:
+ * 1; 4 for Q4_0/Q4_1 and three Q5_K/Q8_0 shapes; 128 for Q8_0 2880 -> 512;
+ * every m for F32 with n <= 128) run oco_matvec instead, exact weights and
+ * fp32, as DenseMatrix::apply does; Q4_0/Q4_1 with n > 1024 scale each
+ * activation row by the reference's power-of-two gain before the f16
+ * rounding (matmul_q4_half). */
 int oco_matmul(uint32_t format, const void *w, const void *x, oco_dtype x_dtype, void *y,
                oco_dtype y_dtype, const float *bias, const oco_matrix *p, oco_stream stream);
 
@@ -269,7 +275,8 @@ int oco_add_norm_mx_split(void *x, const void *y, const float *norm_w, void *out
 
 /* oco_matmul for MXFP4 weights from rows already split by oco_norm_mx_split
  * or oco_add_norm_mx_split (the same m and k): equal to the norm then
- * oco_matmul, bit for bit. */
+ * oco_matmul, bit for bit, from two rows on (one row takes oco_matmul's
+ * matvec; this entry always runs the block-scaled MFMA). */
 int oco_matmul_mx_split(const void *w, const void *split, uint64_t split_bytes, void *y, oco_dtype y_dtype,
                         const float *bias, const oco_matrix *p, oco_stream stream);
 

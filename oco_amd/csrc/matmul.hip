@@ -598,16 +598,41 @@ __global__ __launch_bounds__(256) void operand_kernel(const uint8_t *w, uint64_t
         *reinterpret_cast<uint4 *>(dst + col0[q]) = make_uint4(out[4 * q], out[4 * q + 1], out[4 * q + 2], out[4 * q + 3]);
 }
 
-// y[m, n] = acc + bf16(bias), as f32 or bf16: four columns per thread.
-__global__ __launch_bounds__(256) void gemm_epilogue_kernel(const float *acc, const float *bias, void *y, bool y_bf16,
-                                                            uint32_t n, uint64_t quads) {
+// The scaled Q4_0 / Q4_1 tiles' activations (q4_input_scales and the
+// staging of matmul_q4_half: batch.metal:44-68, q4_tile.metal:44-49, 90-93):
+// per row a power-of-two gain from the exponent e of its max |x|,
+// 2^clamp(141 - e, -120, 120) (1 for a zero row), and the operands
+// half(x * gain); `inv` receives 1 / gain for the epilogue.  One
+// 256-thread workgroup per row.
+__global__ __launch_bounds__(256) void row_gain_f16_kernel(const uint16_t *x, uint16_t *xo, float *inv, uint32_t k) {
+    __shared__ float peaks[4];
+    const uint16_t *xr = x + (uint64_t)blockIdx.x * k;
+    uint16_t *orow = xo + (uint64_t)blockIdx.x * k;
+    float peak = 0.f;
+    for (uint32_t i = threadIdx.x; i < k; i += 256) peak = fmaxf(peak, fabsf(bf16_bits_to_f32(xr[i])));
+    for (int o = 32; o >= 1; o >>= 1) peak = fmaxf(peak, __shfl_xor(peak, o));
+    if ((threadIdx.x & 63) == 0) peaks[threadIdx.x >> 6] = peak;
+    __syncthreads();
+    peak = fmaxf(fmaxf(peaks[0], peaks[1]), fmaxf(peaks[2], peaks[3]));
+    const int e = (int)((__float_as_uint(peak) >> 23) & 255u);
+    const int shift = peak == 0.f ? 0 : min(max(141 - e, -120), 120);
+    const float gain = __uint_as_float((uint32_t)(127 + shift) << 23);
+    if (threadIdx.x == 0) inv[blockIdx.x] = __uint_as_float((uint32_t)(127 - shift) << 23);
+    for (uint32_t i = threadIdx.x; i < k; i += 256) orow[i] = operand_bits<false>(bf16_bits_to_f32(xr[i]) * gain);
+}
+
+// y[m, n] = acc (* 1 / row gain) + bf16(bias), as f32 or bf16: four columns
+// per thread.
+__global__ __launch_bounds__(256) void gemm_epilogue_kernel(const float *acc, const float *bias, const float *inv_gain,
+                                                            void *y, bool y_bf16, uint32_t n, uint64_t quads) {
     const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= quads) return;
     const uint32_t col = (uint32_t)(4 * i % n);
+    const float g = inv_gain ? inv_gain[4 * i / n] : 1.0f;
     const float4 v = *reinterpret_cast<const float4 *>(acc + 4 * i);
     float r[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-    for (int j = 0; j < 4; j++) r[j] += bias ? round_bf16(bias[col + j]) : 0.f;
+    for (int j = 0; j < 4; j++) r[j] = r[j] * g + (bias ? round_bf16(bias[col + j]) : 0.f);
     if (y_bf16)
         *reinterpret_cast<uint2 *>(reinterpret_cast<uint16_t *>(y) + 4 * i) =
             make_uint2(pack2(f32_to_bf16_bits(r[0]), f32_to_bf16_bits(r[1])),
@@ -689,23 +714,32 @@ static bool vendor_format(uint32_t format) {
 // on the box at 32..256 rows: as fast or faster for Q4_K 12288 x 4096, 2-3x
 // for Q8_0 4096 x 4096 and Q6_K 4096 x 12288), unless the
 // OCO_KNOB_MATMUL_VENDOR override chooses.
-static bool use_vendor(uint32_t format, uint32_t m) {
+// The reference scales Q4_0 / Q4_1 activation rows by a power-of-two gain
+// when the matrix has more than 1024 outputs (pipelines.rs:286-288); only
+// the vendor path implements it, so those shapes take it at every tiled m.
+// (f16 activations, which the reference does not take, are used as given.)
+static bool q4_gain(uint32_t format, uint32_t n, oco_dtype x_dtype) {
+    return (format == OCO_Q4_0 || format == OCO_Q4_1) && n > 1024 && x_dtype == OCO_DT_BF16;
+}
+
+static bool use_vendor(uint32_t format, uint32_t m, uint32_t n, oco_dtype x_dtype) {
     if (!vendor_format(format)) return false;
     int32_t ov[4];
     if (plan_override(OCO_KNOB_MATMUL_VENDOR, ov)) return ov[0] != 0;
-    return m >= 32;
+    return m >= 32 || q4_gain(format, n, x_dtype);
 }
 
 struct VendorLayout {
-    uint64_t w, x, d, blas, total;  // byte offsets in the workspace, and its size
+    uint64_t w, x, d, gain, blas, total;  // byte offsets in the workspace, and its size
 };
 static VendorLayout vendor_layout(uint32_t format, oco_dtype x_dtype, uint32_t m, uint32_t n, uint32_t k, uint64_t blas_ws) {
     auto al = [](uint64_t b) { return (b + 255) & ~255ull; };
     VendorLayout v;
     v.w = 0;
     v.x = v.w + (format == OCO_F16 ? 0 : al((uint64_t)n * k * 2));
-    v.d = v.x + (x_dtype == OCO_DT_F16 ? 0 : al((uint64_t)m * k * 2));
-    v.blas = v.d + al((uint64_t)m * n * 4);
+    v.d = v.x + (x_dtype == OCO_DT_F16 && !q4_gain(format, n, x_dtype) ? 0 : al((uint64_t)m * k * 2));
+    v.gain = v.d + al((uint64_t)m * n * 4);
+    v.blas = v.gain + (q4_gain(format, n, x_dtype) ? al((uint64_t)m * 4) : 0);
     v.total = v.blas + blas_ws;
     return v;
 }
@@ -729,10 +763,16 @@ static int vendor_matmul(uint32_t format, const void *w, const void *x, oco_dtyp
         return fail(OCO_ERR_INVALID, "oco_matmul_ws: workspace of %llu bytes, need %llu",
                     (unsigned long long)workspace_bytes, (unsigned long long)v.total);
     uint8_t *ws = (uint8_t *)workspace;
+    const bool gain = q4_gain(format, n, x_dtype);
     uint16_t *wo = format == OCO_F16 ? nullptr : (uint16_t *)(ws + v.w);
-    uint16_t *xo = x_dtype == OCO_DT_F16 ? nullptr : (uint16_t *)(ws + v.x);
-    const uint64_t xchunks = xo ? (uint64_t)m * k / 8 : 0;
-    if (wo || xo) {
+    uint16_t *xo = x_dtype == OCO_DT_F16 && !gain ? nullptr : (uint16_t *)(ws + v.x);
+    float *inv = gain ? (float *)(ws + v.gain) : nullptr;
+    const uint64_t xchunks = xo && !gain ? (uint64_t)m * k / 8 : 0;
+    if (gain) {
+        hipLaunchKernelGGL(row_gain_f16_kernel, dim3(m), dim3(256), 0, stream, (const uint16_t *)x, xo, inv, k);
+        OCO_TRY(launch_check("oco_matmul: row gains"));
+    }
+    if (wo || xchunks) {
         const uint64_t rb = oco_row_bytes(format, k);
         switch (format) {
 #define CASE(F) case F: operand_launch<F>(w, rb, n, k, wo, x, xo, xchunks, stream); break;
@@ -742,7 +782,7 @@ static int vendor_matmul(uint32_t format, const void *w, const void *x, oco_dtyp
         }
         OCO_TRY(launch_check("oco_matmul: operand pass"));
     }
-    const bool direct = y_dtype == OCO_DT_F32 && !(p->has_bias && bias);
+    const bool direct = y_dtype == OCO_DT_F32 && !(p->has_bias && bias) && !gain;
     float *acc = direct ? (float *)y : (float *)(ws + v.d);
     const float alpha = 1.0f, beta = 0.0f;
     const hipblasStatus_t st = hipblasLtMatmul(pl.handle, pl.desc, &alpha, wo ? (const void *)wo : w, pl.a,
@@ -752,7 +792,7 @@ static int vendor_matmul(uint32_t format, const void *w, const void *x, oco_dtyp
     if (!direct) {
         const uint64_t quads = (uint64_t)m * n / 4;
         hipLaunchKernelGGL(gemm_epilogue_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, stream, acc,
-                           p->has_bias ? bias : nullptr, y, y_dtype == OCO_DT_BF16, n, quads);
+                           p->has_bias ? bias : nullptr, inv, y, y_dtype == OCO_DT_BF16, n, quads);
         OCO_TRY(launch_check("oco_matmul: epilogue"));
     }
     return OCO_OK;
@@ -819,17 +859,37 @@ static int matmul_decode_launch(uint32_t format, const void *w, const void *x, o
 
 using namespace oco;
 
+// Builder::dense's vector_rows (pipelines.rs:271-283): a product of at most
+// this many rows runs the decode matvec on each row (exact weights, fp32
+// accumulation), as DenseMatrix::apply does (compute/matrix.rs:174-200).
+// F32 matrices of at most 128 outputs stay on it at every m: the reference
+// keeps them in exact fp32 either way (vector, or its tensor tiles' fp32
+// staging), which only the matvec does here.
+static uint32_t vector_rows(uint32_t format, uint32_t k, uint32_t n) {
+    switch (format) {
+    case OCO_Q4_0:
+    case OCO_Q4_1: return 4;
+    case OCO_Q5_K: return k == 6144 && n == 5120 ? 4 : 1;
+    case OCO_Q8_0: return k == 2880 && n == 512 ? 128 : (k == 2880 && n == 4096) || (k == 4096 && n == 2880) ? 4 : 1;
+    case OCO_F32: return n <= 128 ? 0xffffffffu : 1;
+    }
+    return 1;
+}
+static bool as_matvec(uint32_t format, oco_dtype x_dtype, const oco_matrix *p) {
+    return x_dtype == OCO_DT_BF16 && p->m <= vector_rows(format, p->k, p->n);
+}
+
 // The vendor path needs n % 4 == 0 (the epilogue's four columns per thread).
-static const BlasPlan *vendor_plan(uint32_t format, const oco_matrix *p) {
-    if (!use_vendor(format, p->m) || p->n % 4 || p->m == 0 || p->n == 0) return nullptr;
+static const BlasPlan *vendor_plan(uint32_t format, oco_dtype x_dtype, const oco_matrix *p) {
+    if (!use_vendor(format, p->m, p->n, x_dtype) || p->n % 4 || p->m == 0 || p->n == 0) return nullptr;
     const BlasPlan &pl = blas_plan(p->m, p->n, p->k);
     return pl.ok ? &pl : nullptr;
 }
 
 extern "C" uint64_t oco_matmul_workspace(uint32_t format, oco_dtype x_dtype, const oco_matrix *p) {
-    if (!p) return 0;
+    if (!p || as_matvec(format, x_dtype, p)) return 0;
     if (use_mx(format)) return mx_workspace_bytes(p->m, p->n, p->k);
-    if (const BlasPlan *pl = vendor_plan(format, p)) return vendor_layout(format, x_dtype, p->m, p->n, p->k, pl->ws).total;
+    if (const BlasPlan *pl = vendor_plan(format, x_dtype, p)) return vendor_layout(format, x_dtype, p->m, p->n, p->k, pl->ws).total;
     return 0;
 }
 
@@ -838,6 +898,7 @@ extern "C" int oco_matmul_ws(uint32_t format, const void *w, const void *x, oco_
                              uint64_t workspace_bytes, oco_stream stream) {
     OCO_TRY(matmul_check(format, w, x, x_dtype, y, y_dtype, bias, p));
     if (p->m == 0 || p->n == 0) return OCO_OK;
+    if (as_matvec(format, x_dtype, p)) return oco_matvec(format, w, x, x_dtype, y, y_dtype, bias, nullptr, p, stream);
     if (use_mx(format)) {
         const uint64_t need = mx_workspace_bytes(p->m, p->n, p->k);
         if (!workspace || workspace_bytes < need)
@@ -850,7 +911,7 @@ extern "C" int oco_matmul_ws(uint32_t format, const void *w, const void *x, oco_
     // 16-byte aligned for it; otherwise the fused tiles run.
     const bool aligned = (format != OCO_F16 || ((uintptr_t)w & 15) == 0) &&
                          (x_dtype != OCO_DT_F16 || ((uintptr_t)x & 15) == 0);
-    if (const BlasPlan *pl = aligned ? vendor_plan(format, p) : nullptr)
+    if (const BlasPlan *pl = aligned ? vendor_plan(format, x_dtype, p) : nullptr)
         return vendor_matmul(format, w, x, x_dtype, y, y_dtype, bias, p, *pl, workspace, workspace_bytes,
                              (hipStream_t)stream);
     return matmul_decode_launch(format, w, x, x_dtype, y, y_dtype, bias, p, (hipStream_t)stream);
@@ -860,6 +921,7 @@ extern "C" int oco_matmul(uint32_t format, const void *w, const void *x, oco_dty
                           oco_dtype y_dtype, const float *bias, const oco_matrix *p, oco_stream stream) {
     OCO_TRY(matmul_check(format, w, x, x_dtype, y, y_dtype, bias, p));
     if (p->m == 0 || p->n == 0) return OCO_OK;
+    if (as_matvec(format, x_dtype, p)) return oco_matvec(format, w, x, x_dtype, y, y_dtype, bias, nullptr, p, stream);
     const uint64_t need = oco_matmul_workspace(format, x_dtype, p);
     if (!need) return matmul_decode_launch(format, w, x, x_dtype, y, y_dtype, bias, p, (hipStream_t)stream);
     void *ws = nullptr;

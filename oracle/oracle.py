@@ -316,16 +316,33 @@ def experts_reference(fmt, hidden, ffn, gate, up, down, x, ids, probs, residual_
     return {"gate": gat, "up": upv, "up_mag": mag_up, "act": act, "down": y, "down_mag": mag_y, "out": out}
 
 
-def matmul_reference(fmt, w, x, n, k, half_operands: bool):
+def q4_row_gain(peak: float) -> float:
+    """Power-of-two row gain of the scaled Q4 tiles (q4_tile.metal:44-49):
+    the f32 exponent e of the row's max |x| gives 2^clamp(141 - e, -120, 120),
+    1 for a zero row; x * gain is then rounded to half, and the product
+    multiplied by 1 / gain (batch.metal:44-68, 90-98)."""
+    bits = int(np.float32(peak).view(np.uint32))
+    e = (bits >> 23) & 255
+    shift = 0 if peak == 0.0 else min(max(141 - e, -120), 120)
+    return float(2.0 ** shift)
+
+
+def matmul_reference(fmt, w, x, n, k, half_operands: bool, row_gain: bool = False):
     """Y = X W^T in fp64 (matrix_precision.rs:119-142): optionally with both
     operands rounded to f16 first (the reference's tiled kernels' half(w),
-    half(x)), and sum |w x| for the roundoff bound."""
+    half(x)), and sum |w x| for the roundoff bound.  row_gain: each row
+    rounded as half(x * gain) / gain with q4_row_gain of its peak, as the
+    scaled Q4_0/Q4_1 tiles do."""
     W = dequant(fmt, w, n * k).astype(np.float64).reshape(n, k)
     x = np.asarray(x)
     X = bf16_to_f32(x).astype(np.float64) if x.dtype == np.uint16 else x.astype(np.float64)
     if half_operands:
         W = W.astype(np.float16).astype(np.float64)
-        X = X.astype(np.float16).astype(np.float64)
+        if row_gain:
+            g = np.array([q4_row_gain(float(np.abs(r).max())) for r in X])[:, None]
+            X = (X * g).astype(np.float16).astype(np.float64) / g
+        else:
+            X = X.astype(np.float16).astype(np.float64)
     return X @ W.T, np.abs(X) @ np.abs(W).T
 
 

@@ -35,6 +35,20 @@ def mx_split_bound(x_bits, w, n, k):
     return 2.0 ** -6 * (amax @ wsum.T)
 
 
+def vector_rows(fmt, k, n):
+    """Builder::dense's vector_rows (pipelines.rs:271-283): oco_matmul runs the
+    matvec (exact weights, fp32) up to this many bf16 rows."""
+    if fmt in (P.Q4_0, P.Q4_1):
+        return 4
+    if fmt == P.Q5_K:
+        return 4 if (k, n) == (6144, 5120) else 1
+    if fmt == P.Q8_0:
+        return 128 if (k, n) == (2880, 512) else 4 if (k, n) in ((2880, 4096), (4096, 2880)) else 1
+    if fmt == 0:
+        return 1 << 30 if n <= 128 else 1
+    return 1
+
+
 def run(oco, fmt, w, x, m, n, k, y_bf16=False, bias=None):
     wb = oco.DeviceBuffer.from_array(w)
     xb = oco.DeviceBuffer.from_array(x)
@@ -61,7 +75,11 @@ def test_matmul_reference_packer(lib, fmt, m):
         w = np.frombuffer(data, np.uint8)
     x = P.dense_input(m, k)
     got = run(lib, fmt, w, x, m, n, k)
-    exact, _ = O.matmul_reference(fmt, w, x, n, k, half_operands=False)
+    exact, emag = O.matmul_reference(fmt, w, x, n, k, half_operands=False)
+    if m <= vector_rows(fmt, k, n):  # the matvec: north_star's fp32 bar
+        assert rel_l2(got, exact) <= 1e-5
+        assert np.all(np.abs(got - exact) <= O.roundoff_bound(exact, emag, k, False))
+        return
     half, mag = O.matmul_reference(fmt, w, x, n, k, half_operands=(fmt != 39))
     assert rel_l2(got, exact) <= (MX_BAR if fmt == 39 else 2e-3)
     extra = mx_split_bound(x, w, n, k) if fmt == 39 else 0.0
@@ -105,7 +123,7 @@ def _mx_case(m, n, k, seed, scale_rows=None):
     return w, synth.bf16_bits(x.astype(np.float32)).reshape(m, k)
 
 
-@pytest.mark.parametrize("m,n,k", [(45, 70, 160), (1, 33, 32), (33, 65, 96), (130, 200, 2880)])
+@pytest.mark.parametrize("m,n,k", [(45, 70, 160), (2, 33, 32), (33, 65, 96), (130, 200, 2880)])
 def test_matmul_mxfp4_workspace_tail(lib, m, n, k):
     """Block-scaled MFMA path through oco_matmul_ws: K steps of 64 with a
     lone last block (k % 64 == 32), row/column tails, bias, bf16 output."""
@@ -333,7 +351,7 @@ def test_matmul_f16_input_unaligned(lib):
     assert np.all(np.abs(got - half) <= O.roundoff_bound(half, mag, k, False))
 
 
-@pytest.mark.parametrize("m,k,full,offset", [(1, 2880, 1, 0), (45, 160, 0, 0), (130, 2880, 1, 2), (512, 2880, 0, 0),
+@pytest.mark.parametrize("m,k,full,offset", [(2, 2880, 1, 0), (45, 160, 0, 0), (130, 2880, 1, 2), (512, 2880, 0, 0),
                                              (33, 4128, 1, 0)])
 def test_norm_mx_split_equals_norm_then_matmul(lib, m, k, full, offset):
     """The fused norm + split, then the MXFP4 prefill from the split: the
@@ -359,10 +377,10 @@ def test_norm_mx_split_equals_norm_then_matmul(lib, m, k, full, offset):
     split.fill32(0xdeadbeef)  # the fused kernel writes every byte the product reads
     yn = lib.DeviceBuffer(m * k * 2)
     y2 = lib.DeviceBuffer(m * n * 2)
-    lib.norm_mx_split(xb.ptr + offset, nw, yn if m != 1 else None, m, k, eps, bool(full), split, need)
+    lib.norm_mx_split(xb.ptr + offset, nw, yn if m != 2 else None, m, k, eps, bool(full), split, need)
     lib.matmul_mx_split(w, split, need, y2, p, y_dtype=lib.DType.BF16)
     lib.synchronize()
-    if m != 1:
+    if m != 2:
         assert np.array_equal(yn.download(np.uint16, m * k), xn.download(np.uint16, m * k))
     assert np.array_equal(y2.download(np.uint16, m * n), y1.download(np.uint16, m * n))
     with pytest.raises(RuntimeError):
@@ -395,3 +413,47 @@ def test_add_norm_mx_split_equals_add_norm_then_matmul(lib, m, k):
     assert np.array_equal(x2.download(np.uint16, m * k), x1.download(np.uint16, m * k))
     assert np.array_equal(o2.download(np.uint16, m * k), o1.download(np.uint16, m * k))
     assert np.array_equal(p2.download(np.uint32, m * n), p1.download(np.uint32, m * n))
+
+
+@pytest.mark.parametrize("fmt,m,n,k", [(P.Q4_0, 3, 64, 256), (P.Q4_1, 4, 96, 512), (39, 1, 70, 2880),
+                                       (P.Q8_0, 100, 512, 2880), (0, 200, 64, 96), (P.Q4_K, 1, 256, 512)])
+def test_matmul_vector_rows_take_the_matvec(lib, fmt, m, n, k):
+    """Up to the reference's vector_rows, oco_matmul is oco_matvec on each
+    row, bit for bit, with no workspace."""
+    from oco_amd import synth
+    say("matmul vector rows", fmt, m, n, k)
+    assert m <= vector_rows(fmt, k, n)
+    if fmt == 0:
+        w = np.frombuffer(np.random.default_rng(3).normal(0, 0.1, n * k).astype(np.float32).tobytes(), np.uint8)
+    else:
+        w = synth.weights(fmt, n, k, seed=91)
+    x = synth.bf16_bits(synth.activations(92, m * k))
+    p = lib.Matrix(k, n, m, 0, 1, 1, 0)
+    assert lib.matmul_workspace(fmt, p) == 0
+    wb, xb = lib.DeviceBuffer.from_array(w), lib.DeviceBuffer.from_array(x)
+    y1, y2 = lib.DeviceBuffer(m * n * 2), lib.DeviceBuffer(m * n * 2)
+    lib.matmul(fmt, wb, xb, y1, p, y_dtype=lib.DType.BF16)
+    lib.matvec(fmt, wb, xb, y2, p, x_dtype=lib.DType.BF16, y_dtype=lib.DType.BF16)
+    lib.synchronize()
+    assert np.array_equal(y1.download(np.uint16, m * n), y2.download(np.uint16, m * n))
+
+
+def test_matmul_q4_row_gain(lib):
+    """Q4_0 with more than 1024 outputs: each activation row is scaled by the
+    reference's power-of-two gain before the f16 rounding, so rows far
+    outside f16 range (2^20 and 2^-30 times N(0,1)) stay finite and within
+    the half-operand bound of the gained operands."""
+    from oco_amd import synth
+    m, n, k = 40, 1100, 256
+    w = synth.weights(P.Q4_0, n, k, seed=95)
+    xf = synth.activations(96, m * k).reshape(m, k).astype(np.float64)
+    xf[::3] *= 2.0 ** 20
+    xf[1::3] *= 2.0 ** -30
+    x = synth.bf16_bits(xf.astype(np.float32)).reshape(m, k)
+    got = run(lib, P.Q4_0, w, x, m, n, k)
+    assert np.all(np.isfinite(got))
+    half, mag = O.matmul_reference(P.Q4_0, w, x, n, k, half_operands=True, row_gain=True)
+    assert np.all(np.abs(got - half) <= O.roundoff_bound(half, mag, k, False))
+    exact, _ = O.matmul_reference(P.Q4_0, w, x, n, k, half_operands=False)
+    for r in range(m):  # each row within the bar of its own scale
+        assert rel_l2(got[r], exact[r]) <= 2e-3

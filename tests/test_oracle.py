@@ -460,3 +460,19 @@ def test_add_norm_is_add_then_norm():
     want_x = O.f32_to_bf16((O.bf16_to_f32(x) + O.bf16_to_f32(y)).astype(np.float32)).reshape(2, n)
     assert np.array_equal(xs, want_x)
     assert np.array_equal(out, O.norm(want_x, w, 1e-6, True)[0])
+
+
+def test_q4_row_gain_closed_form():
+    """The scaled Q4 tiles' gain (q4_tile.metal:44-49): 2^(141 - e) for the
+    peak's f32 exponent e, clamped to 2^+-120, 1 for a zero row; x * gain
+    then has its peak in [2^14, 2^15)."""
+    assert O.q4_row_gain(0.0) == 1.0
+    assert O.q4_row_gain(1.0) == 2.0 ** 14
+    assert O.q4_row_gain(1.5) == 2.0 ** 14
+    assert O.q4_row_gain(2.0 ** 14) == 1.0
+    assert O.q4_row_gain(32767.0) == 1.0
+    assert O.q4_row_gain(2.0 ** 15) == 0.5
+    assert O.q4_row_gain(1e30) == 2.0 ** (141 - (127 + 99))
+    assert O.q4_row_gain(1e-38) == 2.0 ** 120  # exponent 0..: clamped
+    for peak in [3e-5, 0.7, 123.0, 6e4, 2.5e9]:
+        assert 2.0 ** 14 <= peak * O.q4_row_gain(peak) < 2.0 ** 15
