@@ -563,9 +563,8 @@ int grouped_matmul_launch(int mode, uint32_t fmt, const MatmulArgs &a, uint32_t 
 // fp32 result then takes the fused tiles' epilogue: + bf16-rounded bias,
 // then f32 or bf16 (weights.metal:24-33).
 
-// Grid: weight blocks first (one thread per 32-coefficient piece of a
-// 128-wide K step, consecutive threads along a row), then activation blocks
-// (eight values per thread).
+// Grid: weight blocks first (four (row, 2048-column chunk) tasks each, one
+// per wavefront), then activation blocks (eight values per thread).
 template <int FMT>
 __global__ __launch_bounds__(256) void operand_kernel(const uint8_t *w, uint64_t row_bytes, uint32_t n, uint32_t k,
                                                       uint16_t *wo, const uint16_t *x, uint16_t *xo, uint64_t xchunks,
@@ -582,20 +581,36 @@ __global__ __launch_bounds__(256) void operand_kernel(const uint8_t *w, uint64_t
         *reinterpret_cast<uint4 *>(xo + 8 * i) = make_uint4(h[0], h[1], h[2], h[3]);
         return;
     }
+    // Each wavefront: one row's 2048-column chunk.  Lane = piece (step
+    // lane / 4, piece lane % 4) decoded into the wavefront's LDS chunk, then
+    // the chunk leaves in 16-byte stores at consecutive addresses across the
+    // lanes (the pieces' own column runs are interleaved within a step).
     using PP = PrefillPiece<FMT, false>;
-    const uint32_t steps = (k + 127) / 128;
-    const uint64_t p = (uint64_t)blockIdx.x * 256 + threadIdx.x;
-    if (p >= (uint64_t)n * steps * 4) return;
-    const uint32_t row = (uint32_t)(p / (steps * 4)), rem = (uint32_t)(p % (steps * 4));
-    const uint32_t k0 = rem / 4 * 128, c = rem % 4;
-    if (k0 + 32 * c >= k) return;  // 32-block formats: the last step may be partial
-    const typename PP::Raw r = PP::load(gp(w) + (uint64_t)row * row_bytes, k0, c);
-    uint32_t out[16], col0[4];
-    PP::decode(r, k0, c, out, col0);
-    uint16_t *dst = wo + (uint64_t)row * k + k0;
+    __shared__ __attribute__((aligned(16))) uint16_t chunkbuf[4][2048];
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63, chunks = (k + 2047) / 2048;
+    const uint64_t task = (uint64_t)blockIdx.x * 4 + wave;
+    const bool live = task < (uint64_t)n * chunks;  // uniform per wavefront
+    const uint32_t row = live ? (uint32_t)(task / chunks) : 0, ch = live ? (uint32_t)(task % chunks) : 0;
+    const uint32_t k0 = ch * 2048 + lane / 4 * 128, c = lane % 4;
+    uint16_t *lb = chunkbuf[wave];
+    if (live && k0 + 32 * c < k) {  // 32-block formats: the last step may be partial
+        const typename PP::Raw r = PP::load(gp(w) + (uint64_t)row * row_bytes, k0, c);
+        uint32_t out[16], col0[4];
+        PP::decode(r, k0, c, out, col0);
 #pragma unroll
-    for (int q = 0; q < 4; q++)
-        *reinterpret_cast<uint4 *>(dst + col0[q]) = make_uint4(out[4 * q], out[4 * q + 1], out[4 * q + 2], out[4 * q + 3]);
+        for (int q = 0; q < 4; q++)
+            *reinterpret_cast<uint4 *>(lb + (k0 - ch * 2048) + col0[q]) =
+                make_uint4(out[4 * q], out[4 * q + 1], out[4 * q + 2], out[4 * q + 3]);
+    }
+    __syncthreads();
+    if (!live) return;
+    const uint32_t units = min(2048u, k - ch * 2048) / 8;
+    uint16_t *dst = wo + (uint64_t)row * k + ch * 2048;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t u = lane + 64 * i;
+        if (u < units) *reinterpret_cast<uint4 *>(dst + 8 * u) = *reinterpret_cast<const uint4 *>(lb + 8 * u);
+    }
 }
 
 // The scaled Q4_0 / Q4_1 tiles' activations (q4_input_scales and the
@@ -747,8 +762,8 @@ static VendorLayout vendor_layout(uint32_t format, oco_dtype x_dtype, uint32_t m
 template <int FMT>
 static void operand_launch(const void *w, uint64_t row_bytes, uint32_t n, uint32_t k, uint16_t *wo, const void *x,
                            uint16_t *xo, uint64_t xchunks, hipStream_t stream) {
-    const uint64_t pieces = (uint64_t)n * ((k + 127) / 128) * 4;
-    const uint32_t wblocks = FMT == OCO_F16 ? 0 : (uint32_t)((pieces + 255) / 256);
+    const uint64_t tasks = (uint64_t)n * ((k + 2047) / 2048);  // (row, 2048-column chunk), four per workgroup
+    const uint32_t wblocks = FMT == OCO_F16 ? 0 : (uint32_t)((tasks + 3) / 4);
     const uint32_t xblocks = (uint32_t)((xchunks + 255) / 256);
     hipLaunchKernelGGL(operand_kernel<FMT>, dim3(wblocks + xblocks), dim3(256), 0, stream, (const uint8_t *)w, row_bytes,
                        n, k, wo, (const uint16_t *)x, xo, xchunks, wblocks);
