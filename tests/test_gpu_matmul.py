@@ -449,6 +449,7 @@ def test_matmul_q4_row_gain(lib):
     xf = synth.activations(96, m * k).reshape(m, k).astype(np.float64)
     xf[::3] *= 2.0 ** 20
     xf[1::3] *= 2.0 ** -30
+    xf[5] = 0.0  # a zero row: gain 1
     x = synth.bf16_bits(xf.astype(np.float32)).reshape(m, k)
     got = run(lib, P.Q4_0, w, x, m, n, k)
     assert np.all(np.isfinite(got))
@@ -456,4 +457,7 @@ def test_matmul_q4_row_gain(lib):
     assert np.all(np.abs(got - half) <= O.roundoff_bound(half, mag, k, False))
     exact, _ = O.matmul_reference(P.Q4_0, w, x, n, k, half_operands=False)
     for r in range(m):  # each row within the bar of its own scale
+        if r == 5:
+            assert np.all(got[r] == 0.0)
+            continue
         assert rel_l2(got[r], exact[r]) <= 2e-3
