@@ -461,3 +461,20 @@ def test_matmul_q4_row_gain(lib):
             assert np.all(got[r] == 0.0)
             continue
         assert rel_l2(got[r], exact[r]) <= 2e-3
+
+
+@pytest.mark.parametrize("m", [31, 32, 33])
+@pytest.mark.parametrize("fmt", [P.Q4_K, P.Q8_0])
+def test_matmul_around_the_vendor_threshold(lib, fmt, m):
+    """Either side of the 32-row switch between the fused tiles and the
+    vendor GEMM: both within the half-operand bound, bias and bf16 output."""
+    from oco_amd import synth
+    n, k = 260, 512
+    w = synth.weights(fmt, n, k, seed=101)
+    x = synth.bf16_bits(synth.activations(102, m * k)).reshape(m, k)
+    bias = np.random.default_rng(103).normal(size=n).astype(np.float32)
+    got = run(lib, fmt, w, x, m, n, k, y_bf16=True, bias=bias)
+    half, mag = O.matmul_reference(fmt, w, x, n, k, half_operands=True)
+    b = O.bf16_round(bias)
+    want = half + b
+    assert np.all(np.abs(got - want) <= O.roundoff_bound(want, mag + np.abs(b), k, True))
