@@ -797,7 +797,8 @@ static int vendor_matmul(uint32_t format, const void *w, const void *x, oco_dtyp
         }
         OCO_TRY(launch_check("oco_matmul: operand pass"));
     }
-    const bool direct = y_dtype == OCO_DT_F32 && !(p->has_bias && bias) && !gain;
+    // f32 output without bias or gain is the GEMM's own output (when aligned for it)
+    const bool direct = y_dtype == OCO_DT_F32 && !(p->has_bias && bias) && !gain && ((uintptr_t)y & 15) == 0;
     float *acc = direct ? (float *)y : (float *)(ws + v.d);
     const float alpha = 1.0f, beta = 0.0f;
     const hipblasStatus_t st = hipblasLtMatmul(pl.handle, pl.desc, &alpha, wo ? (const void *)wo : w, pl.a,
