@@ -892,7 +892,7 @@ static uint32_t vector_rows(uint32_t format, uint32_t k, uint32_t n) {
     return 1;
 }
 static bool as_matvec(uint32_t format, oco_dtype x_dtype, const oco_matrix *p) {
-    return x_dtype == OCO_DT_BF16 && p->m <= vector_rows(format, p->k, p->n);
+    return x_dtype == OCO_DT_BF16 && p->m <= vector_rows(format, p->k, p->n) && p->m <= 65535;  // the matvec's row limit
 }
 
 // The vendor path needs n % 4 == 0 (the epilogue's four columns per thread).
