@@ -438,6 +438,23 @@ def test_matmul_vector_rows_take_the_matvec(lib, fmt, m, n, k):
     assert np.array_equal(y1.download(np.uint16, m * n), y2.download(np.uint16, m * n))
 
 
+def test_matmul_f32_small_n_past_the_matvec_row_limit(lib):
+    """F32 matrices of at most 128 outputs take the matvec at every m up to
+    its 65,535-row grid limit (no workspace); past it they take the
+    f16-operand product, which meets the half-operand bound."""
+    from oco_amd import synth
+    n, k = 64, 256
+    w = _dense_weights(0, n, k, 41)
+    assert lib.matmul_workspace(0, lib.Matrix(k, n, 65535, 0, 1, 1, 0)) == 0
+    m = 65600
+    say("matmul f32 past the matvec row limit", m, n, k)
+    assert lib.matmul_workspace(0, lib.Matrix(k, n, m, 0, 1, 1, 0)) > 0
+    x = synth.bf16_bits(synth.activations(42, m * k)).reshape(m, k)
+    got = _run_dense(lib, 0, w, x, m, n, k)
+    half, mag = O.matmul_reference(0, w, x, n, k, half_operands=True)
+    assert np.all(np.abs(got - half) <= O.roundoff_bound(half, mag, k, False))
+
+
 def test_matmul_q4_row_gain(lib):
     """Q4_0 with more than 1024 outputs: each activation row is scaled by the
     reference's power-of-two gain before the f16 rounding, so rows far
