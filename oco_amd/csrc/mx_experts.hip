@@ -425,25 +425,17 @@ static int mx_experts_go(const MatmulArgs &a, const uint8_t *xrec, hipStream_t s
     return OCO_OK;
 }
 
-constexpr uint32_t MXE_CUS = 256;
-
 template <int G>
 static int mx_experts_go_tr(const MatmulArgs &a, const uint8_t *xrec, uint32_t tile_rows, hipStream_t stream) {
     if (tile_rows == 32) return mx_experts_go<G, 32, 1>(a, xrec, stream);
     if constexpr (G == MM_DOWN) {
-        // Few tiles (small decode batches): split each tile's K over two
-        // halves of the workgroup when twice the grid still fits one round
-        // of resident workgroups (three per CU), halving the serial quads.
-        // The threshold is a constant (MI355X: 256 CUs), not the device's
-        // count, so the kernel and its summation order are a function of the
-        // shape alone.
-        const uint32_t tiles = std::min(a.routes, (a.routes + 15) / 16 + a.experts);
-        const uint32_t wgs = (a.n + 32 * MXE_NW - 1) / (32 * MXE_NW) * tiles;
+        // The down tiles can split each tile's K over two halves of the
+        // workgroup (OCO_KNOB_MX_EXPERTS_KS 2).  With the four-term
+        // activations it no longer pays at any decode batch (gpt-oss, same
+        // box: B = 4 72.0 -> 70.2 us without it, B = 6/8/12 81.5/97.3/113.7
+        // against 85.7/102.3/119.2 with it), so it runs only when forced.
         int32_t ov[4];
-        // Under four quads the second part would hold little or no real work.
-        const uint32_t quads = ((a.k + 63) / 64 + 3) / 4;
-        const int ks = plan_override(OCO_KNOB_MX_EXPERTS_KS, ov) ? ov[0] : 2 * wgs <= 3 * MXE_CUS && quads >= 4 ? 2 : 1;
-        if (ks == 2) return mx_experts_go<G, 16, 2>(a, xrec, stream);
+        if (plan_override(OCO_KNOB_MX_EXPERTS_KS, ov) && ov[0] == 2) return mx_experts_go<G, 16, 2>(a, xrec, stream);
     }
     return mx_experts_go<G, 16, 1>(a, xrec, stream);
 }
