@@ -102,6 +102,25 @@ def test_matmul_prefill_shapes(lib, fmt, n, k):
         assert np.all(np.abs(got - exact) <= O.roundoff_bound(exact, mag, k, False) + mx_split_bound(x, w, n, k))
 
 
+@pytest.mark.parametrize("fmt,n,k", [(12, 12288, 4096), (14, 4096, 12288), (8, 4096, 4096)])
+def test_matmul_dense_prefill_bench_shapes(lib, fmt, n, k):
+    """The dense prefill bench configurations as the bench runs them (its
+    weight and activation seeds, 512 bf16 tokens, bf16 output, the vendor
+    path): every 32nd row against the fp64 oracle, within 2e-3 and the
+    per-element half-operand bound with the output rounding."""
+    from oco_amd import synth
+    m = 512
+    say("matmul dense prefill bench shape", fmt, n, k)
+    w = synth.weights(fmt, n, k, 7)
+    x = synth.bf16_bits(synth.activations(8, m * k)).reshape(m, k)
+    assert lib.matmul_workspace(fmt, lib.Matrix(k, n, m, 0, 1, 1, 0)) > 0  # the vendor path
+    got = _run_dense(lib, fmt, w, x, m, n, k, y_bf16=True)[::32]
+    exact, _ = O.matmul_reference(fmt, w, x[::32], n, k, half_operands=False)
+    half, mag = O.matmul_reference(fmt, w, x[::32], n, k, half_operands=True)
+    assert rel_l2(got, exact) <= 2e-3
+    assert np.all(np.abs(got - half) <= O.roundoff_bound(half, mag, k, True))
+
+
 def test_matmul_bias_and_bf16_output(lib):
     from oco_amd import synth
     m, n, k = 70, 100, 256
