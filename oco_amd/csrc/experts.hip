@@ -125,19 +125,11 @@ __global__ __launch_bounds__(256) void moe_kernel(KPRE_PARAMS, MoeArgs a) {
     const uint32_t expert = tile_meta[0], count = tile_meta[1];
     if (count == 0) return;  // uniform across the workgroup
 
-    // Buffer resources over this expert's rows of each matrix (16-byte aligned
-    // base; range rounded up to the next 16 bytes, see the decode matvec).
-    __amdgpu_buffer_rsrc_t rs[NM];
+    // This expert's rows of each matrix: offsets from the 16-byte boundary
+    // at or below their start.
     uint32_t shift[NM];
 #pragma unroll
-    for (int m = 0; m < NM; m++) {
-        const uint8_t *eb = a.w[m] + (uint64_t)expert * a.n * a.row_bytes;
-        const uintptr_t al = (uintptr_t)eb & ~(uintptr_t)15;
-        shift[m] = (uint32_t)((uintptr_t)eb & 15);
-        const uint64_t span = ((uint64_t)a.n * a.row_bytes + shift[m] + 15) & ~15ull;
-        rs[m] = __builtin_amdgcn_make_buffer_rsrc((void *)al, 0, (uint32_t)std::min<uint64_t>(span, 0xffffffffull),
-                                                  0x00020000);
-    }
+    for (int m = 0; m < NM; m++) shift[m] = (uint32_t)((uintptr_t)(a.w[m] + (uint64_t)expert * a.n * a.row_bytes) & 15);
     const uint32_t row_span = (uint32_t)a.row_bytes, pieces = PT;
     u32x4 regs[TROWS * LPR];
     // Tile row i: matrix i / 2, row (group rows) wave*2 + i % 2.
@@ -145,17 +137,25 @@ __global__ __launch_bounds__(256) void moe_kernel(KPRE_PARAMS, MoeArgs a) {
         const uint32_t row = g * 8 + wave * 2 + (i & 1);
         return (uint32_t)(shift[i >> 1] + (uint64_t)row * a.row_bytes);
     };
+    // One buffer resource per tile row, from the 16-byte boundary at or
+    // below the row to its end rounded up to a whole chunk: the loads need no
+    // per-lane test (a branch around them would make the compiler wait for
+    // every load before the join), since chunks past the range read as zero
+    // without touching memory.  Rows past n get an empty range.
+    const uint8_t *mb[NM];
+#pragma unroll
+    for (int m = 0; m < NM; m++) mb[m] = a.w[m] + (uint64_t)expert * a.n * a.row_bytes;
     auto issue = [&](uint32_t g) {
 #pragma unroll
         for (int i = 0; i < TROWS; i++) {
-            const uint32_t off = row_offset(g, i), start = off & ~15u, need = (off & 15u) + row_span;
+            const uint32_t off = row_offset(g, i), start = off & ~15u;
+            const uint32_t row = g * 8 + wave * 2 + (i & 1);
+            const uint32_t need = row < a.n ? (off & 15u) + row_span : 0u;
+            const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
+                (void *)(((uintptr_t)mb[i >> 1] & ~(uintptr_t)15) + start), 0, (need + 15u) & ~15u, 0x00020000);
 #pragma unroll
-            for (int u = 0; u < LPR; u++) {
-                const uint32_t j = (uint32_t)(u * 64 + lane);
-                regs[i * LPR + u] = 16 * j < need
-                                        ? __builtin_amdgcn_raw_buffer_load_b128(rs[i >> 1], start + 16 * j, 0, 2)
-                                        : u32x4{0, 0, 0, 0};
-            }
+            for (int u = 0; u < LPR; u++)
+                regs[i * LPR + u] = __builtin_amdgcn_raw_buffer_load_b128(rr, 16 * (u * 64 + lane), 0, 2);
         }
     };
     uint32_t g = blockIdx.x;
@@ -167,10 +167,11 @@ __global__ __launch_bounds__(256) void moe_kernel(KPRE_PARAMS, MoeArgs a) {
         for (uint32_t f = threadIdx.x; f < K / 4; f += 256) {
             float v[4];
             if (!a.x_bf16) {
-                float4 t = reinterpret_cast<const float4 *>(a.x)[(uint64_t)in * (K / 4) + f];
-                v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+                const uint4 t = ld_u128((gbytes)a.x + ((uint64_t)in * (K / 4) + f) * 16);
+                v[0] = __uint_as_float(t.x); v[1] = __uint_as_float(t.y);
+                v[2] = __uint_as_float(t.z); v[3] = __uint_as_float(t.w);
             } else {
-                uint2 t = reinterpret_cast<const uint2 *>(a.x)[(uint64_t)in * (K / 4) + f];
+                const uint2 t = ld_u64((gbytes)a.x + ((uint64_t)in * (K / 4) + f) * 8);
                 v[0] = __uint_as_float(t.x << 16); v[1] = __uint_as_float(t.x & 0xffff0000u);
                 v[2] = __uint_as_float(t.y << 16); v[3] = __uint_as_float(t.y & 0xffff0000u);
             }
