@@ -158,13 +158,49 @@ __global__ __launch_bounds__(256) void moe_kernel(KPRE_PARAMS, MoeArgs a) {
                 regs[i * LPR + u] = __builtin_amdgcn_raw_buffer_load_b128(rr, 16 * (u * 64 + lane), 0, 2);
         }
     };
+    // One-route tiles request four float4 of x per thread (the first 1024)
+    // before the weights: loads return in issue order, so x is in registers
+    // while the weights are still in flight, as in the decode matvec.  (Plan
+    // tiles, whose accumulators already take the registers, do not.)
+    float xpre[4][4];
+    if constexpr (T == 1) {
+        const uint32_t in = tile_routes[0] / a.input_div;
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const uint32_t f = threadIdx.x + 256u * u;
+            if (f < K / 4) {
+                if (!a.x_bf16) {
+                    const uint4 t = ld_u128((gbytes)a.x + ((uint64_t)in * (K / 4) + f) * 16);
+                    xpre[u][0] = __uint_as_float(t.x); xpre[u][1] = __uint_as_float(t.y);
+                    xpre[u][2] = __uint_as_float(t.z); xpre[u][3] = __uint_as_float(t.w);
+                } else {
+                    const uint2 t = ld_u64((gbytes)a.x + ((uint64_t)in * (K / 4) + f) * 8);
+                    xpre[u][0] = __uint_as_float(t.x << 16); xpre[u][1] = __uint_as_float(t.x & 0xffff0000u);
+                    xpre[u][2] = __uint_as_float(t.y << 16); xpre[u][3] = __uint_as_float(t.y & 0xffff0000u);
+                }
+            }
+        }
+    }
     uint32_t g = blockIdx.x;
     if (g < a.ngroups) issue(g);
 
     // Stage each route's activation row (piece-major) and its piece sums.
     for (uint32_t j = 0; j < count; j++) {
         const uint32_t in = tile_routes[j] / a.input_div;
-        for (uint32_t f = threadIdx.x; f < K / 4; f += 256) {
+        uint32_t f0 = threadIdx.x;
+        if constexpr (T == 1) {  // one route: its first 1024 float4 are in xpre
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const uint32_t f = threadIdx.x + 256u * u;
+                if (f < K / 4) {
+                    uint32_t pp, tt;
+                    Tl::map(f, pp, tt);
+                    xs4[tt * PT + pp] = make_float4(xpre[u][0], xpre[u][1], xpre[u][2], xpre[u][3]);
+                }
+            }
+            f0 = threadIdx.x + 1024;
+        }
+        for (uint32_t f = f0; f < K / 4; f += 256) {
             float v[4];
             if (!a.x_bf16) {
                 const uint4 t = ld_u128((gbytes)a.x + ((uint64_t)in * (K / 4) + f) * 16);
